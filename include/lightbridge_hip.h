@@ -1,0 +1,169 @@
+/*
+ * lightbridge_hip.h — C ABI of the MI355X (gfx950) backend for LightBridge's
+ * quantized-dot hot path: Q8_K activation quantization, the
+ * {IQ2_S, IQ3_S, Q4_K, Q5_K} x Q8_K integer-dot matvecs and the SwiGLU MoE
+ * expert FFN built from them.
+ *
+ * Plain C types only.  Every buffer argument named *_dev is a device pointer
+ * (hipMalloc / torch CUDA memory) on the context's device; work is ordered on
+ * the context's stream.  Functions return an lbh_status; on error they fill
+ * *err (if non-NULL) and leave every output buffer unchanged (the reference's
+ * atomicity rule, crates/bridge-quant-layout/src/q8_k.rs:16-33,
+ * crates/bridge-kernels-reference/src/gemv.rs:245-272).
+ *
+ * Functions marked [sync] wait for their stream to report an error the
+ * reference reports synchronously.  Functions marked [async] only enqueue.
+ *
+ * Status codes map 1:1 onto QuantError (crates/bridge-quant-layout/src/error.rs:6-65)
+ * and KernelError (crates/bridge-kernels-reference/src/error.rs:7-59).
+ */
+#ifndef LIGHTBRIDGE_HIP_H
+#define LIGHTBRIDGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML type ids (crates/bridge-core/src/ggml_type.rs:10-30). */
+enum lbh_ggml_type {
+    LBH_F32 = 0,
+    LBH_Q4_K = 12,
+    LBH_Q5_K = 13,
+    LBH_Q8_K = 15,
+    LBH_IQ3_S = 21,
+    LBH_IQ2_S = 22,
+};
+
+typedef enum lbh_status {
+    LBH_OK = 0,
+    /* QuantError */
+    LBH_UNSUPPORTED_TYPE = 1,
+    LBH_ZERO_LOGICAL_ELEMENTS = 2,
+    LBH_LOGICAL_ELEMENTS_NOT_DIVISIBLE = 3,
+    LBH_ARITHMETIC_OVERFLOW = 4,
+    LBH_ENCODED_LENGTH_MISMATCH = 6,
+    LBH_OUTPUT_LENGTH_MISMATCH = 7,
+    LBH_NON_FINITE_SCALE = 8,
+    LBH_NON_FINITE_ACTIVATION = 9,
+    LBH_NON_FINITE_Q8_SCALE = 10,
+    /* KernelError */
+    LBH_DIMENSION_MISMATCH = 20,
+    LBH_SCRATCH_TOO_SMALL = 21,
+    LBH_NON_FINITE_VALUE = 22,
+    LBH_ROUTED_EXPERT_ORDER = 23,
+    LBH_DUPLICATE_ROUTED_EXPERT = 24,
+    LBH_INVALID_PARAMETER = 25,
+    /* backend */
+    LBH_HIP_ERROR = 100,
+    LBH_NULL_ARGUMENT = 101,
+    LBH_UNSUPPORTED_SHAPE = 102,
+} lbh_status;
+
+/* Error payload: the fields of the corresponding QuantError/KernelError variant. */
+typedef struct lbh_error {
+    int32_t status;
+    int32_t ty;        /* GGML type the error refers to */
+    uint64_t index;    /* block_index (NonFiniteScale), lane (NonFiniteActivation/Value), expert id */
+    uint64_t expected;
+    uint64_t actual;
+    uint32_t bits;     /* offending binary16 / binary32 bits */
+    uint32_t field;    /* NonFiniteScale: 0 = d, 1 = dmin */
+    uint64_t row;      /* matrix row for weight errors */
+    int32_t hip_error; /* hipError_t for LBH_HIP_ERROR */
+    int32_t reserved;
+} lbh_error;
+
+typedef struct lbh_ctx lbh_ctx;
+typedef struct lbh_matrix lbh_matrix;
+
+/* Q8_K ABI constants (crates/bridge-quant-layout/src/q8_k.rs:7-12). */
+#define LBH_Q8_K_BLOCK_ELEMENTS 256
+#define LBH_Q8_K_BLOCK_BYTES 292
+
+/* ---- backend / dispatch surface -------------------------------------------
+ * Counterpart of CpuBackend / CpuCapabilities (crates/bridge-kernels-cpu/src/lib.rs:19-126):
+ * the hip backend joins cpu_parallel_avx2_q8_k / cpu_parallel_scalar_q8_k. */
+
+/* Backend name reported beside CpuCapabilities::backend_name (lib.rs:50-56): "hip_gfx950_q8_k". */
+const char *lbh_backend_name(void);
+
+/* Number of visible HIP devices whose ISA is gfx950 (0 when none: the caller keeps the CPU backend). */
+int32_t lbh_device_count(void);
+
+/* CpuBackend::new (lib.rs:76-90): opens `device`; `stream` is a hipStream_t or NULL (null stream). */
+lbh_status lbh_ctx_create(int32_t device, void *stream, lbh_ctx **out, lbh_error *err);
+lbh_status lbh_ctx_destroy(lbh_ctx *ctx);
+lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream);
+/* Waits for the context's stream. */
+lbh_status lbh_ctx_synchronize(lbh_ctx *ctx, lbh_error *err);
+
+/* ---- Q8_K quantization ------------------------------------------------------ */
+
+/* [sync] quantize_row_q8_k_into (crates/bridge-quant-layout/src/q8_k.rs:16-76):
+ * n f32 (n % 256 == 0) -> (n/256) * 292 bytes, bit-identical to the reference. */
+lbh_status lbh_quantize_row_q8_k_into(lbh_ctx *ctx, const float *input_dev, size_t n,
+                                      uint8_t *encoded_dev, size_t encoded_len, lbh_error *err);
+
+/* [async] Unchecked form for the hot path: `rows` independent vectors of n floats
+ * (row stride n) -> rows * (n/256) * 292 bytes.  Non-finite input is not
+ * reported (call the checked form to validate). */
+lbh_status lbh_quantize_q8_k_rows(lbh_ctx *ctx, const float *input_dev, size_t rows, size_t n,
+                                  uint8_t *encoded_dev);
+
+/* ---- packed matrices ---------------------------------------------------------
+ * PackedMatrix (crates/bridge-kernels-reference/src/matrix.rs:102-186): GGML
+ * [input_width = k, output_width = rows] row-major block bytes.  Upload checks
+ * the exact byte length and the finiteness of every block's f16 d (and dmin),
+ * the checks validate_vec_dot_q8_k repeats per call (q8_k.rs:121-161,
+ * k_quants.rs:178-208), and stores the bytes in HBM in the backend's lossless
+ * device layout. */
+
+/* [sync] `bytes` is host memory when bytes_on_device == 0, device memory otherwise. */
+lbh_status lbh_matrix_create(lbh_ctx *ctx, int32_t ggml_type, size_t rows, size_t k, const void *bytes,
+                             size_t byte_len, int32_t bytes_on_device, lbh_matrix **out, lbh_error *err);
+lbh_status lbh_matrix_destroy(lbh_matrix *m);
+/* [sync] Inverse of the device layout: writes the original GGML bytes to host memory. */
+lbh_status lbh_matrix_read_ggml(lbh_ctx *ctx, const lbh_matrix *m, void *host_bytes, size_t byte_len,
+                                lbh_error *err);
+size_t lbh_matrix_rows(const lbh_matrix *m);
+size_t lbh_matrix_k(const lbh_matrix *m);
+int32_t lbh_matrix_type(const lbh_matrix *m);
+size_t lbh_matrix_bytes(const lbh_matrix *m);
+
+/* ---- matvec ------------------------------------------------------------------ */
+
+/* [sync] gemv_into(CpuParallelQ8K) (crates/bridge-kernels-reference/src/gemv.rs:56-70, :88-115):
+ * output[r] = vec_dot_q8_k(row r, Q8_K(input)).  q8_scratch_dev holds >= (k/256)*292 bytes. */
+lbh_status lbh_gemv_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input_dev, size_t input_len,
+                         float *output_dev, size_t output_len, uint8_t *q8_scratch_dev, size_t q8_len,
+                         lbh_error *err);
+
+/* [sync] gemv_accumulate_scaled_into (gemv.rs:117-174): destination[r] += scale * dot(row r). */
+lbh_status lbh_gemv_accumulate_scaled_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input_dev,
+                                           size_t input_len, float *destination_dev, size_t dest_len,
+                                           float scale, uint8_t *q8_scratch_dev, size_t q8_len,
+                                           lbh_error *err);
+
+/* [async] The matvec over an already-quantized Q8_K vector (the benchmark unit):
+ * accumulate == 0: y[r] = dot(row r, q8);  accumulate != 0: y[r] += coef * dot(row r, q8). */
+lbh_status lbh_gemv_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, float *y_dev,
+                         float coef, int32_t accumulate);
+
+/* [async] Integer stage for bit-exact verification: per (row, block) the IQ2_S/IQ3_S
+ * block_sum (one int32) or the Q4_K/Q5_K lane_sums[8] + minimum_sum (nine int32)
+ * of q8_k.rs:295-312, :337-364, :380-428.  out_dev holds rows * (k/256) * {1|9} int32. */
+lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, int32_t *out_dev);
+
+/* ---- diagnostics ------------------------------------------------------------- */
+
+/* [sync] Converts n binary16 values with the device conversion the kernels use. */
+lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in_dev, float *out_dev, size_t n,
+                                lbh_error *err);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

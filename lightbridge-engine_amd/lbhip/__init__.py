@@ -1,0 +1,240 @@
+"""Python mirror of the reference's quantized-dot API over the HIP C ABI.
+
+The names, argument meanings and error variants follow the reference crates:
+``quantize_row_q8_k_into`` (crates/bridge-quant-layout/src/q8_k.rs:16),
+``gemv_into`` / ``gemv_accumulate_scaled_into``
+(crates/bridge-kernels-reference/src/gemv.rs:88, :117), and the backend object
+mirrors ``CpuBackend`` (crates/bridge-kernels-cpu/src/lib.rs:59-119).  Device
+buffers are torch CUDA tensors (PyTorch is only the allocator and stream
+provider); every call goes through liblightbridge_hip.so.  There is no CPU
+fallback: if the library or a gfx950 device is missing, construction raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+PKG_DIR = Path(__file__).resolve().parent.parent
+LIB_PATH = PKG_DIR / "liblightbridge_hip.so"
+
+F32, Q4_K, Q5_K, Q8_K, IQ3_S, IQ2_S = 0, 12, 13, 15, 21, 22
+Q8_K_BLOCK_ELEMENTS, Q8_K_BLOCK_BYTES = 256, 292
+BLOCK_BYTES = {Q4_K: 144, Q5_K: 176, IQ2_S: 82, IQ3_S: 110}
+
+STATUS = {
+    0: "Ok", 1: "UnsupportedType", 2: "ZeroLogicalElements", 3: "LogicalElementsNotDivisible",
+    4: "ArithmeticOverflow", 6: "EncodedLengthMismatch", 7: "OutputLengthMismatch",
+    8: "NonFiniteScale", 9: "NonFiniteActivation", 10: "NonFiniteQ8Scale",
+    20: "DimensionMismatch", 21: "ScratchTooSmall", 22: "NonFiniteValue",
+    23: "RoutedExpertOrder", 24: "DuplicateRoutedExpert", 25: "InvalidParameter",
+    100: "HipError", 101: "NullArgument", 102: "UnsupportedShape",
+}
+QUANT_ERRORS = {1, 2, 3, 4, 6, 7, 8, 9, 10}
+
+
+class LbhError(C.Structure):
+    _fields_ = [("status", C.c_int32), ("ty", C.c_int32), ("index", C.c_uint64), ("expected", C.c_uint64),
+                ("actual", C.c_uint64), ("bits", C.c_uint32), ("field", C.c_uint32), ("row", C.c_uint64),
+                ("hip_error", C.c_int32), ("reserved", C.c_int32)]
+
+
+class BackendError(Exception):
+    """Base of the mirrored error enums; ``variant`` is the reference variant name."""
+
+    def __init__(self, err: LbhError):
+        self.code = err.status
+        self.variant = STATUS.get(err.status, str(err.status))
+        self.ty, self.index, self.expected, self.actual = err.ty, err.index, err.expected, err.actual
+        self.bits, self.field, self.row, self.hip_error = err.bits, err.field, err.row, err.hip_error
+        super().__init__(f"{self.variant}(ty={self.ty}, index={self.index}, expected={self.expected}, "
+                         f"actual={self.actual}, bits={self.bits:#x}, field={self.field}, row={self.row}, "
+                         f"hip={self.hip_error})")
+
+
+class QuantError(BackendError):
+    """crates/bridge-quant-layout/src/error.rs:6-65."""
+
+
+class KernelError(BackendError):
+    """crates/bridge-kernels-reference/src/error.rs:7-59."""
+
+
+def _raise(err: LbhError) -> None:
+    raise (QuantError if err.status in QUANT_ERRORS else KernelError)(err)
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"HIP backend library missing: {LIB_PATH} (build with __graft_entry__.build())")
+        L = C.CDLL(str(LIB_PATH))
+        p, sz, i32, u32 = C.c_void_p, C.c_size_t, C.c_int32, C.c_uint32
+        E = C.POINTER(LbhError)
+        sig = {
+            "lbh_backend_name": ([], C.c_char_p),
+            "lbh_device_count": ([], i32),
+            "lbh_ctx_create": ([i32, p, C.POINTER(p), E], i32),
+            "lbh_ctx_destroy": ([p], i32),
+            "lbh_ctx_set_stream": ([p, p], i32),
+            "lbh_ctx_synchronize": ([p, E], i32),
+            "lbh_quantize_row_q8_k_into": ([p, p, sz, p, sz, E], i32),
+            "lbh_quantize_q8_k_rows": ([p, p, sz, sz, p], i32),
+            "lbh_matrix_create": ([p, i32, sz, sz, p, sz, i32, C.POINTER(p), E], i32),
+            "lbh_matrix_destroy": ([p], i32),
+            "lbh_matrix_read_ggml": ([p, p, p, sz, E], i32),
+            "lbh_matrix_rows": ([p], sz),
+            "lbh_matrix_k": ([p], sz),
+            "lbh_matrix_type": ([p], i32),
+            "lbh_matrix_bytes": ([p], sz),
+            "lbh_gemv_into": ([p, p, p, sz, p, sz, p, sz, E], i32),
+            "lbh_gemv_accumulate_scaled_into": ([p, p, p, sz, p, sz, C.c_float, p, sz, E], i32),
+            "lbh_gemv_q8_k": ([p, p, p, p, C.c_float, i32], i32),
+            "lbh_gemv_block_sums": ([p, p, p, p], i32),
+            "lbh_debug_f16_to_f32": ([p, p, p, sz, E], i32),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes, fn.restype = args, res
+        _lib = L
+    return _lib
+
+
+def _dev_ptr(t) -> int:
+    import torch
+    assert isinstance(t, torch.Tensor) and t.is_cuda and t.is_contiguous(), "expected a contiguous CUDA tensor"
+    return t.data_ptr()
+
+
+def _call(fn, *args) -> None:
+    err = LbhError()
+    st = fn(*args, C.byref(err))
+    if st != 0:
+        if err.status == 0:
+            err.status = st
+        _raise(err)
+
+
+def backend_name() -> str:
+    return lib().lbh_backend_name().decode()
+
+
+class HipBackend:
+    """Counterpart of CpuBackend (crates/bridge-kernels-cpu/src/lib.rs:59-119) for gfx950.
+
+    ``execution_mode`` is the extra ReferenceExecutionMode this backend adds
+    beside DequantF32 / LlamaQ8K / CpuParallelQ8K (gemv.rs:12-16)."""
+
+    execution_mode = "HipQ8K"
+
+    def __init__(self, device: int = 0, stream=None):
+        import torch
+        if not torch.cuda.is_available():
+            raise RuntimeError("HipBackend needs a ROCm GPU")
+        self.device = device
+        torch.cuda.set_device(device)
+        self._stream = stream if stream is not None else torch.cuda.current_stream(device)
+        h = C.c_void_p()
+        _call(lib().lbh_ctx_create, device, C.c_void_p(self._stream.cuda_stream), C.byref(h))
+        self.ctx = h
+
+    def backend_name(self) -> str:
+        return backend_name()
+
+    def set_stream(self, stream) -> None:
+        """Order subsequent work on `stream` (a torch.cuda.Stream), e.g. for graph capture."""
+        self._stream = stream
+        lib().lbh_ctx_set_stream(self.ctx, C.c_void_p(stream.cuda_stream))
+
+    def simd_active(self) -> bool:
+        return True
+
+    def synchronize(self) -> None:
+        _call(lib().lbh_ctx_synchronize, self.ctx)
+
+    def close(self) -> None:
+        if self.ctx:
+            lib().lbh_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- matrices -----------------------------------------------------------------
+    def upload(self, ty: int, rows: int, k: int, data) -> "DeviceMatrix":
+        return DeviceMatrix(self, ty, rows, k, data)
+
+    # -- Q8_K ---------------------------------------------------------------------
+    def quantize_row_q8_k_into(self, x, encoded) -> None:
+        _call(lib().lbh_quantize_row_q8_k_into, self.ctx, _dev_ptr(x), x.numel(), _dev_ptr(encoded), encoded.numel())
+
+    def quantize_q8_k_rows(self, x, encoded, rows: int, n: int) -> None:
+        st = lib().lbh_quantize_q8_k_rows(self.ctx, _dev_ptr(x), rows, n, _dev_ptr(encoded))
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    # -- matvec ---------------------------------------------------------------------
+    def gemv_into(self, m: "DeviceMatrix", x, y, q8_scratch) -> None:
+        _call(lib().lbh_gemv_into, self.ctx, m.handle, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel(),
+              _dev_ptr(q8_scratch), q8_scratch.numel())
+
+    def gemv_accumulate_scaled_into(self, m: "DeviceMatrix", x, dest, scale: float, q8_scratch) -> None:
+        _call(lib().lbh_gemv_accumulate_scaled_into, self.ctx, m.handle, _dev_ptr(x), x.numel(), _dev_ptr(dest),
+              dest.numel(), scale, _dev_ptr(q8_scratch), q8_scratch.numel())
+
+    def gemv_q8_k(self, m: "DeviceMatrix", q8, y, coef: float = 0.0, accumulate: bool = False) -> None:
+        st = lib().lbh_gemv_q8_k(self.ctx, m.handle, _dev_ptr(q8), _dev_ptr(y), coef, 1 if accumulate else 0)
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def block_sums(self, m: "DeviceMatrix", q8, out) -> None:
+        st = lib().lbh_gemv_block_sums(self.ctx, m.handle, _dev_ptr(q8), _dev_ptr(out))
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def f16_to_f32(self, src, dst) -> None:
+        _call(lib().lbh_debug_f16_to_f32, self.ctx, _dev_ptr(src), _dev_ptr(dst), src.numel())
+
+
+class DeviceMatrix:
+    """A PackedMatrix (crates/bridge-kernels-reference/src/matrix.rs:102-186) resident in HBM."""
+
+    def __init__(self, be: HipBackend, ty: int, rows: int, k: int, data):
+        import torch
+        self.be, self.ty, self.rows, self.k = be, ty, rows, k
+        h = C.c_void_p()
+        if isinstance(data, torch.Tensor):
+            assert data.is_cuda and data.dtype == torch.uint8
+            data = data.contiguous()
+            _call(lib().lbh_matrix_create, be.ctx, ty, rows, k, C.c_void_p(data.data_ptr()), data.numel(), 1,
+                  C.byref(h))
+        else:
+            arr = np.ascontiguousarray(data, dtype=np.uint8)
+            _call(lib().lbh_matrix_create, be.ctx, ty, rows, k, C.c_void_p(arr.ctypes.data), arr.size, 0,
+                  C.byref(h))
+        self.handle = h
+        self.nbytes = lib().lbh_matrix_bytes(h)
+
+    def read_ggml(self) -> np.ndarray:
+        out = np.zeros(self.nbytes, np.uint8)
+        _call(lib().lbh_matrix_read_ggml, self.be.ctx, self.handle, C.c_void_p(out.ctypes.data), out.size)
+        return out
+
+    def close(self) -> None:
+        if self.handle:
+            lib().lbh_matrix_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
