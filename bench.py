@@ -45,6 +45,7 @@ def parse():
     ap.add_argument("--copies", type=int, default=0, help="weight copies in rotation (0 = enough for 512 MB)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--lpu", type=int, default=0, help="lanes per (row, block) unit (0 = library default)")
     return ap.parse_args()
 
 
@@ -88,6 +89,7 @@ def main():
     from lbhip import synth
 
     be = lbhip.HipBackend(0)
+    be.set_tuning(be.TUNE_GEMV_LPU, args.lpu)
     w_gate = synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, seed=101)
     w_down = synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, seed=102)
     copies = args.copies or max(2, math.ceil(512e6 / (w_gate.nbytes + w_down.nbytes)) + 4)
@@ -106,10 +108,8 @@ def main():
 
     def step(i):
         c = i % copies
-        be.quantize_q8_k_rows(xs[c], q8x[c], 1, HIDDEN)
-        be.gemv_q8_k(gates[c], q8x[c], hs[c])
-        be.quantize_q8_k_rows(hs[c], q8h[c], 1, FFN)
-        be.gemv_q8_k(downs[c], q8h[c], ys[c])
+        be.gemv_f32(gates[c], xs[c], hs[c], q8x[c])      # Q8_K(x) + IQ2_S gate, one launch
+        be.gemv_f32(downs[c], hs[c], ys[c], q8h[c])      # Q8_K(h) + IQ3_S down, one launch
 
     # Capture one rotation (copies steps) per graph; replay it.
     per_graph = copies
@@ -128,11 +128,11 @@ def main():
         g_down = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g_down, stream=stream):
             for i in range(per_graph):
-                be.gemv_q8_k(downs[i], q8h[i], ys[i])
+                be.gemv_f32(downs[i], hs[i], ys[i])
         g_gate = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g_gate, stream=stream):
             for i in range(per_graph):
-                be.gemv_q8_k(gates[i], q8x[i], hs[i])
+                be.gemv_f32(gates[i], xs[i], hs[i])
 
         reps_w = max(1, args.warmup // per_graph)
         reps = max(1, math.ceil(args.steps / per_graph))
@@ -190,9 +190,9 @@ def main():
         "config": {"workload": "configs[1]: IQ2_S gate 1536x4096 + IQ3_S down 4096x1536, batch 1 (1 token)",
                    "weight_copies_in_rotation": copies,
                    "rotation_bytes": copies * (w_gate.nbytes + w_down.nbytes),
-                   "step": "quantize x -> IQ2_S gate -> quantize h -> IQ3_S down (4 kernels, HIP graph)",
+                   "step": "Q8_K(x)+IQ2_S gate -> Q8_K(h)+IQ3_S down (2 fused kernels, HIP graph)", "lpu": args.lpu,
                    "algorithmic_bytes_per_step": STEP_BYTES},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<IQ3_S> (down 4096x1536)",
+        "roofline": {"bound": "hbm", "kernel": "k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)",
                      "achieved": round(down_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "avg_launch_us": round(down_us, 3), "algorithmic_bytes_per_launch": DOWN_BYTES},

@@ -78,6 +78,7 @@ typedef struct lbh_error {
 
 typedef struct lbh_ctx lbh_ctx;
 typedef struct lbh_matrix lbh_matrix;
+typedef struct lbh_moe lbh_moe;
 
 /* Q8_K ABI constants (crates/bridge-quant-layout/src/q8_k.rs:7-12). */
 #define LBH_Q8_K_BLOCK_ELEMENTS 256
@@ -97,6 +98,15 @@ int32_t lbh_device_count(void);
 lbh_status lbh_ctx_create(int32_t device, void *stream, lbh_ctx **out, lbh_error *err);
 lbh_status lbh_ctx_destroy(lbh_ctx *ctx);
 lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream);
+/* Launch-shape knobs (no reference counterpart: the CPU backend's only knob is
+ * its thread count, CpuBackendConfig, lib.rs:7-17).  value 0 restores the default. */
+enum lbh_tuning_key {
+    LBH_TUNE_GEMV_LPU = 1,         /* lanes per (row, block) unit: 1, 2 or 4 */
+    LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop */
+};
+lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value);
+/* Compute units of the context's device. */
+int32_t lbh_ctx_cu_count(const lbh_ctx *ctx);
 /* Waits for the context's stream. */
 lbh_status lbh_ctx_synchronize(lbh_ctx *ctx, lbh_error *err);
 
@@ -152,12 +162,62 @@ lbh_status lbh_gemv_accumulate_scaled_into(lbh_ctx *ctx, const lbh_matrix *m, co
 lbh_status lbh_gemv_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, float *y_dev,
                          float coef, int32_t accumulate);
 
+/* [async] Fused form of gemv_into / gemv_accumulate_scaled_into without the
+ * finiteness checks: the kernel quantizes x (k floats) to Q8_K itself (bytes
+ * identical to lbh_quantize_row_q8_k_into; written to q8_out when non-NULL)
+ * and computes the matvec in the same launch. */
+lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x_dev, uint8_t *q8_out_dev, float *y_dev,
+                        float coef, int32_t accumulate);
+
 /* [async] Integer stage for bit-exact verification: per (row, block) the IQ2_S/IQ3_S
  * block_sum (one int32) or the Q4_K/Q5_K lane_sums[8] + minimum_sum (nine int32)
  * of q8_k.rs:295-312, :337-364, :380-428.  out_dev holds rows * (k/256) * {1|9} int32. */
 lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, int32_t *out_dev);
 
+/* ---- SwiGLU mixture-of-experts block ---------------------------------------------
+ * A resident MoE layer: routed experts (SwiGluExpert, crates/bridge-kernels-reference/
+ * src/activation.rs:6-60: gate/up [ffn, hidden], down [hidden, ffn]) and an optional
+ * always-on shared expert, plus the scratch of one call (allocated once here, as the
+ * reference's SwiGluScratch is: no allocation per call).  Supported type sets: routed
+ * gate/up IQ2_S; routed down IQ3_S or IQ2_S; shared gate/up Q4_K or IQ2_S; shared down
+ * Q5_K, IQ3_S or IQ2_S.  At most 16 routed experts per token. */
+
+/* [sync] */
+lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh_matrix *const *up,
+                          const lbh_matrix *const *down, size_t n_experts, const lbh_matrix *shared_gate,
+                          const lbh_matrix *shared_up, const lbh_matrix *shared_down, lbh_moe **out,
+                          lbh_error *err);
+lbh_status lbh_moe_destroy(lbh_moe *moe);
+/* Launch-shape knob: gate/up rows per workgroup (routed, shared; 16..256, powers of
+ * two) and output rows per down workgroup (1..256). */
+lbh_status lbh_moe_set_tiles(lbh_moe *moe, int32_t tile_r, int32_t tile_s, int32_t tile_d);
+
+/* [sync] moe_routed_by_id_into (crates/bridge-kernels-reference/src/moe.rs:64-147):
+ * ids ascending with no duplicates, coefs finite (host arrays); output[hidden] =
+ * sum over routed experts in id order of coef * down(SwiGLU(gate x, up x)), then
+ * + 1.0 * shared, accumulated in the reference's order; bit-identical results.
+ * Errors follow the reference's precedence and leave the output unchanged, except
+ * NonFiniteValue on an accumulated destination (index = row), where, as in the
+ * reference, the output holds the accumulation up to the step that overflowed. */
+lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, const float *coefs,
+                                     size_t n_routed, const float *input_dev, size_t input_len, float *output_dev,
+                                     size_t output_len, lbh_error *err);
+
+/* [async] The same computation without validation or status readback (graph
+ * capturable): ids must be ascending, distinct and < n_experts (the last is checked),
+ * coefs and x finite. */
+lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, const float *coefs, size_t n_routed,
+                           const float *x_dev, float *y_dev);
+
 /* ---- diagnostics ------------------------------------------------------------- */
+
+/* [sync] The device expf used by SwiGLU and the routers (swiglu == 0), or the
+ * SwiGLU element gate / (1 + exp(-gate)) * up (swiglu != 0, up_dev required). */
+lbh_status lbh_debug_expf(lbh_ctx *ctx, const float *in_dev, float *out_dev, size_t n, int32_t swiglu,
+                          const float *up_dev, lbh_error *err);
+/* The same function compiled for the host CPU (no device needed), for checking
+ * the device arithmetic against the C library on any machine. */
+void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, const float *up);
 
 /* [sync] Converts n binary16 values with the device conversion the kernels use. */
 lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in_dev, float *out_dev, size_t n,

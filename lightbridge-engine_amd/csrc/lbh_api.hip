@@ -13,14 +13,17 @@
 
 #include "../../include/lightbridge_hip.h"
 #include "lbh_internal.h"
+#include "lbh_math.h"
 
 using namespace lbh;
 
 struct lbh_ctx {
     int device;
+    int cu_count;
     hipStream_t stream;
     DevStatus *status;        // device
     DevStatus *status_host;   // pinned mirror
+    GemvTuning tuning;
 };
 
 struct lbh_matrix {
@@ -91,6 +94,7 @@ MatView view_of(const lbh_matrix *m) {
     v.rows = (int32_t)m->rows;
     v.pad = 0;
     v.units = (long long)(m->rows * m->nb);
+    v.bytes = (long long)m->bytes;
     return v;
 }
 
@@ -144,6 +148,9 @@ lbh_status lbh_ctx_create(int32_t device, void *stream, lbh_ctx **out, lbh_error
     lbh_ctx *c = new (std::nothrow) lbh_ctx();
     if (!c) return fail(err, LBH_HIP_ERROR);
     c->device = device;
+    c->cu_count = prop.multiProcessorCount;
+    c->tuning.lpu = 0;
+    c->tuning.max_blocks = 8 * prop.multiProcessorCount;
     c->stream = static_cast<hipStream_t>(stream);
     hipError_t e = hipMalloc(&c->status, sizeof(DevStatus));
     if (e == hipSuccess) e = hipHostMalloc(&c->status_host, sizeof(DevStatus), hipHostMallocDefault);
@@ -173,6 +180,23 @@ lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream) {
     ctx->stream = static_cast<hipStream_t>(stream);
     return LBH_OK;
 }
+
+lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
+    if (!ctx) return LBH_NULL_ARGUMENT;
+    switch (key) {
+    case LBH_TUNE_GEMV_LPU:
+        if (value != 0 && value != 1 && value != 2 && value != 4) return LBH_INVALID_PARAMETER;
+        ctx->tuning.lpu = value;
+        return LBH_OK;
+    case LBH_TUNE_GEMV_MAX_BLOCKS:
+        if (value < 0) return LBH_INVALID_PARAMETER;
+        ctx->tuning.max_blocks = value ? value : 8 * ctx->cu_count;
+        return LBH_OK;
+    default: return LBH_INVALID_PARAMETER;
+    }
+}
+
+int32_t lbh_ctx_cu_count(const lbh_ctx *ctx) { return ctx ? ctx->cu_count : 0; }
 
 lbh_status lbh_ctx_synchronize(lbh_ctx *ctx, lbh_error *err) {
     if (!ctx) return fail(err, LBH_NULL_ARGUMENT);
@@ -227,6 +251,8 @@ lbh_status lbh_matrix_create(lbh_ctx *ctx, int32_t ty, size_t rows, size_t k, co
     if (byte_len != want) return fail(err, LBH_ENCODED_LENGTH_MISMATCH, ty, 0, want, byte_len);
     if (!bytes) return fail(err, LBH_NULL_ARGUMENT);
     if (nb > 64 || rows > 0x7fffffffull) return fail(err, LBH_UNSUPPORTED_SHAPE, ty, 0, 64, nb);
+    // Kernels address the planes with 32-bit buffer offsets.
+    if (want >= (1ull << 32)) return fail(err, LBH_UNSUPPORTED_SHAPE, ty, 0, (1ull << 32) - 1, want);
     DeviceGuard g(ctx->device);
     uint8_t *staging = nullptr, *planes = nullptr;
     const uint8_t *src = static_cast<const uint8_t *>(bytes);
@@ -329,16 +355,16 @@ lbh_status gemv_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, s
     HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
     if (accumulate) HIP_TRY(launch_find_nonfinite(out, (long long)out_len, &ctx->status->first_bad_dest, ctx->stream));
     HIP_TRY(launch_find_nonfinite(input, (long long)input_len, &ctx->status->first_bad_input, ctx->stream));
-    HIP_TRY(launch_quantize_q8k(input, q8, (long long)(m->k / 256), ctx->status, ctx->stream));
     GemvArgs a{};
     a.m = view_of(m);
-    a.q8 = q8;
+    a.x = input;        // quantized inside the matvec kernel ...
+    a.q8_out = q8;      // ... and published to the caller's scratch (gemv.rs:267)
     a.y = out;
     a.coef = scale;
     a.accumulate = accumulate;
     a.block_sums = nullptr;
     a.status = ctx->status;
-    HIP_TRY(launch_gemv(a, ctx->stream));
+    HIP_TRY(launch_gemv(a, ctx->tuning, ctx->stream));
     lbh_status st = read_status(ctx, err);
     if (st) return st;
     if (ctx->status_host->first_bad_dest != ~0ull) {
@@ -375,7 +401,21 @@ lbh_status lbh_gemv_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, f
     a.y = y;
     a.coef = coef;
     a.accumulate = accumulate;
-    return launch_gemv(a, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+    return launch_gemv(a, ctx->tuning, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+}
+
+lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x, uint8_t *q8_out, float *y, float coef,
+                        int32_t accumulate) {
+    if (!ctx || !m || !x || !y) return LBH_NULL_ARGUMENT;
+    DeviceGuard g(ctx->device);
+    GemvArgs a{};
+    a.m = view_of(m);
+    a.x = x;
+    a.q8_out = q8_out;
+    a.y = y;
+    a.coef = coef;
+    a.accumulate = accumulate;
+    return launch_gemv(a, ctx->tuning, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
 
 lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, int32_t *out) {
@@ -389,7 +429,7 @@ lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t 
     a.q8 = q8;
     a.y = y;
     a.block_sums = out;
-    hipError_t e = launch_gemv(a, ctx->stream);
+    hipError_t e = launch_gemv(a, ctx->tuning, ctx->stream);
     (void)hipFreeAsync(y, ctx->stream);
     return e == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
@@ -400,6 +440,293 @@ lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in, float *out, si
     HIP_TRY(launch_f16_to_f32(in, out, (long long)n, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     return ok(err);
+}
+
+
+
+}  // extern "C"
+
+// ===================================================================== MoE
+
+struct lbh_moe {
+    int device;
+    size_t n_experts, hidden, ffn_r, ffn_s;
+    int type_gate_r, type_down_r;
+    ExpertDev *experts_dev;
+    ExpertDev shared;
+    int has_shared;
+    float *h;
+    uint8_t *q8h;
+    uint32_t *counters;
+    int h_stride, q8_stride, cnt_stride;
+    MoeStatus *status;
+    MoeStatus *status_host;
+    int tile_r, tile_s, tile_d;
+};
+
+namespace {
+
+void free_moe(lbh_moe *m) {
+    if (!m) return;
+    DeviceGuard g(m->device);
+    if (m->experts_dev) (void)hipFree(m->experts_dev);
+    if (m->h) (void)hipFree(m->h);
+    if (m->q8h) (void)hipFree(m->q8h);
+    if (m->counters) (void)hipFree(m->counters);
+    if (m->status) (void)hipFree(m->status);
+    if (m->status_host) (void)hipHostFree(m->status_host);
+    delete m;
+}
+
+bool moe_types_supported(int gr, int ts_gate, int dr, int ts_down) {
+    const bool g = gr == LBH_IQ2_S && (ts_gate == LBH_Q4_K || ts_gate == LBH_IQ2_S);
+    const bool d = (dr == LBH_IQ3_S && (ts_down == LBH_Q5_K || ts_down == LBH_IQ3_S)) ||
+                   (dr == LBH_IQ2_S && (ts_down == LBH_IQ2_S || ts_down == LBH_IQ3_S));
+    return g && d;
+}
+
+MoeArgs moe_args(const lbh_moe *m, const float *x, float *y) {
+    MoeArgs a{};
+    a.experts = m->experts_dev;
+    a.shared = m->shared;
+    a.has_shared = m->has_shared;
+    a.hidden = (int32_t)m->hidden;
+    a.ffn_r = (int32_t)m->ffn_r;
+    a.ffn_s = (int32_t)(m->has_shared ? m->ffn_s : m->ffn_r);
+    a.x = x;
+    a.y = y;
+    a.h = m->h;
+    a.q8h = m->q8h;
+    a.counters = m->counters;
+    a.h_stride = m->h_stride;
+    a.q8_stride = m->q8_stride;
+    a.cnt_stride = m->cnt_stride;
+    a.tile_r = m->tile_r;
+    a.tile_s = m->tile_s;
+    a.tiles_r = (int32_t)((m->ffn_r + m->tile_r - 1) / m->tile_r);
+    a.tiles_s = m->has_shared ? (int32_t)((m->ffn_s + m->tile_s - 1) / m->tile_s) : 0;
+    a.tile_d = m->tile_d;
+    a.stop_step = 0x7fffffff;
+    a.type_gate_r = m->type_gate_r;
+    a.type_down_r = m->type_down_r;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh_matrix *const *up,
+                          const lbh_matrix *const *down, size_t n_experts, const lbh_matrix *shared_gate,
+                          const lbh_matrix *shared_up, const lbh_matrix *shared_down, lbh_moe **out, lbh_error *err) {
+    if (!ctx || !out || !gate || !up || !down) return fail(err, LBH_NULL_ARGUMENT);
+    *out = nullptr;
+    if (n_experts == 0) return fail(err, LBH_DIMENSION_MISMATCH, 0, 3, 1, 0);
+    const bool has_shared = shared_gate || shared_up || shared_down;
+    if (has_shared && !(shared_gate && shared_up && shared_down)) return fail(err, LBH_NULL_ARGUMENT);
+    for (size_t e = 0; e < n_experts; ++e)
+        if (!gate[e] || !up[e] || !down[e]) return fail(err, LBH_NULL_ARGUMENT, 0, e);
+    const size_t hidden = gate[0]->k, ffn_r = gate[0]->rows;
+    const int tg = gate[0]->type, td = down[0]->type;
+    // SwiGluExpert shape rules (activation.rs:6-60): gate/up [ffn, hidden], down [hidden, ffn].
+    for (size_t e = 0; e < n_experts; ++e) {
+        const lbh_matrix *g = gate[e], *u = up[e], *d = down[e];
+        if (g->type != tg || u->type != tg || d->type != td) return fail(err, LBH_UNSUPPORTED_TYPE, g->type, e);
+        if (g->k != hidden || u->k != hidden) return fail(err, LBH_DIMENSION_MISMATCH, g->type, e, hidden, g->k);
+        if (g->rows != ffn_r || u->rows != ffn_r) return fail(err, LBH_DIMENSION_MISMATCH, g->type, e, ffn_r, g->rows);
+        if (d->rows != hidden || d->k != ffn_r) return fail(err, LBH_DIMENSION_MISMATCH, d->type, e, hidden, d->rows);
+        if (g->device != ctx->device || u->device != ctx->device || d->device != ctx->device)
+            return fail(err, LBH_INVALID_PARAMETER, 0, e);
+    }
+    size_t ffn_s = 0;
+    if (has_shared) {
+        ffn_s = shared_gate->rows;
+        if (shared_gate->k != hidden || shared_up->k != hidden || shared_up->rows != ffn_s ||
+            shared_up->type != shared_gate->type || shared_down->rows != hidden || shared_down->k != ffn_s)
+            return fail(err, LBH_DIMENSION_MISMATCH, shared_gate->type, n_experts, hidden, shared_gate->k);
+    }
+    if (!moe_types_supported(tg, has_shared ? shared_gate->type : tg, td, has_shared ? shared_down->type : td))
+        return fail(err, LBH_UNSUPPORTED_TYPE, tg);
+    if (hidden / 256 > 64 || ffn_r / 256 > 64 || ffn_s / 256 > 64) return fail(err, LBH_UNSUPPORTED_SHAPE);
+    DeviceGuard guard(ctx->device);
+    lbh_moe *m = new (std::nothrow) lbh_moe();
+    if (!m) return fail(err, LBH_HIP_ERROR);
+    m->device = ctx->device;
+    m->n_experts = n_experts;
+    m->hidden = hidden;
+    m->ffn_r = ffn_r;
+    m->ffn_s = ffn_s;
+    m->type_gate_r = tg;
+    m->type_down_r = td;
+    m->has_shared = has_shared;
+    if (has_shared) {
+        m->shared.gate = view_of(shared_gate);
+        m->shared.up = view_of(shared_up);
+        m->shared.down = view_of(shared_down);
+    }
+    m->tile_r = 32;
+    m->tile_s = 32;
+    m->tile_d = 16;
+    const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
+    m->h_stride = (int)max_ffn;
+    m->q8_stride = (int)(max_ffn / 256 * 292);
+    m->cnt_stride = (int)(max_ffn / 256);
+    const size_t slots = MOE_MAX_ROUTED + 1;
+    ExpertDev *table = new (std::nothrow) ExpertDev[n_experts];
+    if (!table) {
+        free_moe(m);
+        return fail(err, LBH_HIP_ERROR);
+    }
+    for (size_t e = 0; e < n_experts; ++e) {
+        table[e].gate = view_of(gate[e]);
+        table[e].up = view_of(up[e]);
+        table[e].down = view_of(down[e]);
+    }
+    hipError_t e = hipMalloc(&m->experts_dev, n_experts * sizeof(ExpertDev));
+    if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
+    delete[] table;
+    if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&m->q8h, slots * (size_t)m->q8_stride);
+    if (e == hipSuccess) e = hipMalloc(&m->counters, slots * (size_t)m->cnt_stride * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(m->counters, 0, slots * (size_t)m->cnt_stride * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&m->status, sizeof(MoeStatus));
+    if (e == hipSuccess) e = hipHostMalloc(&m->status_host, sizeof(MoeStatus), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_moe(m);
+        return hip_fail(err, e);
+    }
+    *out = m;
+    return ok(err);
+}
+
+lbh_status lbh_moe_destroy(lbh_moe *m) {
+    if (!m) return LBH_NULL_ARGUMENT;
+    free_moe(m);
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_set_tiles(lbh_moe *m, int32_t tile_r, int32_t tile_s, int32_t tile_d) {
+    if (!m) return LBH_NULL_ARGUMENT;
+    auto ok_tile = [](int t) { return t == 16 || t == 32 || t == 64 || t == 128 || t == 256; };
+    if (!ok_tile(tile_r) || !ok_tile(tile_s) || tile_d < 1 || tile_d > 256) return LBH_INVALID_PARAMETER;
+    m->tile_r = tile_r;
+    m->tile_s = tile_s;
+    m->tile_d = tile_d;
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_routed,
+                           const float *x, float *y) {
+    if (!ctx || !m || !ids || !coefs || !x || !y) return LBH_NULL_ARGUMENT;
+    if (n_routed == 0 || n_routed > MOE_MAX_ROUTED) return LBH_UNSUPPORTED_SHAPE;
+    MoeArgs a = moe_args(m, x, y);
+    a.route.n = (int32_t)n_routed;
+    for (size_t i = 0; i < n_routed; ++i) {
+        if (ids[i] >= m->n_experts) return LBH_INVALID_PARAMETER;   // never index past the expert table
+        a.route.ids[i] = ids[i];
+        a.route.coefs[i] = coefs[i];
+    }
+    a.n_launch = (int32_t)n_routed;
+    DeviceGuard g(ctx->device);
+    if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs,
+                                     size_t n_routed, const float *input, size_t input_len, float *output,
+                                     size_t output_len, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    // moe.rs:73-92
+    if (n_routed == 0) return fail(err, LBH_DIMENSION_MISMATCH, 0, 3, 1, 0);
+    if (input_len != m->hidden) return fail(err, LBH_DIMENSION_MISMATCH, 0, 0, m->hidden, input_len);
+    if (output_len != m->hidden) return fail(err, LBH_DIMENSION_MISMATCH, 0, 1, m->hidden, output_len);
+    if (!ids || !coefs || !input || !output) return fail(err, LBH_NULL_ARGUMENT);
+    if (n_routed > MOE_MAX_ROUTED) return fail(err, LBH_UNSUPPORTED_SHAPE, 0, 0, MOE_MAX_ROUTED, n_routed);
+    // Per-expert checks (moe.rs:94-129) run interleaved with that expert's
+    // preflight in the reference: find the first failing index here, preflight
+    // the experts before it on the device, and report whichever comes first.
+    size_t i_host = n_routed;
+    lbh_error host_err{};
+    for (size_t i = 0; i < n_routed && i_host == n_routed; ++i) {
+        uint32_t bits;
+        std::memcpy(&bits, &coefs[i], 4);
+        if ((bits & 0x7f800000u) == 0x7f800000u) {
+            fail(&host_err, LBH_NON_FINITE_VALUE, 0, 0, 0, 0, bits, 6);
+            i_host = i;
+        } else if (i > 0 && ids[i] == ids[i - 1]) {
+            fail(&host_err, LBH_DUPLICATE_ROUTED_EXPERT, 0, ids[i]);
+            i_host = i;
+        } else if (i > 0 && ids[i] < ids[i - 1]) {
+            fail(&host_err, LBH_ROUTED_EXPERT_ORDER, 0, ids[i], ids[i - 1], ids[i]);
+            i_host = i;
+        } else if (ids[i] >= m->n_experts) {
+            fail(&host_err, LBH_INVALID_PARAMETER, 0, ids[i], m->n_experts, ids[i]);
+            i_host = i;
+        }
+    }
+    if (i_host == 0) {
+        if (err) *err = host_err;
+        return (lbh_status)host_err.status;
+    }
+    DeviceGuard g(ctx->device);
+    MoeArgs a = moe_args(m, input, output);
+    a.route.n = (int32_t)n_routed;
+    for (size_t i = 0; i < i_host; ++i) {
+        a.route.ids[i] = ids[i];
+        a.route.coefs[i] = coefs[i];
+    }
+    a.status = m->status;
+    a.check = 1;
+    a.n_launch = (int32_t)i_host;
+    if (i_host < n_routed) a.has_shared = 0;   // the reference stops before the shared preflight
+    HIP_TRY(launch_moe_reset_status(m->status, ctx->stream));
+    HIP_TRY(launch_find_nonfinite(input, (long long)input_len, &m->status->first_bad_input, ctx->stream));
+    HIP_TRY(launch_moe_gate_up(a, ctx->stream));
+    if (i_host == n_routed) HIP_TRY(launch_moe_down(a, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(m->status_host, m->status, sizeof(MoeStatus), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    const MoeStatus st = *m->status_host;
+    if (st.first_bad_input != ~0ull)   // gemv_into's validate_dimensions on the first expert
+        return fail(err, LBH_NON_FINITE_VALUE, m->type_gate_r, st.first_bad_input, 0, 0,
+                    read_f32_bits(ctx, input + st.first_bad_input), 0);
+    if (st.first_bad_swiglu != ~0ull) {   // apply_swiglu (activation.rs:170-178)
+        const unsigned order = (unsigned)(st.first_bad_swiglu >> 32), lane = (unsigned)st.first_bad_swiglu;
+        const int slot = order < n_routed ? (int)order : MOE_SHARED_SLOT;
+        return fail(err, LBH_NON_FINITE_VALUE, 0, lane, 0, 0,
+                    read_f32_bits(ctx, m->h + (size_t)slot * m->h_stride + lane), 5);
+    }
+    if (i_host < n_routed) {
+        if (err) *err = host_err;
+        return (lbh_status)host_err.status;
+    }
+    if (st.first_bad_fold != ~0ull) {
+        // The accumulation call after step i* rejects the non-finite
+        // destination (gemv.rs:126-127), leaving the output as it stood after
+        // step i*: recompute the combine up to that step.
+        const int step = (int)(st.first_bad_fold >> 32);
+        const unsigned row = (unsigned)st.first_bad_fold;
+        a.check = 0;
+        a.stop_step = step;
+        HIP_TRY(launch_moe_down(a, ctx->stream));
+        HIP_TRY(hipStreamSynchronize(ctx->stream));
+        return fail(err, LBH_NON_FINITE_VALUE, 0, row, 0, 0, read_f32_bits(ctx, output + row), 3);
+    }
+    return ok(err);
+}
+
+lbh_status lbh_debug_expf(lbh_ctx *ctx, const float *in, float *out, size_t n, int32_t swiglu, const float *up,
+                          lbh_error *err) {
+    if (!ctx || !in || !out || (swiglu && !up)) return fail(err, LBH_NULL_ARGUMENT);
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_expf(in, out, (long long)n, swiglu, up, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    return ok(err);
+}
+
+void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, const float *up) {
+    for (size_t i = 0; i < n; ++i) out[i] = swiglu ? swiglu_ref(in[i], up[i]) : expf_libm(in[i]);
 }
 
 }  // extern "C"

@@ -1,0 +1,586 @@
+// lbh_dev.h — device building blocks shared by every kernel translation unit.
+//
+// Arithmetic contract (bit-identical to the reference CPU path,
+// crates/bridge-quant-layout/src/q8_k.rs):
+//   * integer block sums are exact int32 (v_dot4_i32_i8 on signed bytes);
+//   * every f32 operation is a separately rounded IEEE op in the reference's
+//     order (built with -ffp-contract=off; __fmul_rn/__fadd_rn where the order
+//     matters), divides are correctly rounded, denormals are preserved.
+//
+// Work decomposition used by the matvec kernels: a "unit" is one
+// (row, 256-element super-block) pair; LPU lanes ("parts") share a unit, each
+// taking NG/LPU of its natural groups (8 groups of 32 for IQ2_S/IQ3_S, 4
+// groups of 64 for Q4_K/Q5_K).  Lane l of a wave owns
+//     part = l % LPU,  block b = (l / LPU) % NB,  row slot = l / (LPU * NB),
+// so its K-range (block b, part p) is fixed for the whole kernel: the Q8_K
+// activation bytes it needs live in registers while rows stream past.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lbh_layout.h"
+
+namespace lbh {
+
+// ------------------------------------------------------------------ helpers
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4(static_cast<int>(a), static_cast<int>(b), c, false);
+}
+
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+    return __builtin_amdgcn_perm(s0, s1, sel);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t v, int i) { return (v >> (8 * i)) & 0xffu; }
+
+// Byte-wise negation of grid magnitudes (all grid bytes are in 1..63: no borrows).
+__device__ __forceinline__ uint32_t neg_bytes(uint32_t g) { return (g ^ 0xffffffffu) + 0x01010101u; }
+
+// v_perm selector applying four sign bits to a dword of magnitudes: byte i
+// takes the negated magnitude (selector 4 + i, from the first source) when bit
+// i of nib is set, else the magnitude (selector i, second source).
+// nib * 0x810204 moves bit i to bit 8i+2 with no carries between terms.
+__device__ __forceinline__ uint32_t sign_sel(uint32_t nib) {
+    return ((nib * 0x810204u) & 0x04040404u) | 0x03020100u;
+}
+
+// Signed grid dword from a (magnitude, negated magnitude) pair.
+__device__ __forceinline__ uint32_t apply_signs(uint32_t pos, uint32_t neg, uint32_t nib) {
+    return perm(neg, pos, sign_sel(nib));
+}
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+__device__ __forceinline__ uint2 ld_u64(const uint8_t *p) { return *reinterpret_cast<const uint2 *>(p); }
+__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+__device__ __forceinline__ uint4 ld_chunk(const uint8_t *planes, long long U, int c, long long u) {
+    return *reinterpret_cast<const uint4 *>(planes + ((long long)c * U + u) * 16);
+}
+
+// Weight planes read through a raw buffer resource: SGPR base + 32-bit
+// offsets, so a chunk load costs no VALU address arithmetic (the plane offset
+// c * U * 16 is a scalar operand) and out-of-range offsets read zero.
+// Matrices are limited to < 4 GiB of planes.  Word 3 = 0x00020000 is the
+// raw-buffer configuration of the gfx9 family (gfx950 included).
+struct Planes {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t U16;   // units * 16: byte size of one chunk plane
+    uint32_t U;     // units
+};
+
+__device__ __forceinline__ Planes make_planes(const uint8_t *base, long long units, long long bytes) {
+    Planes p;
+    p.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), (short)0, (int)(uint32_t)bytes, 0x00020000);
+    p.U16 = (uint32_t)(units * 16);
+    p.U = (uint32_t)units;
+    return p;
+}
+
+__device__ __forceinline__ uint4 bld128(const Planes &P, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(P.rsrc, voff, soff, 0));
+}
+__device__ __forceinline__ uint2 bld64(const Planes &P, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(P.rsrc, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t bld32(const Planes &P, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(P.rsrc, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bld16(const Planes &P, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b16(P.rsrc, voff, soff, 0);
+}
+__device__ __forceinline__ uint32_t bld8(const Planes &P, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b8(P.rsrc, voff, soff, 0);
+}
+
+// 24-bit signed multiply (full rate): every integer product in the dots has
+// operands well inside +-2^23.
+__device__ __forceinline__ int32_t mul24(int32_t a, int32_t b) { return __mul24(a, b); }
+
+// ------------------------------------------------------------ Q8_K quantize
+
+// nearest_int (q8_k.rs:224-228): magic-number rounding, ties to even.
+__device__ __forceinline__ int32_t nearest_int(float v) {
+    const float s = __fadd_rn(v, 12582912.0f);
+    const int32_t b = __float_as_int(s);
+    return (b & 0x007fffff) - 0x00400000;
+}
+
+// One wave quantizes up to four consecutive 256-element blocks, 16 lanes per
+// block and 16 elements per lane: quantize_row_q8_k_into (q8_k.rs:35-73).
+// Block first + (lane / 16) reads x + 256 * block and writes 292 bytes at
+// out + 292 * block (global memory or LDS).  Every lane of the wave must call
+// it; blocks at or beyond `nblocks` are skipped.
+//
+// The arg-max keeps the first index of the largest |x| (q8_k.rs:43-49): each
+// lane scans its 16 elements in order with a strict compare, the row of 16
+// lanes reduces the maximum, and the lowest lane holding it (a ballot) owns
+// the first index, since lane order is element order.  bsums[g] covers
+// exactly the 16 elements of lane g.
+__device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x, uint8_t *out, long long first,
+                                                     long long nblocks) {
+    const int lane = threadIdx.x & 63;
+    const int li = lane & 15;
+    const long long blk = first + (lane >> 4);
+    const bool valid = blk < nblocks;
+    float v[16];
+    if (valid) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + blk * 256 + 16 * li);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 f = src[i];
+            v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+    }
+    uint32_t amax_l = __float_as_uint(fabsf(v[0]));
+    float max_l = v[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        const uint32_t a = __float_as_uint(fabsf(v[i]));
+        if (a > amax_l) amax_l = a, max_l = v[i];
+    }
+    uint32_t amax = amax_l;
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+        const uint32_t o = __shfl_xor(amax, off, 16);
+        amax = o > amax ? o : amax;
+    }
+    const unsigned long long hit = __ballot(amax_l == amax);
+    const int row0 = lane & 48;
+    const int owner = row0 + __builtin_ctzll((hit >> row0) & 0xffffull);
+    const float maxv = __shfl(max_l, owner, 64);
+    uint32_t packed[4] = {0, 0, 0, 0};
+    int32_t qsum = 0;
+    float d = 0.0f;
+    if (amax != 0) {
+        const float iscale = -127.0f / maxv;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int32_t q = nearest_int(__fmul_rn(iscale, v[i]));
+            q = q < 127 ? q : 127;
+            packed[i >> 2] |= (uint32_t)(uint8_t)(int8_t)q << (8 * (i & 3));
+            qsum += (int8_t)q;
+        }
+        d = 1.0f / iscale;
+    }
+    const int32_t next = __shfl_down(qsum, 1, 64);
+    if (valid) {
+        uint8_t *ob = out + blk * 292;
+        uint32_t *qs = reinterpret_cast<uint32_t *>(ob + 4 + 16 * li);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qs[i] = packed[i];
+        if ((li & 1) == 0)
+            *reinterpret_cast<uint32_t *>(ob + 260 + 2 * li) =
+                (uint32_t)(uint16_t)(int16_t)qsum | ((uint32_t)(uint16_t)(int16_t)next << 16);
+        if (li == 0) *reinterpret_cast<uint32_t *>(ob) = __float_as_uint(d);
+    }
+}
+
+// ------------------------------------------------------------ type traits
+
+template <int TY>
+struct Traits;
+template <>
+struct Traits<T_IQ2_S> {
+    static constexpr int NG = 8;      // natural groups per block
+    static constexpr int NCH = 1;     // f32 chains of the fold
+    static constexpr bool KQ = false;
+};
+template <>
+struct Traits<T_IQ3_S> {
+    static constexpr int NG = 8;
+    static constexpr int NCH = 1;
+    static constexpr bool KQ = false;
+};
+template <>
+struct Traits<T_Q4_K> {
+    static constexpr int NG = 4;
+    static constexpr int NCH = 9;     // lane sums 0..7 + minimum sum
+    static constexpr bool KQ = true;
+};
+template <>
+struct Traits<T_Q5_K> {
+    static constexpr int NG = 4;
+    static constexpr int NCH = 9;
+    static constexpr bool KQ = true;
+};
+
+// ---------------------------------------------------------- activations
+
+// IQ activation slice: the 32*G quants of groups [G*p, G*p + G) as dwords.
+template <int G>
+struct ActIQ {
+    uint32_t q[8 * G];
+    float d8;
+};
+
+// K-quant activation slice for groups [G*p, G*p + G): sub-blocks j = 2g, 2g+1;
+// t[j][r] holds the four bytes 32j + r + 8k (k = 0..3) so one dot4 per
+// residue r reproduces the reference's lane split (q8_k.rs:301-312);
+// bsp[j] = bsums[2j] + bsums[2j+1].
+template <int G>
+struct ActKQ {
+    uint32_t t[2 * G][8];
+    int32_t bsp[2 * G];
+    float d8;
+};
+
+template <int TY, int LPU>
+using ActOf = typename std::conditional<Traits<TY>::KQ, ActKQ<Traits<TY>::NG / LPU>,
+                                        ActIQ<Traits<TY>::NG / LPU>>::type;
+
+// `blk` is a 292-byte Q8_K block (global or LDS); part p of LPU.
+template <int G>
+__device__ __forceinline__ void load_act(const uint8_t *blk, int p, ActIQ<G> &a) {
+    a.d8 = __uint_as_float(ld_u32(blk));
+    const uint8_t *q = blk + 4 + 32 * G * p;
+#pragma unroll
+    for (int i = 0; i < 8 * G; ++i) a.q[i] = ld_u32(q + 4 * i);
+}
+
+template <int G>
+__device__ __forceinline__ void load_act(const uint8_t *blk, int p, ActKQ<G> &a) {
+    a.d8 = __uint_as_float(ld_u32(blk));
+    const uint8_t *q = blk + 4 + 64 * G * p;
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+        uint32_t n[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) n[i] = ld_u32(q + 32 * j + 4 * i);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v |= byte_of(n[2 * k + t / 4], t % 4) << (8 * k);
+            a.t[j][t] = v;
+        }
+    }
+    const uint8_t *bs = blk + 260 + 8 * G * p;
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+        const uint32_t w = ld_u32(bs + 4 * j);
+        a.bsp[j] = (int32_t)(int16_t)(w & 0xffff) + (int32_t)(int16_t)(w >> 16);
+    }
+}
+
+// ----------------------------------------------------------- grid tables
+//
+// LDS copies of the IQ codebooks, laid out so a signed grid dword is one v_perm:
+//   IQ2S: uint2 x 1024 (8 KiB) of byte codes 0/1/2 for the magnitudes 8/25/43
+//         (the only values in the codebook); v_perm with selector code + 4*sign
+//         picks from the constant dwords {8,25,43} / {-8,-25,-43}.
+//   IQ3S: uint2 {pos, neg} x 512 (4 KiB): each entry next to its byte-wise negation.
+
+// Each translation unit holds its own copy (no relocatable device code).
+#include "lbh_iq_grids.inc"
+static __constant__ uint64_t c_iq2s_grid[1024] = {LBH_IQ2S_GRID_VALUES};
+static __constant__ uint32_t c_iq3s_grid[512] = {LBH_IQ3S_GRID_VALUES};
+
+template <int TY>
+struct GridLDS {
+    static constexpr int BYTES = TY == T_IQ2_S ? 1024 * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
+};
+
+// Fills the grid for TY into `lds` (cooperatively, all threads of the block);
+// the caller synchronises afterwards.
+template <int TY>
+__device__ __forceinline__ void fill_grid(void *lds) {
+    if constexpr (TY == T_IQ2_S) {
+        uint2 *g = reinterpret_cast<uint2 *>(lds);
+        for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
+            const uint64_t v = c_iq2s_grid[i];
+            uint32_t c[2] = {0, 0};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t m = (uint32_t)(v >> (8 * e)) & 0xffu;
+                c[e >> 2] |= (m == 8 ? 0u : m == 25 ? 1u : 2u) << (8 * (e & 3));
+            }
+            g[i] = make_uint2(c[0], c[1]);
+        }
+    } else if constexpr (TY == T_IQ3_S) {
+        uint2 *g = reinterpret_cast<uint2 *>(lds);
+        for (int i = threadIdx.x; i < 512; i += blockDim.x) {
+            const uint32_t v = c_iq3s_grid[i];
+            g[i] = make_uint2(v, neg_bytes(v));
+        }
+    }
+}
+
+// ------------------------------------------------------------ weight slices
+//
+// The bytes one lane needs from its unit, loaded from the device layout
+// (lbh_layout.h).  Load and compute are separate so a caller can keep the
+// loads of the next unit in flight while computing the current one.
+
+template <int TY, int LPU>
+struct WSlice;
+
+// IQ2_S: G = 8 / LPU groups; qs[4G], signs[4G], qh[G], scales[G] bytes.
+template <int LPU>
+struct WSlice<T_IQ2_S, LPU> {
+    static constexpr int G = 8 / LPU;
+    uint32_t qs[G], sg[G];
+    uint32_t qh, sc;   // G bytes each (G <= 4), or the low 4 when G == 8 (see hq, hs)
+    uint32_t qh2, sc2; // G == 8: groups 4..7
+    uint32_t d;
+};
+
+// Per-lane constant part of a slice's load offsets (the lane's part p never
+// changes), added to u * 16 each step.
+template <int TY, int LPU>
+__device__ __forceinline__ uint32_t part_offset(const Planes &P, int p) {
+    if constexpr (TY == T_IQ2_S && LPU == 4) return (uint32_t)(p >> 1) * P.U16 + 8u * (uint32_t)(p & 1);
+    else if constexpr (TY == T_IQ2_S && LPU == 2) return (uint32_t)p * P.U16;
+    else if constexpr (TY == T_IQ3_S && LPU == 4) return (uint32_t)p * P.U16;
+    else if constexpr (TY == T_IQ3_S && LPU == 2) return (uint32_t)(2 * p) * P.U16;
+    else if constexpr ((TY == T_Q4_K || TY == T_Q5_K) && LPU < 4) return (uint32_t)(2 * (4 / LPU) * p) * P.U16;
+    else if constexpr (TY == T_Q4_K || TY == T_Q5_K) return (uint32_t)(2 * p) * P.U16;
+    else return 0u;
+}
+
+template <int LPU>
+__device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t po, int p, WSlice<T_IQ2_S, LPU> &w) {
+    constexpr int G = 8 / LPU;
+    const uint32_t u16 = u * 16;
+    w.d = bld16(P, u * 2, 5 * P.U16);
+    if constexpr (G == 8) {
+        const uint4 a = bld128(P, u16, 0), b = bld128(P, u16, P.U16);
+        const uint4 c = bld128(P, u16, 2 * P.U16), d = bld128(P, u16, 3 * P.U16);
+        const uint4 e = bld128(P, u16, 4 * P.U16);
+        w.qs[0] = a.x, w.qs[1] = a.y, w.qs[2] = a.z, w.qs[3] = a.w;
+        w.qs[4] = b.x, w.qs[5] = b.y, w.qs[6] = b.z, w.qs[7] = b.w;
+        w.sg[0] = c.x, w.sg[1] = c.y, w.sg[2] = c.z, w.sg[3] = c.w;
+        w.sg[4] = d.x, w.sg[5] = d.y, w.sg[6] = d.z, w.sg[7] = d.w;
+        w.qh = e.x, w.qh2 = e.y, w.sc = e.z, w.sc2 = e.w;
+    } else if constexpr (G == 4) {
+        const uint4 a = bld128(P, u16 + po, 0), c = bld128(P, u16 + po, 2 * P.U16);
+        w.qs[0] = a.x, w.qs[1] = a.y, w.qs[2] = a.z, w.qs[3] = a.w;
+        w.sg[0] = c.x, w.sg[1] = c.y, w.sg[2] = c.z, w.sg[3] = c.w;
+        const uint32_t e = u16 + 4u * (uint32_t)p;
+        w.qh = bld32(P, e, 4 * P.U16);
+        w.sc = bld32(P, e + 8, 4 * P.U16);
+        w.qh2 = w.sc2 = 0;
+    } else {  // G == 2
+        const uint2 a = bld64(P, u16 + po, 0);
+        const uint2 c = bld64(P, u16 + po, 2 * P.U16);
+        w.qs[0] = a.x, w.qs[1] = a.y;
+        w.sg[0] = c.x, w.sg[1] = c.y;
+        const uint32_t e = u16 + 2u * (uint32_t)p;
+        w.qh = bld16(P, e, 4 * P.U16);
+        w.sc = bld16(P, e + 8, 4 * P.U16);
+        w.qh2 = w.sc2 = 0;
+    }
+}
+
+// IQ2_S magnitudes {8, 25, 43} and their negations as v_perm sources.
+constexpr uint32_t IQ2S_POS = 0x002b1908u;
+constexpr uint32_t IQ2S_NEG = 0x00d5e7f8u;
+
+// IQ2_S integer block sum over the slice's groups (q8_k.rs:337-364).
+template <int LPU>
+__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, const ActIQ<8 / LPU> &a,
+                                             const uint2 *grid) {
+    constexpr int G = 8 / LPU;
+    int32_t bsum = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+        const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
+        int32_t part[2] = {0, 0};
+#pragma unroll
+        for (int lg = 0; lg < 4; ++lg) {
+            const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
+            const uint2 code = grid[idx];
+            const uint32_t s = byte_of(w.sg[g], lg);
+            // bit i of a sign nibble -> bit 8i+2 (value 4: the negated
+            // source).  The nibble must be isolated first: with all eight
+            // bits, bit 7 and bit 0 would collide at bit 9 and carry.
+            const uint32_t sel_lo = (((s & 15u) * 0x810204u) & 0x04040404u) | code.x;
+            const uint32_t sel_hi = (((s >> 4) * 0x810204u) & 0x04040404u) | code.y;
+            part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
+            part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
+        }
+        bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
+    }
+    return bsum;
+}
+
+// IQ3_S: G = 8 / LPU groups; qs[8G], signs[4G], qh[G], scale nibbles[G].
+template <int LPU>
+struct WSlice<T_IQ3_S, LPU> {
+    static constexpr int G = 8 / LPU;
+    uint32_t qs[2 * G], sg[G];
+    uint32_t qh, qh2, sc;
+    uint32_t d;
+};
+
+template <int LPU>
+__device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t po, int p, WSlice<T_IQ3_S, LPU> &w) {
+    constexpr int G = 8 / LPU;
+    const uint32_t u16 = u * 16, tail = u * 12, tail_base = 6 * P.U16;
+    w.d = bld16(P, u * 2, 6 * P.U16 + 12 * P.U);
+    if constexpr (G == 8) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 v = bld128(P, u16, c * P.U16);
+            w.qs[4 * c] = v.x, w.qs[4 * c + 1] = v.y, w.qs[4 * c + 2] = v.z, w.qs[4 * c + 3] = v.w;
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint4 v = bld128(P, u16, (4 + c) * P.U16);
+            w.sg[4 * c] = v.x, w.sg[4 * c + 1] = v.y, w.sg[4 * c + 2] = v.z, w.sg[4 * c + 3] = v.w;
+        }
+        w.qh = bld32(P, tail, tail_base), w.qh2 = bld32(P, tail + 4, tail_base), w.sc = bld32(P, tail + 8, tail_base);
+    } else if constexpr (G == 4) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint4 v = bld128(P, u16 + po, c * P.U16);
+            w.qs[4 * c] = v.x, w.qs[4 * c + 1] = v.y, w.qs[4 * c + 2] = v.z, w.qs[4 * c + 3] = v.w;
+        }
+        const uint4 sv = bld128(P, u16 + (uint32_t)p * P.U16, 4 * P.U16);
+        w.sg[0] = sv.x, w.sg[1] = sv.y, w.sg[2] = sv.z, w.sg[3] = sv.w;
+        w.qh = bld32(P, tail + 4u * (uint32_t)p, tail_base);
+        w.sc = bld16(P, tail + 8u + 2u * (uint32_t)p, tail_base);
+        w.qh2 = 0;
+    } else {  // G == 2
+        const uint4 v = bld128(P, u16 + po, 0);
+        w.qs[0] = v.x, w.qs[1] = v.y, w.qs[2] = v.z, w.qs[3] = v.w;
+        const uint2 sv = bld64(P, u16 + (uint32_t)(p >> 1) * P.U16 + 8u * (uint32_t)(p & 1), 4 * P.U16);
+        w.sg[0] = sv.x, w.sg[1] = sv.y;
+        w.qh = bld16(P, tail + 2u * (uint32_t)p, tail_base);
+        w.sc = bld8(P, tail + 8u + (uint32_t)p, tail_base);
+        w.qh2 = 0;
+    }
+}
+
+// IQ3_S integer block sum over the slice's groups (q8_k.rs:380-428).
+template <int LPU>
+__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, const ActIQ<8 / LPU> &a,
+                                             const uint2 *grid) {
+    constexpr int G = 8 / LPU;
+    int32_t bsum = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+        // local group g is global group gg = G*p + g; its scale nibble is
+        // nibble (gg & 1) of scale byte gg / 2, i.e. nibble g of w.sc (G <= 4)
+        // or nibble g of the 32-bit word holding all four scale bytes (G == 8).
+        const uint32_t ps = (w.sc >> (4 * g)) & 15u;
+        int32_t gs = 0;
+#pragma unroll
+        for (int lg = 0; lg < 4; ++lg) {
+            const uint32_t qq = w.qs[2 * g + (lg >> 1)];
+            const int sh = 16 * (lg & 1);
+            const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
+            const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
+            const uint32_t s = byte_of(w.sg[g], lg);
+            const uint2 g1 = grid[i1], g2 = grid[i2];
+            gs = dot4(apply_signs(g1.x, g1.y, s & 15u), a.q[8 * g + 2 * lg], gs);
+            gs = dot4(apply_signs(g2.x, g2.y, s >> 4), a.q[8 * g + 2 * lg + 1], gs);
+        }
+        bsum += mul24(gs, (int32_t)(2 * ps + 1));
+    }
+    return bsum;
+}
+
+// Q4_K / Q5_K: G = 4 / LPU groups of 64 (sub-blocks 2g, 2g+1).
+template <int TY, int LPU>
+struct WSliceKQ {
+    static constexpr int G = 4 / LPU;
+    uint4 hdr;                     // d|dmin, scales[12]
+    uint32_t q[G][8];              // residue-major qs of each group
+    uint32_t qh[TY == T_Q5_K ? 8 : 1];
+};
+template <int LPU>
+struct WSlice<T_Q4_K, LPU> : WSliceKQ<T_Q4_K, LPU> {};
+template <int LPU>
+struct WSlice<T_Q5_K, LPU> : WSliceKQ<T_Q5_K, LPU> {};
+
+template <int TY, int LPU>
+__device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t po, int p, WSliceKQ<TY, LPU> &w) {
+    constexpr int G = 4 / LPU;
+    constexpr int QS0 = TY == T_Q5_K ? 3 : 1;
+    const uint32_t u16 = u * 16;
+    w.hdr = bld128(P, u16, 0);
+    if constexpr (TY == T_Q5_K) {
+        const uint4 v0 = bld128(P, u16, P.U16), v1 = bld128(P, u16, 2 * P.U16);
+        w.qh[0] = v0.x, w.qh[1] = v0.y, w.qh[2] = v0.z, w.qh[3] = v0.w;
+        w.qh[4] = v1.x, w.qh[5] = v1.y, w.qh[6] = v1.z, w.qh[7] = v1.w;
+    }
+    // chunks QS0 + 2 * (G * p + g) and the one after it; po = 2 * G * p * U16
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint4 v0 = bld128(P, u16 + po, (QS0 + 2 * g) * P.U16);
+        const uint4 v1 = bld128(P, u16 + po, (QS0 + 2 * g + 1) * P.U16);
+        w.q[g][0] = v0.x, w.q[g][1] = v0.y, w.q[g][2] = v0.z, w.q[g][3] = v0.w;
+        w.q[g][4] = v1.x, w.q[g][5] = v1.y, w.q[g][6] = v1.z, w.q[g][7] = v1.w;
+    }
+}
+
+// scale_min (k_quants.rs:231-240) of sub-block j from the 12 packed bytes
+// (s0 = bytes 0-3, s1 = 4-7, s2 = 8-11).
+__device__ __forceinline__ void scale_min_of(uint32_t s0, uint32_t s1, uint32_t s2, int j, int32_t &sc, int32_t &mn) {
+    if (j < 4) {
+        sc = byte_of(s0, j) & 63;
+        mn = byte_of(s1, j) & 63;
+    } else {
+        sc = (byte_of(s2, j - 4) & 15) | ((byte_of(s0, j - 4) >> 6) << 4);
+        mn = (byte_of(s2, j - 4) >> 4) | ((byte_of(s1, j - 4) >> 6) << 4);
+    }
+}
+
+// Q4_K / Q5_K integer stage over the slice (q8_k.rs:288-312): lane sums by
+// residue and the slice's share of minimum_sum.  Sub-block index j is global
+// (2 * (G*p + g) + h); p is the lane's part.
+template <int TY, int LPU>
+__device__ __forceinline__ void slice_sums(const WSliceKQ<TY, LPU> &w, const ActKQ<4 / LPU> &a, int p,
+                                           int32_t ls[8], int32_t &ms) {
+    constexpr int G = 4 / LPU;
+    ms = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) ls[t] = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int gg = G * p + g;
+        int32_t sc0, mn0, sc1, mn1;
+        scale_min_of(w.hdr.y, w.hdr.z, w.hdr.w, 2 * gg, sc0, mn0);
+        scale_min_of(w.hdr.y, w.hdr.z, w.hdr.w, 2 * gg + 1, sc1, mn1);
+        ms += mul24(mn0, a.bsp[2 * g]) + mul24(mn1, a.bsp[2 * g + 1]);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t lo = w.q[g][t] & 0x0f0f0f0fu;
+            uint32_t hi = (w.q[g][t] >> 4) & 0x0f0f0f0fu;
+            if constexpr (TY == T_Q5_K) {
+                lo |= ((w.qh[t] >> (2 * gg)) & 0x01010101u) << 4;
+                hi |= ((w.qh[t] >> (2 * gg + 1)) & 0x01010101u) << 4;
+            }
+            ls[t] += mul24(sc0, dot4(lo, a.t[2 * g][t], 0));
+            ls[t] += mul24(sc1, dot4(hi, a.t[2 * g + 1][t], 0));
+        }
+    }
+}
+
+// Sum an int32 over the LPU lanes of a unit (exact; the result is valid in every lane).
+template <int LPU>
+__device__ __forceinline__ int32_t unit_reduce(int32_t v) {
+    if constexpr (LPU >= 2) v += __shfl_xor(v, 1, 64);
+    if constexpr (LPU >= 4) v += __shfl_xor(v, 2, 64);
+    if constexpr (LPU >= 8) v += __shfl_xor(v, 4, 64);
+    return v;
+}
+
+}  // namespace lbh

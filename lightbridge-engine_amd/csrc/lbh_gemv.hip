@@ -1,0 +1,149 @@
+// lbh_gemv.hip — {IQ2_S, IQ3_S, Q4_K, Q5_K} x Q8_K matvec for gfx950.
+//
+// y[r] = vec_dot_q8_k(row r, q8)  (crates/bridge-quant-layout/src/q8_k.rs:80-89,
+// row loop of crates/bridge-kernels-reference/src/gemv.rs:56-70), or
+// y[r] += coef * dot (gemv.rs:161-171).
+//
+// Decode matvecs are HBM-bound: every weight byte is read once with 16-byte
+// loads from the chunk-major device layout (lbh_layout.h), the IQ codebooks
+// sit in LDS next to their negations, the integer block sums use v_dot4, and
+// the per-row f32 fold runs in the reference's sequential block order out of
+// LDS.  With FUSEQ the kernel also performs the Q8_K quantization of the f32
+// input itself (each workgroup quantizes into LDS; workgroup 0 publishes the
+// bytes), which removes a launch from every gemv_into.
+#include "lbh_internal.h"
+#include "lbh_rows.h"
+
+namespace lbh {
+
+constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_WAVES = GEMV_THREADS / 64;
+constexpr int MAX_NB = 64;
+
+__device__ __forceinline__ bool status_set(const DevStatus *st) {
+    return st && (st->first_bad_input != ~0ull || st->first_bad_dest != ~0ull);
+}
+
+__device__ __forceinline__ void store_y(const GemvArgs &p, int r, float v) {
+    if (p.accumulate)
+        p.y[r] = __fadd_rn(p.y[r], __fmul_rn(p.coef, v));
+    else
+        p.y[r] = v;
+}
+
+template <int TY, int LPU, bool FUSEQ>
+__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
+    constexpr int GB = GridLDS<TY>::BYTES > 0 ? GridLDS<TY>::BYTES : 16;
+    __shared__ __align__(16) uint8_t s_grid[GB];
+    __shared__ __align__(16) uint8_t s_q8[FUSEQ ? MAX_NB * 292 : 16];
+    __shared__ FoldLDS<TY> s_fold[GEMV_WAVES];
+
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int NB = p.m.nb;
+    const LaneMap<LPU> L(lane, NB);
+    const int rows = p.m.rows;
+    const Planes P = make_planes(p.m.planes, p.m.units, p.m.bytes);
+    const uint32_t po = part_offset<TY, LPU>(P, L.part);
+    const int items = (rows + L.rpw - 1) / L.rpw;
+    const int nw = gridDim.x * GEMV_WAVES;
+    using W = WOf<TY, LPU>;
+
+    auto issue = [&](int it, W &w) {
+        const int r = it * L.rpw + L.slot;
+        if (it < items && L.lane_on && r < rows) load_slice(P, (uint32_t)(r * NB + L.b), po, L.part, w);
+    };
+
+    // The first weight loads go out before the codebook fill, the in-kernel
+    // quantization and the barrier, so their HBM latency overlaps that setup.
+    int it = blockIdx.x * GEMV_WAVES + wid;
+    W wa, wb;
+    issue(it, wa);
+
+    fill_grid<TY>(s_grid);
+    if constexpr (FUSEQ) {
+        for (int b0 = 4 * wid; b0 < NB; b0 += 4 * GEMV_WAVES) quantize_blocks_wave(p.x, s_q8, b0, NB);
+    }
+    __syncthreads();
+    if (status_set(p.status)) return;
+    if constexpr (FUSEQ) {
+        if (p.q8_out && blockIdx.x == 0)
+            for (int i = threadIdx.x; i < NB * 73; i += GEMV_THREADS)
+                reinterpret_cast<uint32_t *>(p.q8_out)[i] = reinterpret_cast<const uint32_t *>(s_q8)[i];
+    }
+
+    ActOf<TY, LPU> act;
+    load_act(FUSEQ ? s_q8 + L.b * 292 : p.q8 + (long long)L.b * 292, L.part, act);
+
+    auto process = [&](int it, const W &w) {
+        const int r = it * L.rpw + L.slot;
+        const bool on = L.lane_on && r < rows;
+        const float v = row_dot<TY, LPU>(w, act, on, L, s_grid, s_fold[wid], p.block_sums, (long long)r * NB + L.b);
+        if (on && L.leader()) store_y(p, r, v);
+    };
+
+    // Software pipeline, unrolled twice so the two register buffers alternate
+    // without copies: the loads of the wave's next rows are in flight while
+    // the current rows are computed.
+    while (it < items) {
+        issue(it + nw, wb);
+        process(it, wa);
+        it += nw;
+        if (it >= items) break;
+        issue(it + nw, wa);
+        process(it, wb);
+        it += nw;
+    }
+}
+
+static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+template <int TY, int LPU>
+static hipError_t launch_typed(const GemvArgs &a, int max_blocks, hipStream_t s) {
+    const int rpw = (64 / LPU) / a.m.nb;
+    const int items = cdiv(a.m.rows, rpw);
+    int grid = cdiv(items, GEMV_WAVES);
+    if (max_blocks > 0 && grid > max_blocks) grid = max_blocks;
+    if (a.x)
+        hipLaunchKernelGGL((k_gemv<TY, LPU, true>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemv<TY, LPU, false>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int TY>
+static hipError_t launch_lpu(const GemvArgs &a, int lpu, int max_blocks, hipStream_t s) {
+    // A wave step must hold at least one whole row: NB * LPU <= 64.
+    while (lpu > 1 && a.m.nb * lpu > 64) lpu >>= 1;
+    switch (lpu) {
+    case 4: return launch_typed<TY, 4>(a, max_blocks, s);
+    case 2: return launch_typed<TY, 2>(a, max_blocks, s);
+    default: return launch_typed<TY, 1>(a, max_blocks, s);
+    }
+}
+
+// Built-in lanes-per-unit choice per type.
+static int default_lpu(int ty) {
+    switch (ty) {
+    case T_IQ2_S: return 2;
+    case T_IQ3_S: return 2;
+    case T_Q4_K: return 2;
+    case T_Q5_K: return 2;
+    default: return 1;
+    }
+}
+
+hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
+    const int nb = a.m.nb;
+    if (nb < 1 || nb > MAX_NB || a.m.rows < 1) return hipErrorInvalidValue;
+    if (!a.q8 && !a.x) return hipErrorInvalidValue;
+    const int lpu = t.lpu > 0 ? t.lpu : default_lpu(a.m.type);
+    switch (a.m.type) {
+    case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, lpu, t.max_blocks, s);
+    case T_IQ3_S: return launch_lpu<T_IQ3_S>(a, lpu, t.max_blocks, s);
+    case T_Q4_K: return launch_lpu<T_Q4_K>(a, lpu, t.max_blocks, s);
+    case T_Q5_K: return launch_lpu<T_Q5_K>(a, lpu, t.max_blocks, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace lbh

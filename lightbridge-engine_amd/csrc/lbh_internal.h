@@ -25,11 +25,14 @@ struct MatView {
     int32_t rows;
     int32_t pad;
     long long units;   // rows * nb
+    long long bytes;   // size of the planes allocation
 };
 
 struct GemvArgs {
     MatView m;
-    const uint8_t *q8;            // (nb) Q8_K blocks
+    const uint8_t *q8;            // (nb) Q8_K blocks, or NULL when x is given
+    const float *x;               // f32 input quantized inside the kernel (q8 == NULL)
+    uint8_t *q8_out;              // optional: the Q8_K bytes of x, written by workgroup 0
     float *y;
     float coef;
     int32_t accumulate;
@@ -37,11 +40,72 @@ struct GemvArgs {
     const DevStatus *status;      // optional: skip when any validation word is set
 };
 
+// Launch-shape knobs of the matvec kernels (0 = built-in default).
+struct GemvTuning {
+    int lpu;          // lanes per (row, block) unit: 1, 2 or 4
+    int max_blocks;   // cap on workgroups of the persistent row loop
+};
+
+// ---------------------------------------------------------------- MoE block
+
+constexpr int MOE_MAX_ROUTED = 16;
+constexpr int MOE_SHARED_SLOT = MOE_MAX_ROUTED;   // scratch slot of the shared expert
+
+// Routing of one token: routed expert ids (ascending) and coefficients.
+struct MoeRoute {
+    int32_t n;
+    int32_t pad;
+    uint32_t ids[MOE_MAX_ROUTED];
+    float coefs[MOE_MAX_ROUTED];
+};
+
+struct ExpertDev {
+    MatView gate, up, down;
+};
+
+// Device status of one MoE call (~0 when clean).
+struct MoeStatus {
+    unsigned long long first_bad_swiglu;   // (expert order << 32) | lane; order n = shared
+    unsigned long long first_bad_fold;     // (accumulate step << 32) | row
+    unsigned long long first_bad_input;    // first non-finite input lane
+    unsigned long long pad;
+};
+
+struct MoeArgs {
+    const ExpertDev *experts;   // device table [n_experts]
+    ExpertDev shared;
+    int32_t has_shared;
+    int32_t hidden;             // input / output width
+    int32_t ffn_r, ffn_s;       // hidden widths of the routed / shared experts
+    MoeRoute route;             // routing, unless route_dev is set
+    const MoeRoute *route_dev;  // routing written by the device router
+    const float *x;             // [hidden]
+    float *h;                   // SwiGLU outputs: slot * h_stride
+    uint8_t *q8h;               // their Q8_K encodings: slot * q8_stride
+    uint32_t *counters;         // arrivals per (slot, 256-row block); self-resetting
+    int32_t h_stride, q8_stride, cnt_stride;
+    float *y;                   // [hidden]
+    MoeStatus *status;
+    int32_t tile_r, tile_s;     // gate/up rows per workgroup (routed, shared)
+    int32_t tiles_r, tiles_s;   // workgroups per routed expert / for the shared expert
+    int32_t tile_d;             // output rows per down workgroup
+    int32_t stop_step;          // combine steps 0..stop_step only (error fix-up); large = all
+    int32_t check;              // record non-finite SwiGLU lanes / accumulations
+    int32_t n_launch;           // routed experts covered by this launch
+    int32_t type_gate_r;        // GGML type of every routed gate/up matrix
+    int32_t type_down_r;        // GGML type of every routed down matrix
+};
+
+hipError_t launch_moe_gate_up(const MoeArgs &a, hipStream_t s);
+hipError_t launch_moe_down(const MoeArgs &a, hipStream_t s);
+hipError_t launch_moe_reset_status(MoeStatus *st, hipStream_t s);
+hipError_t launch_expf(const float *in, float *out, long long n, int swiglu, const float *up, hipStream_t s);
+
 hipError_t launch_quantize_q8k(const float *x, uint8_t *out, long long nblocks, const DevStatus *st,
                                hipStream_t s);
 hipError_t launch_find_nonfinite(const float *x, long long n, unsigned long long *first, hipStream_t s);
 hipError_t launch_reset_status(DevStatus *st, hipStream_t s);
-hipError_t launch_gemv(const GemvArgs &a, hipStream_t s);
+hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s);
 hipError_t launch_repack(int ty, const uint8_t *ggml, uint8_t *planes, long long units, int to_device,
                          hipStream_t s);
 hipError_t launch_validate_scales(int ty, const uint8_t *ggml, long long units,

@@ -83,6 +83,8 @@ def lib() -> C.CDLL:
             "lbh_ctx_destroy": ([p], i32),
             "lbh_ctx_set_stream": ([p, p], i32),
             "lbh_ctx_synchronize": ([p, E], i32),
+            "lbh_ctx_set_tuning": ([p, i32, i32], i32),
+            "lbh_ctx_cu_count": ([p], i32),
             "lbh_quantize_row_q8_k_into": ([p, p, sz, p, sz, E], i32),
             "lbh_quantize_q8_k_rows": ([p, p, sz, sz, p], i32),
             "lbh_matrix_create": ([p, i32, sz, sz, p, sz, i32, C.POINTER(p), E], i32),
@@ -95,8 +97,16 @@ def lib() -> C.CDLL:
             "lbh_gemv_into": ([p, p, p, sz, p, sz, p, sz, E], i32),
             "lbh_gemv_accumulate_scaled_into": ([p, p, p, sz, p, sz, C.c_float, p, sz, E], i32),
             "lbh_gemv_q8_k": ([p, p, p, p, C.c_float, i32], i32),
+            "lbh_gemv_f32": ([p, p, p, p, p, C.c_float, i32], i32),
             "lbh_gemv_block_sums": ([p, p, p, p], i32),
             "lbh_debug_f16_to_f32": ([p, p, p, sz, E], i32),
+            "lbh_moe_create": ([p, p, p, p, sz, p, p, p, C.POINTER(p), E], i32),
+            "lbh_moe_destroy": ([p], i32),
+            "lbh_moe_set_tiles": ([p, i32, i32, i32], i32),
+            "lbh_moe_routed_by_id_into": ([p, p, p, p, sz, p, sz, p, sz, E], i32),
+            "lbh_moe_forward": ([p, p, p, p, sz, p, p], i32),
+            "lbh_debug_expf": ([p, p, p, sz, i32, p, E], i32),
+            "lbh_debug_expf_host": ([p, p, sz, i32, p], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -151,6 +161,17 @@ class HipBackend:
         self._stream = stream
         lib().lbh_ctx_set_stream(self.ctx, C.c_void_p(stream.cuda_stream))
 
+    TUNE_GEMV_LPU, TUNE_GEMV_MAX_BLOCKS = 1, 2
+
+    def set_tuning(self, key: int, value: int) -> None:
+        """Launch-shape knob (lanes per unit, workgroup cap); 0 restores the default."""
+        st = lib().lbh_ctx_set_tuning(self.ctx, key, value)
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def cu_count(self) -> int:
+        return lib().lbh_ctx_cu_count(self.ctx)
+
     def simd_active(self) -> bool:
         return True
 
@@ -195,6 +216,13 @@ class HipBackend:
         if st:
             raise KernelError(LbhError(status=st))
 
+    def gemv_f32(self, m: "DeviceMatrix", x, y, q8_out=None, coef: float = 0.0, accumulate: bool = False) -> None:
+        """Quantize x to Q8_K inside the matvec kernel and compute y (= or +=)."""
+        q8p = _dev_ptr(q8_out) if q8_out is not None else None
+        st = lib().lbh_gemv_f32(self.ctx, m.handle, _dev_ptr(x), q8p, _dev_ptr(y), coef, 1 if accumulate else 0)
+        if st:
+            raise KernelError(LbhError(status=st))
+
     def block_sums(self, m: "DeviceMatrix", q8, out) -> None:
         st = lib().lbh_gemv_block_sums(self.ctx, m.handle, _dev_ptr(q8), _dev_ptr(out))
         if st:
@@ -202,6 +230,72 @@ class HipBackend:
 
     def f16_to_f32(self, src, dst) -> None:
         _call(lib().lbh_debug_f16_to_f32, self.ctx, _dev_ptr(src), _dev_ptr(dst), src.numel())
+
+    def expf(self, x, out, up=None) -> None:
+        """Device expf (or the SwiGLU element when `up` is given)."""
+        _call(lib().lbh_debug_expf, self.ctx, _dev_ptr(x), _dev_ptr(out), x.numel(), 1 if up is not None else 0,
+              _dev_ptr(up) if up is not None else None)
+
+    # -- MoE ------------------------------------------------------------------------
+    def moe_create(self, experts, shared=None) -> "MoeLayer":
+        """experts: list of (gate, up, down) DeviceMatrix; shared: the same triple or None."""
+        return MoeLayer(self, experts, shared)
+
+    def moe_routed_by_id_into(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
+        """moe_routed_by_id_into (crates/bridge-kernels-reference/src/moe.rs:64-147)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        coefs = np.ascontiguousarray(coefs, dtype=np.float32)
+        _call(lib().lbh_moe_routed_by_id_into, self.ctx, moe.handle, C.c_void_p(ids.ctypes.data),
+              C.c_void_p(coefs.ctypes.data), ids.size, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel())
+
+    def moe_forward(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
+        """Unchecked, asynchronous form (graph capturable)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        coefs = np.ascontiguousarray(coefs, dtype=np.float32)
+        st = lib().lbh_moe_forward(self.ctx, moe.handle, C.c_void_p(ids.ctypes.data), C.c_void_p(coefs.ctypes.data),
+                                   ids.size, _dev_ptr(x), _dev_ptr(y))
+        if st:
+            raise KernelError(LbhError(status=st))
+
+
+def expf_host(x: np.ndarray, up: np.ndarray | None = None) -> np.ndarray:
+    """The device expf / SwiGLU arithmetic compiled for the host CPU."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    u = np.ascontiguousarray(up, dtype=np.float32) if up is not None else None
+    lib().lbh_debug_expf_host(C.c_void_p(x.ctypes.data), C.c_void_p(out.ctypes.data), x.size,
+                              1 if u is not None else 0, C.c_void_p(u.ctypes.data) if u is not None else None)
+    return out
+
+
+class MoeLayer:
+    """A resident routed + shared SwiGLU MoE layer (moe.rs:17-21 RoutedMoeSelection)."""
+
+    def __init__(self, be: HipBackend, experts, shared=None):
+        n = len(experts)
+        arr = [(C.c_void_p * n)(*[e[i].handle for e in experts]) for i in range(3)]
+        sh = [shared[i].handle if shared is not None else None for i in range(3)]
+        h = C.c_void_p()
+        _call(lib().lbh_moe_create, be.ctx, arr[0], arr[1], arr[2], n, sh[0], sh[1], sh[2], C.byref(h))
+        self.be, self.handle = be, h
+        self._keep = (experts, shared)
+        self.n_experts = n
+
+    def set_tiles(self, tile_r: int = 32, tile_s: int = 32, tile_d: int = 16) -> None:
+        st = lib().lbh_moe_set_tiles(self.handle, tile_r, tile_s, tile_d)
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().lbh_moe_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class DeviceMatrix:

@@ -86,6 +86,10 @@ static inline float rd_f32(const uint8_t *p) { return bits_f32(rd_u32(p)); }
 
 float lbo_expf(float x) { return expf(x); }
 
+void lbo_expf_array(const float *x, float *out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = expf(x[i]);
+}
+
 size_t lbo_block_bytes(int ty) {
     switch (ty) {
     case LBO_F32: return 4;
@@ -776,13 +780,17 @@ int lbo_gemv_accumulate(const lbo_exec *ex, const lbo_matrix *m, const float *in
 
 /* --------------------------------------------------------------- SwiGLU */
 
+/* apply_swiglu (activation.rs:170-178).  On a non-finite product the
+ * reference returns NonFiniteValue carrying that product's bits
+ * (validate_finite_value, gemv.rs); it is left in gate[i] so the caller can
+ * report them (the reference's scratch is not observable otherwise). */
 int64_t lbo_apply_swiglu(float *gate, const float *up, size_t n) {
     for (size_t i = 0; i < n; ++i) {
         float g = gate[i];
         float act = g / (1.0f + expf(-g));
         float v = act * up[i];
-        if (!f32_finite(v)) return (int64_t)i;
         gate[i] = v;
+        if (!f32_finite(v)) return (int64_t)i;
     }
     return -1;
 }

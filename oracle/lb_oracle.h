@@ -160,6 +160,7 @@ float lbo_f16_to_f32(uint16_t h);
 
 /* glibc expf as the reference's f32::exp links it (exposed for the GPU expf check). */
 float lbo_expf(float x);
+void lbo_expf_array(const float *x, float *out, size_t n);
 
 #ifdef __cplusplus
 }

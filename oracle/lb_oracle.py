@@ -93,6 +93,8 @@ def lib():
         L.lbo_f16_to_f32.restype = C.c_float
         L.lbo_expf.argtypes = [C.c_float]
         L.lbo_expf.restype = C.c_float
+        L.lbo_expf_array.argtypes = [p, p, C.c_size_t]
+        L.lbo_expf_array.restype = None
         _lib = L
     return _lib
 
@@ -204,6 +206,21 @@ def moe_routed_by_id(ex: LboExec, ids, coefs, experts: list, shared: LboExpert, 
     return out
 
 
+def moe_routed_by_id_status(ex: LboExec, ids, coefs, experts: list, shared: LboExpert, x: np.ndarray,
+                            out: np.ndarray, preflight: bool = True) -> LboError:
+    """As moe_routed_by_id, but returns the error record and leaves `out` as the
+    reference leaves its output (unchanged, or partially accumulated)."""
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    coefs = np.ascontiguousarray(coefs, dtype=np.float32)
+    arr = (LboExpert * len(experts))(*experts)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert out.dtype == np.float32 and out.flags.c_contiguous
+    err = LboError()
+    lib().lbo_moe_routed_by_id(C.byref(ex), _ptr(ids), _ptr(coefs), ids.size, arr, len(experts), C.byref(shared),
+                               _ptr(x), _ptr(out), 1 if preflight else 0, C.byref(err))
+    return err
+
+
 def route_sigmoid_bias(logits, bias, top_k: int, weight_scale: float):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     bias = np.ascontiguousarray(bias, dtype=np.float32)
@@ -241,6 +258,14 @@ def apply_swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     if bad >= 0:
         raise OracleError(LboError(22, 0, bad, 0, 0, 0, 5))
     return g
+
+
+def expf_array(x: np.ndarray) -> np.ndarray:
+    """The host C library's expf (what the reference's f32::exp links) over an array."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().lbo_expf_array(_ptr(x), _ptr(out), x.size)
+    return out
 
 
 def default_threads() -> int:

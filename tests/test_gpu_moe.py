@@ -1,0 +1,242 @@
+"""GPU parity of the MoE expert FFN block (lbh_moe_*) against the CPU oracle.
+
+The oracle restates moe_routed_by_id_into (crates/bridge-kernels-reference/
+src/moe.rs:64-147) with the reference's per-expert SwiGLU (activation.rs) and
+the host C library's expf.  Outputs are compared bit for bit; error cases
+compare the variant, index and bits and the output buffer afterwards
+(unchanged, or the reference's partial accumulation).
+"""
+import numpy as np
+import pytest
+
+from lbhip import synth
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+Q4_K, Q5_K, IQ3_S, IQ2_S = 12, 13, 21, 22
+
+
+@pytest.fixture(scope="module")
+def be():
+    import lbhip
+    if not torch.cuda.is_available():
+        pytest.fail("no GPU visible")
+    b = lbhip.HipBackend(0)
+    yield b
+    b.close()
+
+
+def dev(a):
+    return torch.from_numpy(np.array(a, copy=True)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+class Layer:
+    """One MoE layer uploaded to the GPU and described to the oracle."""
+
+    def __init__(self, be, oracle, n_experts, hidden, ffn_r, ffn_s, types, seed, scale=None):
+        gr, dr, gs, ds = types
+        self.hidden = hidden
+        self.np = []
+        dev_exp, orc_exp = [], []
+        for e in range(n_experts):
+            g = synth.random_matrix(gr, ffn_r, hidden, seed + 7 * e)
+            u = synth.random_matrix(gr, ffn_r, hidden, seed + 7 * e + 1)
+            d = synth.random_matrix(dr, hidden, ffn_r, seed + 7 * e + 2)
+            if scale is not None:
+                scale(e, g, u, d)
+            self.np.append((g, u, d))
+            dev_exp.append((be.upload(gr, ffn_r, hidden, g), be.upload(gr, ffn_r, hidden, u),
+                            be.upload(dr, hidden, ffn_r, d)))
+            orc_exp.append(oracle.make_expert(oracle.make_matrix(gr, ffn_r, hidden, g),
+                                              oracle.make_matrix(gr, ffn_r, hidden, u),
+                                              oracle.make_matrix(dr, hidden, ffn_r, d)))
+        sg = synth.random_matrix(gs, ffn_s, hidden, seed + 1001)
+        su = synth.random_matrix(gs, ffn_s, hidden, seed + 1002)
+        sd = synth.random_matrix(ds, hidden, ffn_s, seed + 1003)
+        self.shared_np = (sg, su, sd)
+        dev_sh = (be.upload(gs, ffn_s, hidden, sg), be.upload(gs, ffn_s, hidden, su), be.upload(ds, hidden, ffn_s, sd))
+        self.orc_shared = oracle.make_expert(oracle.make_matrix(gs, ffn_s, hidden, sg),
+                                             oracle.make_matrix(gs, ffn_s, hidden, su),
+                                             oracle.make_matrix(ds, hidden, ffn_s, sd))
+        self.orc_experts = orc_exp
+        self.moe = be.moe_create(dev_exp, dev_sh)
+        self._keep = (dev_exp, dev_sh)
+
+    def oracle_out(self, oracle, ids, coefs, x, sentinel=None):
+        out = np.full(self.hidden, np.nan, np.float32) if sentinel is None else sentinel.copy()
+        ex = oracle.make_exec(oracle.MODE_CPU_PARALLEL_Q8K, 8, True)
+        err = oracle.moe_routed_by_id_status(ex, ids, coefs, self.orc_experts, self.orc_shared, x, out)
+        return out, err
+
+
+def _run(be, layer, ids, coefs, x, sentinel=None):
+    y = dev(np.full(layer.hidden, np.nan, np.float32) if sentinel is None else sentinel)
+    import lbhip
+    try:
+        be.moe_routed_by_id_into(layer.moe, ids, coefs, dev(x), y)
+        e = None
+    except lbhip.BackendError as ex:
+        e = ex
+    return host(y), e
+
+
+def _same(a, b):
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def small(be, oracle):
+    return Layer(be, oracle, 6, 512, 256, 512, (IQ2_S, IQ3_S, Q4_K, Q5_K), seed=11)
+
+
+@pytest.fixture(scope="module")
+def config3(be, oracle):
+    # BASELINE configs[2] shapes with 16 experts (the per-token work of top-8 is the same).
+    return Layer(be, oracle, 16, 4096, 1536, 4096, (IQ2_S, IQ3_S, Q4_K, Q5_K), seed=23)
+
+
+def test_device_expf_matches_libm(be, oracle):
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0, 1 << 32, size=1 << 24, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32).copy()
+    x[:4] = [float.fromhex("0x1.04845ep+5"), float.fromhex("-0x1.f8cbb2p+5"), 88.72283, -103.97208]
+    x[4:4 + 200000] = np.linspace(-110, 95, 200000, dtype=np.float32)
+    want = oracle.expf_array(x)
+    out = torch.empty(x.size, dtype=torch.float32, device="cuda")
+    be.expf(dev(x), out)
+    got = host(out)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert _same(got[~nan], want[~nan])
+
+
+@pytest.mark.parametrize("ids", [[0, 2, 5], [4], [0, 1, 2, 3, 4, 5]])
+def test_moe_small_bit_exact(be, oracle, small, ids):
+    rng = np.random.default_rng(len(ids))
+    coefs = rng.random(len(ids)).astype(np.float32)
+    x = rng.standard_normal(512).astype(np.float32)
+    want, err = small.oracle_out(oracle, ids, coefs, x)
+    assert err.status == 0
+    got, e = _run(be, small, ids, coefs, x)
+    assert e is None and _same(got, want)
+
+
+def test_moe_config3_shapes_bit_exact_and_repeatable(be, oracle, config3):
+    rng = np.random.default_rng(9)
+    for call in range(3):   # arrival counters must reset between calls
+        logits = rng.standard_normal(16).astype(np.float32)
+        ids, coefs = oracle.route_softmax_topk(logits, 8)
+        x = rng.standard_normal(4096).astype(np.float32)
+        want, err = config3.oracle_out(oracle, ids, coefs, x)
+        assert err.status == 0
+        got, e = _run(be, config3, ids, coefs, x)
+        assert e is None and _same(got, want), f"call {call}"
+        # the unchecked asynchronous form computes the same bits
+        y = dev(np.zeros(4096, np.float32))
+        config3.moe.be.moe_forward(config3.moe, ids, coefs, dev(x), y)
+        assert _same(host(y), want)
+
+
+@pytest.mark.parametrize("tiles", [(16, 16, 1), (64, 128, 7), (256, 256, 256), (32, 32, 20)])
+def test_moe_launch_shapes_give_the_same_bits(be, oracle, config3, tiles):
+    rng = np.random.default_rng(sum(tiles))
+    ids = np.sort(rng.choice(16, size=8, replace=False)).astype(np.uint32)
+    coefs = rng.random(8).astype(np.float32)
+    x = rng.standard_normal(4096).astype(np.float32)
+    want, _ = config3.oracle_out(oracle, ids, coefs, x)
+    config3.moe.set_tiles(*tiles)
+    try:
+        got, e = _run(be, config3, ids, coefs, x)
+    finally:
+        config3.moe.set_tiles(32, 32, 16)
+    assert e is None and _same(got, want)
+
+
+def test_moe_real_hy3_types(be, oracle):
+    """Hy3's own shared expert is IQ2_S/IQ3_S with ffn 1536 (profile.rs, schema.rs)."""
+    layer = Layer(be, oracle, 4, 1024, 512, 512, (IQ2_S, IQ3_S, IQ2_S, IQ3_S), seed=31)
+    ids, coefs = np.array([1, 3], np.uint32), np.array([0.7, 0.3], np.float32)
+    x = np.random.default_rng(1).standard_normal(1024).astype(np.float32)
+    want, _ = layer.oracle_out(oracle, ids, coefs, x)
+    got, e = _run(be, layer, ids, coefs, x)
+    assert e is None and _same(got, want)
+    layer2 = Layer(be, oracle, 3, 512, 256, 256, (IQ2_S, IQ2_S, IQ2_S, IQ2_S), seed=32)
+    want, _ = layer2.oracle_out(oracle, [0, 2], [0.5, 0.25], x[:512])
+    got, e = _run(be, layer2, [0, 2], np.array([0.5, 0.25], np.float32), x[:512])
+    assert e is None and _same(got, want)
+
+
+ERROR_CASES = {
+    "empty": ([], []),
+    "duplicate": ([1, 1], [0.5, 0.5]),
+    "order": ([3, 1], [0.5, 0.5]),
+    "bad_id": ([2, 9], [0.5, 0.5]),
+    "nan_coef_first": ([0, 1], [np.nan, 0.5]),
+    "inf_coef_later": ([0, 1, 4], [0.5, 0.25, np.inf]),
+}
+
+
+@pytest.mark.parametrize("case", sorted(ERROR_CASES))
+def test_moe_routing_errors_match_and_leave_output_unchanged(be, oracle, small, case):
+    ids, coefs = ERROR_CASES[case]
+    ids, coefs = np.array(ids, np.uint32), np.array(coefs, np.float32)
+    x = np.random.default_rng(2).standard_normal(512).astype(np.float32)
+    sentinel = np.arange(512, dtype=np.float32) * np.float32(0.25) - 7
+    want, err = small.oracle_out(oracle, ids, coefs, x, sentinel)
+    got, e = _run(be, small, ids, coefs, x, sentinel)
+    assert err.status != 0 and e is not None
+    assert e.code == err.status and e.index == err.index and e.bits == err.bits, (e, err.status, err.index)
+    assert _same(got, want) and _same(got, sentinel)
+
+
+def test_moe_nonfinite_input_is_rejected(be, oracle, small):
+    x = np.random.default_rng(4).standard_normal(512).astype(np.float32)
+    x[77] = np.inf
+    sentinel = np.full(512, 3.5, np.float32)
+    want, err = small.oracle_out(oracle, [1, 2], np.array([0.5, 0.5], np.float32), x, sentinel)
+    got, e = _run(be, small, [1, 2], np.array([0.5, 0.5], np.float32), x, sentinel)
+    assert e.variant == "NonFiniteValue" and e.index == err.index == 77 and e.bits == err.bits
+    assert _same(got, sentinel)
+
+
+def test_moe_swiglu_overflow_is_reported_at_the_reference_lane(be, oracle):
+    # Expert 2's gate/up rows from 40 on get the largest f16 scale on every
+    # block: with |x| ~ 1e15 their SwiGLU product overflows, the other experts'
+    # stays finite (~1e29).
+    def scale(e, g, u, d):
+        if e == 2:
+            for m in (g, u):
+                blocks = m.reshape(m.shape[0], -1, 82)
+                blocks[40:, :, 0:2] = np.array([0x7BFF], np.uint16).view(np.uint8)
+    layer = Layer(be, oracle, 4, 512, 256, 256, (IQ2_S, IQ3_S, IQ2_S, IQ3_S), seed=41, scale=scale)
+    x = (np.random.default_rng(6).standard_normal(512) * 1e15).astype(np.float32)
+    sentinel = np.full(512, -1.25, np.float32)
+    outcomes = []
+    for ids in ([0, 2, 3], [2], [0, 1]):
+        coefs = np.full(len(ids), 0.5, np.float32)
+        want, err = layer.oracle_out(oracle, ids, coefs, x, sentinel)
+        outcomes.append(err.status)
+        got, e = _run(be, layer, ids, coefs, x, sentinel)
+        if err.status == 0:
+            assert e is None and _same(got, want)
+        else:
+            assert e is not None and (e.code, e.index, e.bits) == (err.status, err.index, err.bits)
+            assert _same(got, want)
+    assert outcomes[0] != 0 and outcomes[1] != 0 and outcomes[2] == 0, outcomes
+
+
+def test_moe_accumulation_overflow_keeps_the_reference_partial_output(be, oracle, small):
+    x = np.random.default_rng(8).standard_normal(512).astype(np.float32)
+    ids = np.array([0, 3, 5], np.uint32)
+    coefs = np.array([3e38, 3e38, 0.5], np.float32)
+    sentinel = np.zeros(512, np.float32)
+    want, err = small.oracle_out(oracle, ids, coefs, x, sentinel)
+    got, e = _run(be, small, ids, coefs, x, sentinel)
+    assert err.status != 0, "the case must overflow"
+    assert e is not None and (e.code, e.index, e.bits) == (err.status, err.index, err.bits)
+    assert _same(got, want)

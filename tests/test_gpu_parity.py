@@ -224,3 +224,46 @@ def test_upload_shape_errors(be):
         be.upload(Q4_K, 2, 256, np.zeros(143, np.uint8))
     with pytest.raises(lbhip.QuantError, match="LogicalElementsNotDivisible"):
         be.upload(Q4_K, 2, 100, np.zeros(144, np.uint8))
+
+
+@pytest.mark.parametrize("lpu", [1, 2, 4])
+@pytest.mark.parametrize("ty,rows,k", [(Q4_K, 300, 4096), (Q5_K, 97, 2048), (IQ2_S, 515, 4096),
+                                       (IQ3_S, 1029, 1536), (IQ2_S, 33, 256), (Q5_K, 17, 16384)])
+def test_gemv_every_lanes_per_unit_and_persistent_loop(be, oracle, lpu, ty, rows, k):
+    """Every launch shape gives the same bits: lanes per unit 1/2/4, and a
+    workgroup cap of 3 so each wave walks many rows of the persistent loop."""
+    try:
+        for cap in (0, 3):
+            be.set_tuning(be.TUNE_GEMV_LPU, lpu)
+            be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
+            _check_gemv(be, oracle, ty, rows, k, seed=rows + lpu + cap)
+    finally:
+        be.set_tuning(be.TUNE_GEMV_LPU, 0)
+        be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, 0)
+
+
+@pytest.mark.parametrize("ty,rows,k", [(Q4_K, 4096, 4096), (IQ2_S, 1536, 4096), (IQ3_S, 4096, 1536),
+                                       (Q5_K, 333, 768)])
+def test_fused_quantize_gemv_matches_quantize_then_dot(be, oracle, ty, rows, k):
+    """lbh_gemv_f32 quantizes inside the matvec kernel: its published Q8_K bytes
+    and its outputs equal quantize_row_q8_k_into followed by the row dots."""
+    w = synth.random_matrix(ty, rows, k, 77 + ty)
+    x = synth.random_activations(k, 78 + ty)
+    x[:256] *= 1e-3                       # a block with a different scale
+    q8_ref = oracle.quantize_q8_k(x)
+    om = oracle.make_matrix(ty, rows, k, w)
+    ex = oracle.make_exec(oracle.MODE_CPU_PARALLEL_Q8K, 8, True)
+    want = oracle.gemv_prequantized(ex, om, q8_ref)
+    m = be.upload(ty, rows, k, w)
+    y = torch.full((rows,), float("nan"), device="cuda")
+    q8 = torch.zeros(q8_ref.size, dtype=torch.uint8, device="cuda")
+    be.gemv_f32(m, dev(x), y, q8)
+    assert np.array_equal(host(q8), q8_ref)
+    assert np.array_equal(host(y).view(np.uint32), want.view(np.uint32))
+    # accumulate form: dest += coef * dot, the order of gemv_accumulate_scaled_into
+    dest0 = synth.random_activations(rows, 79)
+    want_acc = dest0.copy()
+    oracle.gemv_accumulate(ex, om, x, want_acc, -0.75)
+    d = dev(dest0)
+    be.gemv_f32(m, dev(x), d, None, coef=-0.75, accumulate=True)
+    assert np.array_equal(host(d).view(np.uint32), want_acc.view(np.uint32))
