@@ -79,6 +79,7 @@ typedef struct lbh_error {
 typedef struct lbh_ctx lbh_ctx;
 typedef struct lbh_matrix lbh_matrix;
 typedef struct lbh_moe lbh_moe;
+typedef struct lbh_router lbh_router;
 
 /* Q8_K ABI constants (crates/bridge-quant-layout/src/q8_k.rs:7-12). */
 #define LBH_Q8_K_BLOCK_ELEMENTS 256
@@ -208,6 +209,31 @@ lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *moe, const uint32_t 
  * coefs and x finite. */
 lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, const float *coefs, size_t n_routed,
                            const float *x_dev, float *y_dev);
+
+/* ---- router -------------------------------------------------------------------
+ * F32 router [hidden, n_experts] (GGML; n_experts rows of `hidden` floats) resident
+ * in HBM, n_experts <= 256.  bias (optional) is the selection bias exp_probs_b. */
+
+/* [sync] `weights`/`bias` are host memory when on_device == 0, device memory otherwise. */
+lbh_status lbh_router_create(lbh_ctx *ctx, const float *weights, size_t n_experts, size_t hidden, const float *bias,
+                             int32_t on_device, lbh_router **out, lbh_error *err);
+lbh_status lbh_router_destroy(lbh_router *router);
+
+/* [sync] Router logits (gemv_into of the F32 router, gemv.rs:286-303: bit-identical
+ * sequential sums) and top_k selection into host ids/coefs (ascending ids):
+ *   mode 0: softmax over the top k by (logit desc, id asc), renormalised (the
+ *           benchmark configuration; no reference counterpart);
+ *   mode 1: route_experts_into (crates/bridge-model-hy3/src/routing.rs:25-107).
+ * logits_host (optional) receives the n_experts logits. */
+lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *router, const float *x_dev, size_t x_len, size_t top_k,
+                                 int32_t mode, float weight_scale, uint32_t *ids, float *coefs, float *logits_host,
+                                 lbh_error *err);
+
+/* [async] One MoE block decode step entirely on the device: router + top-k, then the
+ * routed and shared experts (lbh_moe_forward semantics) reading the device routing.
+ * Unchecked: x must be finite. */
+lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev, size_t top_k,
+                                 int32_t mode, float weight_scale, float *y_dev);
 
 /* ---- diagnostics ------------------------------------------------------------- */
 

@@ -730,3 +730,174 @@ void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, 
 }
 
 }  // extern "C"
+
+// ================================================================== router
+
+struct lbh_router {
+    int device;
+    size_t n_experts, hidden;
+    float *w;            // [n_experts][hidden]
+    float *bias;         // [n_experts] or NULL
+    float *logits;
+    uint32_t *counter;
+    MoeRoute *route;     // device
+    MoeRoute *route_host;
+    unsigned long long *status;
+    unsigned long long *status_host;
+    int epw;
+};
+
+namespace {
+
+void free_router(lbh_router *r) {
+    if (!r) return;
+    DeviceGuard g(r->device);
+    if (r->w) (void)hipFree(r->w);
+    if (r->bias) (void)hipFree(r->bias);
+    if (r->logits) (void)hipFree(r->logits);
+    if (r->counter) (void)hipFree(r->counter);
+    if (r->route) (void)hipFree(r->route);
+    if (r->status) (void)hipFree(r->status);
+    if (r->route_host) (void)hipHostFree(r->route_host);
+    if (r->status_host) (void)hipHostFree(r->status_host);
+    delete r;
+}
+
+RouterArgs router_args(const lbh_router *r, const float *x, size_t top_k, int32_t mode, float scale) {
+    RouterArgs a{};
+    a.w = r->w;
+    a.bias = r->bias;
+    a.x = x;
+    a.logits = r->logits;
+    a.counter = r->counter;
+    a.route = r->route;
+    a.n_experts = (int32_t)r->n_experts;
+    a.hidden = (int32_t)r->hidden;
+    a.top_k = (int32_t)top_k;
+    a.mode = mode;
+    a.weight_scale = scale;
+    a.epw = r->epw;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+lbh_status lbh_router_create(lbh_ctx *ctx, const float *weights, size_t n_experts, size_t hidden, const float *bias,
+                             int32_t on_device, lbh_router **out, lbh_error *err) {
+    if (!ctx || !weights || !out) return fail(err, LBH_NULL_ARGUMENT);
+    *out = nullptr;
+    if (n_experts == 0 || n_experts > 256) return fail(err, LBH_UNSUPPORTED_SHAPE, LBH_F32, 0, 256, n_experts);
+    if (hidden == 0 || hidden % 256) return fail(err, LBH_DIMENSION_MISMATCH, LBH_F32, 0, 256, hidden);
+    DeviceGuard g(ctx->device);
+    lbh_router *r = new (std::nothrow) lbh_router();
+    if (!r) return fail(err, LBH_HIP_ERROR);
+    r->device = ctx->device;
+    r->n_experts = n_experts;
+    r->hidden = hidden;
+    r->epw = 2;
+    const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    hipError_t e = hipMalloc(&r->w, n_experts * hidden * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(r->w, weights, n_experts * hidden * sizeof(float), kind);
+    if (e == hipSuccess && bias) {
+        e = hipMalloc(&r->bias, n_experts * sizeof(float));
+        if (e == hipSuccess) e = hipMemcpy(r->bias, bias, n_experts * sizeof(float), kind);
+    }
+    if (e == hipSuccess) e = hipMalloc(&r->logits, n_experts * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&r->counter, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(r->counter, 0, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&r->route, sizeof(MoeRoute));
+    if (e == hipSuccess) e = hipMemset(r->route, 0, sizeof(MoeRoute));
+    if (e == hipSuccess) e = hipMalloc(&r->status, 2 * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipHostMalloc(&r->route_host, sizeof(MoeRoute), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc(&r->status_host, 2 * sizeof(unsigned long long), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_router(r);
+        return hip_fail(err, e);
+    }
+    *out = r;
+    return ok(err);
+}
+
+lbh_status lbh_router_destroy(lbh_router *r) {
+    if (!r) return LBH_NULL_ARGUMENT;
+    free_router(r);
+    return LBH_OK;
+}
+
+lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, size_t x_len, size_t top_k, int32_t mode,
+                                 float weight_scale, uint32_t *ids, float *coefs, float *logits_host, lbh_error *err) {
+    if (!ctx || !r || !x || !ids || !coefs) return fail(err, LBH_NULL_ARGUMENT);
+    if (x_len != r->hidden) return fail(err, LBH_DIMENSION_MISMATCH, LBH_F32, 0, r->hidden, x_len);
+    if (mode != 0 && mode != 1) return fail(err, LBH_INVALID_PARAMETER, 0, (uint64_t)mode);
+    if (mode == 1 && !r->bias) return fail(err, LBH_NULL_ARGUMENT);
+    // route_experts_into (routing.rs:48-71): top-k range, then weight_scale.
+    if (top_k == 0 || top_k > r->n_experts) return fail(err, LBH_INVALID_PARAMETER, 0, top_k, r->n_experts, top_k);
+    if (top_k > MOE_MAX_ROUTED) return fail(err, LBH_UNSUPPORTED_SHAPE, 0, top_k, MOE_MAX_ROUTED, top_k);
+    uint32_t sbits;
+    std::memcpy(&sbits, &weight_scale, 4);
+    if (mode == 1 && (sbits & 0x7f800000u) == 0x7f800000u) return fail(err, LBH_NON_FINITE_VALUE, 0, 0, 0, 0, sbits, 7);
+    DeviceGuard g(ctx->device);
+    RouterArgs a = router_args(r, x, top_k, mode, weight_scale);
+    a.status = r->status;
+    // The router matvec is gemv_into on an F32 matrix: its input must be finite (gemv.rs:195-211).
+    HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+    HIP_TRY(launch_find_nonfinite(x, (long long)x_len, &ctx->status->first_bad_input, ctx->stream));
+    HIP_TRY(hipMemsetAsync(r->status, 0xff, sizeof(unsigned long long), ctx->stream));
+    HIP_TRY(launch_router(a, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(r->status_host, r->status, sizeof(unsigned long long), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(r->route_host, r->route, sizeof(MoeRoute), hipMemcpyDeviceToHost, ctx->stream));
+    lbh_status st = read_status(ctx, err);
+    if (st) return st;
+    if (ctx->status_host->first_bad_input != ~0ull) {
+        const unsigned long long i = ctx->status_host->first_bad_input;
+        return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, i, 0, 0, read_f32_bits(ctx, x + i), 0);
+    }
+    const unsigned long long bad = r->status_host[0];
+    if (bad != ~0ull) {
+        const uint64_t e = bad >> 2;
+        const uint32_t field = (uint32_t)(bad & 3);   // 0 logit, 1 bias, 2 score
+        float v = 0.0f;
+        if (field == 0) {
+            uint32_t b = read_f32_bits(ctx, r->logits + e);
+            std::memcpy(&v, &b, 4);
+        } else {
+            uint32_t lb = read_f32_bits(ctx, r->logits + e), bb = read_f32_bits(ctx, r->bias + e);
+            float l, bv;
+            std::memcpy(&l, &lb, 4);
+            std::memcpy(&bv, &bb, 4);
+            v = field == 1 ? bv : 1.0f / (1.0f + expf_libm(-l)) + bv;
+        }
+        uint32_t vb;
+        std::memcpy(&vb, &v, 4);
+        return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, e, 0, 0, vb, 8 + field);
+    }
+    for (size_t i = 0; i < top_k; ++i) {
+        ids[i] = r->route_host->ids[i];
+        coefs[i] = r->route_host->coefs[i];
+    }
+    if (logits_host) HIP_TRY(hipMemcpy(logits_host, r->logits, r->n_experts * sizeof(float), hipMemcpyDeviceToHost));
+    return ok(err);
+}
+
+lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const float *x, size_t top_k, int32_t mode,
+                                 float weight_scale, float *y) {
+    if (!ctx || !m || !r || !x || !y) return LBH_NULL_ARGUMENT;
+    if (r->n_experts != m->n_experts || r->hidden != m->hidden) return LBH_DIMENSION_MISMATCH;
+    if (top_k == 0 || top_k > r->n_experts || top_k > MOE_MAX_ROUTED) return LBH_INVALID_PARAMETER;
+    if (mode != 0 && (mode != 1 || !r->bias)) return LBH_INVALID_PARAMETER;
+    DeviceGuard g(ctx->device);
+    RouterArgs ra = router_args(r, x, top_k, mode, weight_scale);
+    if (launch_router(ra, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    MoeArgs a = moe_args(m, x, y);
+    a.route_dev = r->route;
+    a.route.n = (int32_t)top_k;
+    a.n_launch = (int32_t)top_k;
+    if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    return LBH_OK;
+}
+
+}  // extern "C"

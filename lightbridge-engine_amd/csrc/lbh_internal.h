@@ -96,6 +96,20 @@ struct MoeArgs {
     int32_t type_down_r;        // GGML type of every routed down matrix
 };
 
+struct RouterArgs {
+    const float *w;             // [n_experts][hidden] f32 rows (GGML F32 [hidden, n_experts])
+    const float *bias;          // selection bias [n_experts] (mode 1)
+    const float *x;             // [hidden]
+    float *logits;              // [n_experts]
+    uint32_t *counter;          // arrivals; self-resetting
+    MoeRoute *route;            // output
+    unsigned long long *status; // optional: (first bad expert << 2) | field
+    int32_t n_experts, hidden, top_k, mode;
+    float weight_scale;
+    int32_t epw;                // experts per workgroup
+};
+
+hipError_t launch_router(const RouterArgs &a, hipStream_t s);
 hipError_t launch_moe_gate_up(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_down(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_reset_status(MoeStatus *st, hipStream_t s);

@@ -107,6 +107,10 @@ def lib() -> C.CDLL:
             "lbh_moe_forward": ([p, p, p, p, sz, p, p], i32),
             "lbh_debug_expf": ([p, p, p, sz, i32, p, E], i32),
             "lbh_debug_expf_host": ([p, p, sz, i32, p], None),
+            "lbh_router_create": ([p, p, sz, sz, p, i32, C.POINTER(p), E], i32),
+            "lbh_router_destroy": ([p], i32),
+            "lbh_router_route_into": ([p, p, p, sz, sz, i32, C.c_float, p, p, p, E], i32),
+            "lbh_moe_block_forward": ([p, p, p, p, sz, i32, C.c_float, p], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -256,6 +260,52 @@ class HipBackend:
                                    ids.size, _dev_ptr(x), _dev_ptr(y))
         if st:
             raise KernelError(LbhError(status=st))
+
+
+class Router:
+    """The F32 MoE router resident in HBM: weights [n_experts][hidden] (GGML F32
+    [hidden, n_experts]) and an optional selection bias (routing.rs:25-107)."""
+
+    SOFTMAX, SIGMOID_BIAS = 0, 1
+
+    def __init__(self, be: HipBackend, weights: np.ndarray, bias: np.ndarray | None = None):
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        b = np.ascontiguousarray(bias, dtype=np.float32) if bias is not None else None
+        self.be, self.n_experts, self.hidden = be, w.shape[0], w.shape[1]
+        h = C.c_void_p()
+        _call(lib().lbh_router_create, be.ctx, C.c_void_p(w.ctypes.data), self.n_experts, self.hidden,
+              C.c_void_p(b.ctypes.data) if b is not None else None, 0, C.byref(h))
+        self.handle = h
+
+    def route_into(self, x, top_k: int, mode: int = 0, weight_scale: float = 1.0, want_logits: bool = False):
+        """Host (ids, coefs[, logits]) of one token; ids ascending."""
+        ids = np.zeros(top_k, np.uint32)
+        coefs = np.zeros(top_k, np.float32)
+        logits = np.zeros(self.n_experts, np.float32) if want_logits else None
+        _call(lib().lbh_router_route_into, self.be.ctx, self.handle, _dev_ptr(x), x.numel(), top_k, mode,
+              weight_scale, C.c_void_p(ids.ctypes.data), C.c_void_p(coefs.ctypes.data),
+              C.c_void_p(logits.ctypes.data) if logits is not None else None)
+        return (ids, coefs, logits) if want_logits else (ids, coefs)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().lbh_router_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def moe_block_forward(be: HipBackend, moe: "MoeLayer", router: Router, x, y, top_k: int, mode: int = 0,
+                      weight_scale: float = 1.0) -> None:
+    """Device router + top-k + MoE experts of one token (asynchronous, unchecked)."""
+    st = lib().lbh_moe_block_forward(be.ctx, moe.handle, router.handle, _dev_ptr(x), top_k, mode, weight_scale,
+                                     _dev_ptr(y))
+    if st:
+        raise KernelError(LbhError(status=st))
 
 
 def expf_host(x: np.ndarray, up: np.ndarray | None = None) -> np.ndarray:

@@ -240,3 +240,80 @@ def test_moe_accumulation_overflow_keeps_the_reference_partial_output(be, oracle
     assert err.status != 0, "the case must overflow"
     assert e is not None and (e.code, e.index, e.bits) == (err.status, err.index, err.bits)
     assert _same(got, want)
+
+
+# ------------------------------------------------------------------ router
+
+def _router(be, n_experts, hidden, seed, bias=False):
+    import lbhip
+    w = synth.router_weights(n_experts, hidden, seed)
+    b = (np.random.default_rng(seed + 1).standard_normal(n_experts) * 0.05).astype(np.float32) if bias else None
+    return lbhip.Router(be, w, b), w, b
+
+
+@pytest.mark.parametrize("n_experts,hidden,top_k", [(192, 4096, 8), (16, 4096, 8), (7, 256, 3), (256, 1536, 16)])
+def test_router_logits_and_softmax_route_bit_exact(be, oracle, n_experts, hidden, top_k):
+    r, w, _ = _router(be, n_experts, hidden, seed=n_experts)
+    rng = np.random.default_rng(hidden)
+    for _ in range(3):
+        x = rng.standard_normal(hidden).astype(np.float32)
+        ids, coefs, logits = r.route_into(dev(x), top_k, want_logits=True)
+        want_logits = oracle.router_logits_f32(w, x)
+        assert _same(logits, want_logits)
+        wid, wco = oracle.route_softmax_topk(want_logits, top_k)
+        assert np.array_equal(ids, wid) and _same(coefs, wco)
+
+
+def test_router_sigmoid_bias_matches_route_experts_into(be, oracle):
+    r, w, b = _router(be, 192, 4096, seed=5, bias=True)
+    x = np.random.default_rng(4).standard_normal(4096).astype(np.float32)
+    ids, coefs = r.route_into(dev(x), 8, mode=1, weight_scale=2.826)
+    wid, wco = oracle.route_sigmoid_bias(oracle.router_logits_f32(w, x), b, 8, 2.826)
+    assert np.array_equal(ids, wid) and _same(coefs, wco)
+
+
+def test_router_ties_prefer_the_lower_id(be, oracle):
+    import lbhip
+    w = synth.router_weights(64, 256, 3)
+    w[[9, 20, 41]] = w[5]      # four identical rows: equal logits
+    w[[3, 30]] = -w[5]
+    b = np.zeros(64, np.float32)
+    r = lbhip.Router(be, w, b)
+    x = np.abs(np.random.default_rng(2).standard_normal(256)).astype(np.float32)
+    x *= np.sign(w[5]) * 0 + 1
+    logits = oracle.router_logits_f32(w, x)
+    for mode in (0, 1):
+        ids, coefs = r.route_into(dev(x), 3, mode=mode, weight_scale=1.0)
+        want = oracle.route_softmax_topk(logits, 3) if mode == 0 else oracle.route_sigmoid_bias(logits, b, 3, 1.0)
+        assert np.array_equal(ids, want[0]) and _same(coefs, want[1])
+
+
+def test_router_rejects_non_finite_input_and_bias(be, oracle):
+    import lbhip
+    r, w, b = _router(be, 32, 512, seed=9, bias=True)
+    x = np.ones(512, np.float32)
+    x[100] = np.nan
+    with pytest.raises(lbhip.KernelError) as e:
+        r.route_into(dev(x), 4)
+    assert e.value.variant == "NonFiniteValue" and e.value.index == 100
+    b2 = b.copy()
+    b2[17] = np.inf
+    r2 = lbhip.Router(be, w, b2)
+    with pytest.raises(lbhip.KernelError) as e:
+        r2.route_into(dev(np.ones(512, np.float32)), 4, mode=1)
+    with pytest.raises(oracle.OracleError) as oe:
+        oracle.route_sigmoid_bias(oracle.router_logits_f32(w, np.ones(512, np.float32)), b2, 4, 1.0)
+    assert e.value.index == oe.value.index == 17 and e.value.bits == oe.value.bits
+
+
+def test_moe_block_forward_router_plus_experts_bit_exact(be, oracle, config3):
+    import lbhip
+    r, w, _ = _router(be, 16, 4096, seed=77)
+    rng = np.random.default_rng(12)
+    for _ in range(3):
+        x = rng.standard_normal(4096).astype(np.float32)
+        ids, coefs = oracle.route_softmax_topk(oracle.router_logits_f32(w, x), 8)
+        want, err = config3.oracle_out(oracle, ids, coefs, x)
+        y = dev(np.zeros(4096, np.float32))
+        lbhip.moe_block_forward(be, config3.moe, r, dev(x), y, 8)
+        assert err.status == 0 and _same(host(y), want)
