@@ -189,9 +189,9 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
                           const lbh_matrix *shared_up, const lbh_matrix *shared_down, lbh_moe **out,
                           lbh_error *err);
 lbh_status lbh_moe_destroy(lbh_moe *moe);
-/* Launch-shape knob: gate/up rows per workgroup (routed, shared; 16..256, powers of
- * two) and output rows per down workgroup (1..256). */
-lbh_status lbh_moe_set_tiles(lbh_moe *moe, int32_t tile_r, int32_t tile_s, int32_t tile_d);
+/* Launch-shape knob: workgroups of the routed and shared gate/up streams
+ * (1..65536 each) and output rows per down workgroup (1..256). */
+lbh_status lbh_moe_set_tiles(lbh_moe *moe, int32_t wg_routed, int32_t wg_shared, int32_t tile_d);
 
 /* [sync] moe_routed_by_id_into (crates/bridge-kernels-reference/src/moe.rs:64-147):
  * ids ascending with no duplicates, coefs finite (host arrays); output[hidden] =

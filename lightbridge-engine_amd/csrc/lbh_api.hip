@@ -456,12 +456,10 @@ struct lbh_moe {
     ExpertDev shared;
     int has_shared;
     float *h;
-    uint8_t *q8h;
-    uint32_t *counters;
-    int h_stride, q8_stride, cnt_stride;
+    int h_stride;
     MoeStatus *status;
     MoeStatus *status_host;
-    int tile_r, tile_s, tile_d;
+    int wg_r, wg_s, tile_d;   // gate/up workgroups (routed, shared stream); down rows per workgroup
 };
 
 namespace {
@@ -471,8 +469,6 @@ void free_moe(lbh_moe *m) {
     DeviceGuard g(m->device);
     if (m->experts_dev) (void)hipFree(m->experts_dev);
     if (m->h) (void)hipFree(m->h);
-    if (m->q8h) (void)hipFree(m->q8h);
-    if (m->counters) (void)hipFree(m->counters);
     if (m->status) (void)hipFree(m->status);
     if (m->status_host) (void)hipHostFree(m->status_host);
     delete m;
@@ -496,15 +492,9 @@ MoeArgs moe_args(const lbh_moe *m, const float *x, float *y) {
     a.x = x;
     a.y = y;
     a.h = m->h;
-    a.q8h = m->q8h;
-    a.counters = m->counters;
     a.h_stride = m->h_stride;
-    a.q8_stride = m->q8_stride;
-    a.cnt_stride = m->cnt_stride;
-    a.tile_r = m->tile_r;
-    a.tile_s = m->tile_s;
-    a.tiles_r = (int32_t)((m->ffn_r + m->tile_r - 1) / m->tile_r);
-    a.tiles_s = m->has_shared ? (int32_t)((m->ffn_s + m->tile_s - 1) / m->tile_s) : 0;
+    a.tiles_r = m->wg_r;
+    a.tiles_s = m->has_shared ? m->wg_s : 0;
     a.tile_d = m->tile_d;
     a.stop_step = 0x7fffffff;
     a.type_gate_r = m->type_gate_r;
@@ -564,13 +554,19 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
         m->shared.up = view_of(shared_up);
         m->shared.down = view_of(shared_down);
     }
-    m->tile_r = 32;
-    m->tile_s = 32;
+    // Gate/up workgroups: two per CU, split in proportion to the bytes of the
+    // top-8 routed experts and of the shared expert.
+    {
+        const double br = 8.0 * 2.0 * (double)gate[0]->bytes;
+        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes : 0.0;
+        const int total = 2 * ctx->cu_count;
+        m->wg_s = has_shared ? (int)(total * bs / (br + bs) + 0.5) : 0;
+        if (has_shared && m->wg_s < 1) m->wg_s = 1;
+        m->wg_r = total - m->wg_s > 1 ? total - m->wg_s : 1;
+    }
     m->tile_d = 16;
     const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
     m->h_stride = (int)max_ffn;
-    m->q8_stride = (int)(max_ffn / 256 * 292);
-    m->cnt_stride = (int)(max_ffn / 256);
     const size_t slots = MOE_MAX_ROUTED + 1;
     ExpertDev *table = new (std::nothrow) ExpertDev[n_experts];
     if (!table) {
@@ -586,9 +582,6 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
     if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
     delete[] table;
     if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc(&m->q8h, slots * (size_t)m->q8_stride);
-    if (e == hipSuccess) e = hipMalloc(&m->counters, slots * (size_t)m->cnt_stride * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(m->counters, 0, slots * (size_t)m->cnt_stride * sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&m->status, sizeof(MoeStatus));
     if (e == hipSuccess) e = hipHostMalloc(&m->status_host, sizeof(MoeStatus), hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -606,12 +599,12 @@ lbh_status lbh_moe_destroy(lbh_moe *m) {
     return LBH_OK;
 }
 
-lbh_status lbh_moe_set_tiles(lbh_moe *m, int32_t tile_r, int32_t tile_s, int32_t tile_d) {
+lbh_status lbh_moe_set_tiles(lbh_moe *m, int32_t wg_routed, int32_t wg_shared, int32_t tile_d) {
     if (!m) return LBH_NULL_ARGUMENT;
-    auto ok_tile = [](int t) { return t == 16 || t == 32 || t == 64 || t == 128 || t == 256; };
-    if (!ok_tile(tile_r) || !ok_tile(tile_s) || tile_d < 1 || tile_d > 256) return LBH_INVALID_PARAMETER;
-    m->tile_r = tile_r;
-    m->tile_s = tile_s;
+    if (wg_routed < 1 || wg_routed > 65536 || wg_shared < 1 || wg_shared > 65536 || tile_d < 1 || tile_d > 256)
+        return LBH_INVALID_PARAMETER;
+    m->wg_r = wg_routed;
+    m->wg_s = wg_shared;
     m->tile_d = tile_d;
     return LBH_OK;
 }
@@ -684,7 +677,9 @@ lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *i
     HIP_TRY(launch_moe_reset_status(m->status, ctx->stream));
     HIP_TRY(launch_find_nonfinite(input, (long long)input_len, &m->status->first_bad_input, ctx->stream));
     HIP_TRY(launch_moe_gate_up(a, ctx->stream));
-    if (i_host == n_routed) HIP_TRY(launch_moe_down(a, ctx->stream));
+    if (i_host == n_routed) {
+        HIP_TRY(launch_moe_down(a, ctx->stream));
+    }
     HIP_TRY(hipMemcpyAsync(m->status_host, m->status, sizeof(MoeStatus), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     const MoeStatus st = *m->status_host;
@@ -736,15 +731,13 @@ void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, 
 struct lbh_router {
     int device;
     size_t n_experts, hidden;
-    float *w;            // [n_experts][hidden]
+    float *w;            // transposed, interleaved by four (RouterArgs::w)
     float *bias;         // [n_experts] or NULL
     float *logits;
-    uint32_t *counter;
     MoeRoute *route;     // device
     MoeRoute *route_host;
     unsigned long long *status;
     unsigned long long *status_host;
-    int epw;
 };
 
 namespace {
@@ -755,7 +748,6 @@ void free_router(lbh_router *r) {
     if (r->w) (void)hipFree(r->w);
     if (r->bias) (void)hipFree(r->bias);
     if (r->logits) (void)hipFree(r->logits);
-    if (r->counter) (void)hipFree(r->counter);
     if (r->route) (void)hipFree(r->route);
     if (r->status) (void)hipFree(r->status);
     if (r->route_host) (void)hipHostFree(r->route_host);
@@ -769,14 +761,12 @@ RouterArgs router_args(const lbh_router *r, const float *x, size_t top_k, int32_
     a.bias = r->bias;
     a.x = x;
     a.logits = r->logits;
-    a.counter = r->counter;
     a.route = r->route;
     a.n_experts = (int32_t)r->n_experts;
     a.hidden = (int32_t)r->hidden;
     a.top_k = (int32_t)top_k;
     a.mode = mode;
     a.weight_scale = scale;
-    a.epw = r->epw;
     return a;
 }
 
@@ -796,17 +786,28 @@ lbh_status lbh_router_create(lbh_ctx *ctx, const float *weights, size_t n_expert
     r->device = ctx->device;
     r->n_experts = n_experts;
     r->hidden = hidden;
-    r->epw = 2;
     const hipMemcpyKind kind = on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-    hipError_t e = hipMalloc(&r->w, n_experts * hidden * sizeof(float));
-    if (e == hipSuccess) e = hipMemcpy(r->w, weights, n_experts * hidden * sizeof(float), kind);
+    // Device layout: transposed and interleaved by four, so the lane of expert
+    // e reads w[e][4j..4j+3] at ((j * n_experts) + e) * 16 bytes.
+    const size_t count = n_experts * hidden;
+    float *src = new (std::nothrow) float[count];
+    float *dst = new (std::nothrow) float[count];
+    hipError_t e = (src && dst) ? hipSuccess : hipErrorOutOfMemory;
+    if (e == hipSuccess)
+        e = hipMemcpy(src, weights, count * sizeof(float), on_device ? hipMemcpyDeviceToHost : hipMemcpyHostToHost);
+    if (e == hipSuccess) {
+        for (size_t x = 0; x < n_experts; ++x)
+            for (size_t i = 0; i < hidden; ++i) dst[((i / 4) * n_experts + x) * 4 + (i % 4)] = src[x * hidden + i];
+        e = hipMalloc(&r->w, count * sizeof(float));
+    }
+    if (e == hipSuccess) e = hipMemcpy(r->w, dst, count * sizeof(float), hipMemcpyHostToDevice);
+    delete[] src;
+    delete[] dst;
     if (e == hipSuccess && bias) {
         e = hipMalloc(&r->bias, n_experts * sizeof(float));
         if (e == hipSuccess) e = hipMemcpy(r->bias, bias, n_experts * sizeof(float), kind);
     }
     if (e == hipSuccess) e = hipMalloc(&r->logits, n_experts * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc(&r->counter, sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMemset(r->counter, 0, sizeof(uint32_t));
     if (e == hipSuccess) e = hipMalloc(&r->route, sizeof(MoeRoute));
     if (e == hipSuccess) e = hipMemset(r->route, 0, sizeof(MoeRoute));
     if (e == hipSuccess) e = hipMalloc(&r->status, 2 * sizeof(unsigned long long));
@@ -845,7 +846,6 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, si
     // The router matvec is gemv_into on an F32 matrix: its input must be finite (gemv.rs:195-211).
     HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
     HIP_TRY(launch_find_nonfinite(x, (long long)x_len, &ctx->status->first_bad_input, ctx->stream));
-    HIP_TRY(hipMemsetAsync(r->status, 0xff, sizeof(unsigned long long), ctx->stream));
     HIP_TRY(launch_router(a, ctx->stream));
     HIP_TRY(hipMemcpyAsync(r->status_host, r->status, sizeof(unsigned long long), hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipMemcpyAsync(r->route_host, r->route, sizeof(MoeRoute), hipMemcpyDeviceToHost, ctx->stream));
@@ -889,12 +889,20 @@ lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const 
     if (top_k == 0 || top_k > r->n_experts || top_k > MOE_MAX_ROUTED) return LBH_INVALID_PARAMETER;
     if (mode != 0 && (mode != 1 || !r->bias)) return LBH_INVALID_PARAMETER;
     DeviceGuard g(ctx->device);
-    RouterArgs ra = router_args(r, x, top_k, mode, weight_scale);
-    if (launch_router(ra, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     MoeArgs a = moe_args(m, x, y);
+    a.router = router_args(r, x, top_k, mode, weight_scale);
     a.route_dev = r->route;
     a.route.n = (int32_t)top_k;
     a.n_launch = (int32_t)top_k;
+    a.select_in_kernel = 1;
+    if (m->has_shared) {
+        // Router chains beside the shared gate/up, then the routed gate/up
+        // (selecting from the logits), then down + combine.
+        a.skip_shared_gate_up = 1;
+        if (launch_moe_router_shared(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    } else if (launch_router_logits(a.router, ctx->stream) != hipSuccess) {
+        return LBH_HIP_ERROR;
+    }
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;

@@ -63,6 +63,18 @@ struct ExpertDev {
     MatView gate, up, down;
 };
 
+struct RouterArgs {
+    const float *w;             // transposed, interleaved by four: w[(j * n_experts + e) * 4 + c] = row e, input 4j + c
+    const float *bias;          // selection bias [n_experts] (mode 1)
+    const float *x;             // [hidden]
+    float *logits;              // [n_experts]
+    MoeRoute *route;            // selection output
+    unsigned long long *status; // optional: (first bad expert << 2) | field
+    int32_t n_experts, hidden, top_k, mode;
+    float weight_scale;
+    int32_t pad;
+};
+
 // Device status of one MoE call (~0 when clean).
 struct MoeStatus {
     unsigned long long first_bad_swiglu;   // (expert order << 32) | lane; order n = shared
@@ -81,9 +93,7 @@ struct MoeArgs {
     const MoeRoute *route_dev;  // routing written by the device router
     const float *x;             // [hidden]
     float *h;                   // SwiGLU outputs: slot * h_stride
-    uint8_t *q8h;               // their Q8_K encodings: slot * q8_stride
-    uint32_t *counters;         // arrivals per (slot, 256-row block); self-resetting
-    int32_t h_stride, q8_stride, cnt_stride;
+    int32_t h_stride;
     float *y;                   // [hidden]
     MoeStatus *status;
     int32_t tile_r, tile_s;     // gate/up rows per workgroup (routed, shared)
@@ -94,22 +104,17 @@ struct MoeArgs {
     int32_t n_launch;           // routed experts covered by this launch
     int32_t type_gate_r;        // GGML type of every routed gate/up matrix
     int32_t type_down_r;        // GGML type of every routed down matrix
-};
-
-struct RouterArgs {
-    const float *w;             // [n_experts][hidden] f32 rows (GGML F32 [hidden, n_experts])
-    const float *bias;          // selection bias [n_experts] (mode 1)
-    const float *x;             // [hidden]
-    float *logits;              // [n_experts]
-    uint32_t *counter;          // arrivals; self-resetting
-    MoeRoute *route;            // output
-    unsigned long long *status; // optional: (first bad expert << 2) | field
-    int32_t n_experts, hidden, top_k, mode;
-    float weight_scale;
-    int32_t epw;                // experts per workgroup
+    // Block decode: the gate/up kernel selects the routing from finished router
+    // logits (router.logits) and publishes it to route_dev for the down kernel;
+    // the shared expert's gate/up ran beside the router chains.
+    int32_t select_in_kernel;
+    int32_t skip_shared_gate_up;
+    RouterArgs router;
 };
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t s);
+hipError_t launch_router_logits(const RouterArgs &a, hipStream_t s);
+hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_gate_up(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_down(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_reset_status(MoeStatus *st, hipStream_t s);

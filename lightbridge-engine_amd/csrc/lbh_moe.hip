@@ -4,20 +4,23 @@
 //
 //   k_moe_gate_up  one workgroup per (expert, tile of hidden rows): Q8_K(x) into
 //                  LDS, gate and up row dots of the tile, SwiGLU with the
-//                  libm-exact expf (activation.rs:170-178), h to scratch; the
-//                  last workgroup to finish a 256-row block of h quantizes it
-//                  to Q8_K (release/acquire on a self-resetting arrival count).
-//   k_moe_down     one workgroup per tile of output rows: the down row dots of
+//                  libm-exact expf (activation.rs:170-178), h to scratch;
+//   k_moe_down     one workgroup per tile of output rows: Q8_K of every
+//                  expert's h into LDS, the down row dots of
 //                  every routed expert and of the shared expert, then each row
 //                  is combined in the reference order
 //                      y = ((0 + c_0 d_0) + c_1 d_1) + ... + 1.0 * d_shared
 //                  (gemv_accumulate_scaled_into, gemv.rs:161-171, moe.rs:141-146).
 //
 // The result is bit-identical to the reference: the same Q8_K bytes, integer
-// block sums, per-row folds, SwiGLU and accumulation order.
+// block sums, per-row folds, SwiGLU and accumulation order.  Data moves
+// between workgroups only across kernel boundaries: an agent-scope fence
+// inside a kernel writes back and invalidates the whole L2 of the XCD, which
+// measured slower than an extra launch.
 #include "lbh_internal.h"
 #include "lbh_math.h"
 #include "lbh_rows.h"
+#include "lbh_router.h"
 
 namespace lbh {
 
@@ -34,39 +37,45 @@ __device__ __forceinline__ float route_coef(const MoeArgs &a, int s) {
     return a.route_dev ? a.route_dev->coefs[s] : a.route.coefs[s];
 }
 
-// LDS bytes of one gate/up tile body.
+// LDS bytes of one gate/up workgroup of type TY.
 template <int TY>
 __host__ __device__ constexpr int gate_up_lds(int nb) {
-    return align16(GridLDS<TY>::BYTES) + align16(nb * 292) + MOE_WAVES * (int)sizeof(FoldLDS<TY>) + 16;
+    return align16(GridLDS<TY>::BYTES) + align16(nb * 292) + MOE_WAVES * (int)sizeof(FoldLDS<TY>);
 }
 
-// Gate and up rows [r0, r1) of one expert, SwiGLU into h (slot), then the
-// last-arriving tile of each 256-row block quantizes it to Q8_K.
-template <int TY, int LPU>
-__device__ __forceinline__ void gate_up_tile(const MoeArgs &a, const MatView &G, const MatView &Uv, int rows_total,
-                                             int tile, int r0, int r1, int slot, int order, uint8_t *smem) {
+// Gate and up rows of `count` experts of one type, SwiGLU into h.  The
+// workgroup's waves walk the flattened (slot, row step) items of all of them
+// with a stride of `nwaves`: Q8_K(x) stays in registers (the same input for
+// every expert), the codebook is filled once per workgroup, and the next
+// item's weights are loaded while the current item is computed.
+template <int TY, int LPU, class SlotOf>
+__device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &slot_of, int count, int rows,
+                                               int first_wave, int nwaves, uint8_t *smem) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int NB = a.hidden / 256;
     uint8_t *s_grid = smem;
     uint8_t *s_q8 = smem + align16(GridLDS<TY>::BYTES);
     FoldLDS<TY> *s_fold = reinterpret_cast<FoldLDS<TY> *>(s_q8 + align16(NB * 292));
-    int *s_flag = reinterpret_cast<int *>(s_fold + MOE_WAVES);
 
     const LaneMap<LPU> L(lane, NB);
-    const Planes PG = make_planes(G.planes, G.units, G.bytes);
-    const Planes PU = make_planes(Uv.planes, Uv.units, Uv.bytes);
-    const uint32_t po = part_offset<TY, LPU>(PG, L.part);   // gate and up share the shape
-    const int items = (r1 - r0 + L.rpw - 1) / L.rpw;
+    const int per = (rows + L.rpw - 1) / L.rpw;
+    const int items = count * per;
     using W = WOf<TY, LPU>;
+    // item -> (slot index, expert views, row)
     auto issue = [&](int it, W &wg, W &wu) {
-        const int r = r0 + it * L.rpw + L.slot;
-        if (it < items && L.lane_on && r < r1) {
-            const uint32_t u = (uint32_t)(r * NB + L.b);
-            load_slice(PG, u, po, L.part, wg);
-            load_slice(PU, u, po, L.part, wu);
-        }
+        if (it >= items) return;
+        const int m = it / per, j = it - m * per;
+        const int r = j * L.rpw + L.slot;
+        if (!(L.lane_on && r < rows)) return;
+        const ExpertDev &E = slot_of(m);
+        const Planes PG = make_planes(E.gate.planes, E.gate.units, E.gate.bytes);
+        const Planes PU = make_planes(E.up.planes, E.up.units, E.up.bytes);
+        const uint32_t po = part_offset<TY, LPU>(PG, L.part);
+        const uint32_t u = (uint32_t)(r * NB + L.b);
+        load_slice(PG, u, po, L.part, wg);
+        load_slice(PU, u, po, L.part, wu);
     };
-    int it = wid;
+    int it = first_wave + wid;
     W ga, ua, gb, ub;
     issue(it, ga, ua);
 
@@ -76,97 +85,132 @@ __device__ __forceinline__ void gate_up_tile(const MoeArgs &a, const MatView &G,
     ActOf<TY, LPU> act;
     load_act(s_q8 + L.b * 292, L.part, act);
 
-    float *h = a.h + (long long)slot * a.h_stride;
     auto process = [&](int it, const W &wg, const W &wu) {
-        const int r = r0 + it * L.rpw + L.slot;
-        const bool on = L.lane_on && r < r1;
+        const int m = it / per, j = it - m * per;
+        const int r = j * L.rpw + L.slot;
+        const bool on = L.lane_on && r < rows;
         const float gv = row_dot<TY, LPU>(wg, act, on, L, s_grid, s_fold[wid], nullptr, 0);
         const float uv = row_dot<TY, LPU>(wu, act, on, L, s_grid, s_fold[wid], nullptr, 0);
         if (on && L.leader()) {
+            const int slot = slot_of.slot(m), order = slot_of.order(m);
             const float hv = swiglu_ref(gv, uv);
-            h[r] = hv;
+            a.h[(long long)slot * a.h_stride + r] = hv;
             if (a.check && !isfinite(hv))
                 atomicMin(&a.status->first_bad_swiglu, ((unsigned long long)order << 32) | (unsigned)r);
         }
     };
     while (it < items) {
-        issue(it + MOE_WAVES, gb, ub);
+        issue(it + nwaves, gb, ub);
         process(it, ga, ua);
-        it += MOE_WAVES;
+        it += nwaves;
         if (it >= items) break;
-        issue(it + MOE_WAVES, ga, ua);
+        issue(it + nwaves, ga, ua);
         process(it, gb, ub);
-        it += MOE_WAVES;
-    }
-
-    // Publish this tile's h rows; the tile that completes a 256-row block
-    // quantizes it (the count resets itself for the next call).
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int b_first = r0 / 256, b_last = (r1 - 1) / 256;
-        for (int blk = b_first, i = 0; i < 2; ++blk, ++i) {
-            s_flag[i] = -1;
-            if (blk > b_last) continue;
-            const int t_first = (blk * 256) / tile;
-            const int t_last = ((blk + 1) * 256 < rows_total ? (blk + 1) * 256 : rows_total) - 1;
-            const unsigned need = (unsigned)(t_last / tile - t_first + 1);
-            uint32_t *c = a.counters + (long long)slot * a.cnt_stride + blk;
-            const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-            if (old + 1 == need) {
-                s_flag[i] = blk;
-                __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-    }
-    __syncthreads();
-    if (wid < 2 && s_flag[wid] >= 0) {
-        __threadfence();
-        quantize_blocks_wave(h, a.q8h + (long long)slot * a.q8_stride, s_flag[wid], s_flag[wid] + 1);
+        it += nwaves;
     }
 }
 
+struct RoutedSlots {
+    const MoeArgs &a;
+    const uint32_t *ids;   // LDS copy of the routed ids
+    __device__ const ExpertDev &operator()(int m) const { return a.experts[ids[m]]; }
+    __device__ int slot(int m) const { return m; }
+    __device__ int order(int m) const { return m; }
+};
+struct SharedSlot {
+    const MoeArgs &a;
+    int n;
+    __device__ const ExpertDev &operator()(int) const { return a.shared; }
+    __device__ int slot(int) const { return MOE_SHARED_SLOT; }
+    __device__ int order(int) const { return n; }
+};
+
+// Workgroups [0, wg_s) stream the shared expert, the rest the routed experts.
 template <int TYR, int LPUR, int TYS, int LPUS>
 __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ uint32_t s_ids[MOE_MAX_ROUTED];
     if (a.status && a.status->first_bad_input != ~0ull) return;
-    const int n = route_n(a);
-    int bid = blockIdx.x;
-    const int ts = a.has_shared ? a.tiles_s : 0;
-    if (bid < ts) {
-        const int r0 = bid * a.tile_s, r1 = r0 + a.tile_s < a.ffn_s ? r0 + a.tile_s : a.ffn_s;
-        gate_up_tile<TYS, LPUS>(a, a.shared.gate, a.shared.up, a.ffn_s, a.tile_s, r0, r1, MOE_SHARED_SLOT, n, smem);
+    const int wg_s = a.has_shared && !a.skip_shared_gate_up ? a.tiles_s : 0;
+    if ((int)blockIdx.x < wg_s) {
+        const int n = a.route_dev && !a.select_in_kernel ? a.route_dev->n : a.route.n;
+        gate_up_stream<TYS, LPUS>(a, SharedSlot{a, n}, 1, a.ffn_s, blockIdx.x * MOE_WAVES, wg_s * MOE_WAVES, smem);
         return;
     }
-    bid -= ts;
-    const int s = bid / a.tiles_r, t = bid - s * a.tiles_r;
-    const ExpertDev &E = a.experts[route_id(a, s)];
-    const int r0 = t * a.tile_r, r1 = r0 + a.tile_r < a.ffn_r ? r0 + a.tile_r : a.ffn_r;
-    gate_up_tile<TYR, LPUR>(a, E.gate, E.up, a.ffn_r, a.tile_r, r0, r1, s, s, smem);
+    if (a.select_in_kernel) {
+        // Every workgroup selects the same route from the finished logits;
+        // workgroup wg_s publishes it for the down kernel.
+        if (threadIdx.x < 64) {
+            MoeRoute r;
+            unsigned long long bad;
+            select_route(a.router, r, bad);
+            if (threadIdx.x == 0) {
+#pragma unroll
+                for (int q = 0; q < MOE_MAX_ROUTED; ++q) s_ids[q] = r.ids[q];
+                if ((int)blockIdx.x == wg_s) *const_cast<MoeRoute *>(a.route_dev) = r;
+            }
+        }
+    } else if (threadIdx.x < MOE_MAX_ROUTED) {
+        s_ids[threadIdx.x] = route_id(a, threadIdx.x < route_n(a) ? threadIdx.x : 0);
+    }
+    __syncthreads();
+    const int wg_r = gridDim.x - wg_s;
+    gate_up_stream<TYR, LPUR>(a, RoutedSlots{a, s_ids}, a.n_launch, a.ffn_r, (blockIdx.x - wg_s) * MOE_WAVES,
+                              wg_r * MOE_WAVES, smem);
 }
 
-// Down row dots of `count` matrices of one type for rows [r0, r1): matrix m
-// reads its Q8_K input from s_q8 + m * in_stride and writes s_y[m][row - r0].
-template <int TY, int LPU, class GetView>
-__device__ __forceinline__ void down_rows(const GetView &view_of, int count, int nb, const uint8_t *s_q8, int in_stride,
-                                          int r0, int r1, const void *s_grid, FoldLDS<TY> &fold, float *s_y, int y_stride,
-                                          int m_base) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+// Block decode, first launch: router chains (one wave per 64 experts, in the
+// first workgroups) beside the shared expert's gate/up stream, which does not
+// depend on the routing.
+template <int TYS, int LPUS>
+__global__ void __launch_bounds__(MOE_THREADS) k_moe_router_shared(MoeArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int rw = (a.router.n_experts + 63) / 64;
+    if ((int)blockIdx.x < rw) {
+        if (threadIdx.x < 64) router_chain_wave(a.router, blockIdx.x * 64);
+        return;
+    }
+    gate_up_stream<TYS, LPUS>(a, SharedSlot{a, a.route.n}, 1, a.ffn_s, (blockIdx.x - rw) * MOE_WAVES,
+                              a.tiles_s * MOE_WAVES, smem);
+}
+
+// Down projections and the ordered combine for output rows [r0, r0 + tile_d).
+// Waves 0..n-1 take routed expert m = wave (its Q8_K(h) slice in registers),
+// waves n.. share the shared expert's rows; the row dots meet in LDS and one
+// lane per row accumulates them in the reference order
+//     y = ((0 + c_0 d_0) + c_1 d_1) + ... + 1.0 * d_shared   (moe.rs:141-146).
+template <int TY, int LPU>
+__device__ __forceinline__ void down_wave(const MatView &V, const uint8_t *q8, int nb, int r0, int r1, int first,
+                                          int stride, const void *s_grid, FoldLDS<TY> &fold, float *s_y) {
+    const int lane = threadIdx.x & 63;
     const LaneMap<LPU> L(lane, nb);
-    const int per = (r1 - r0 + L.rpw - 1) / L.rpw;
-    const int total = count * per;
-    for (int i = wid; i < total; i += MOE_WAVES) {
-        const int m = i / per, j = i - m * per;
-        const MatView V = view_of(m);
-        const Planes P = make_planes(V.planes, V.units, V.bytes);
-        const int r = r0 + j * L.rpw + L.slot;
+    const Planes P = make_planes(V.planes, V.units, V.bytes);
+    const uint32_t po = part_offset<TY, LPU>(P, L.part);
+    const int items = (r1 - r0 + L.rpw - 1) / L.rpw;
+    using W = WOf<TY, LPU>;
+    auto issue = [&](int it, W &w) {
+        const int r = r0 + it * L.rpw + L.slot;
+        if (it < items && L.lane_on && r < r1) load_slice(P, (uint32_t)(r * nb + L.b), po, L.part, w);
+    };
+    int it = first;
+    W wa, wb;
+    issue(it, wa);
+    ActOf<TY, LPU> act;
+    load_act(q8 + L.b * 292, L.part, act);
+    auto process = [&](int it, const W &w) {
+        const int r = r0 + it * L.rpw + L.slot;
         const bool on = L.lane_on && r < r1;
-        WOf<TY, LPU> w;
-        if (on) load_slice(P, (uint32_t)(r * nb + L.b), part_offset<TY, LPU>(P, L.part), L.part, w);
-        ActOf<TY, LPU> act;
-        load_act(s_q8 + m * in_stride + L.b * 292, L.part, act);
         const float v = row_dot<TY, LPU>(w, act, on, L, s_grid, fold, nullptr, 0);
-        if (on && L.leader()) s_y[(m_base + m) * y_stride + (r - r0)] = v;
+        if (on && L.leader()) s_y[r - r0] = v;
+    };
+    while (it < items) {
+        issue(it + stride, wb);
+        process(it, wa);
+        it += stride;
+        if (it >= items) break;
+        issue(it + stride, wa);
+        process(it, wb);
+        it += stride;
     }
 }
 
@@ -175,8 +219,12 @@ __host__ __device__ constexpr int down_fold_bytes() {
     return (int)sizeof(FoldLDS<TYR>) > (int)sizeof(FoldLDS<TYS>) ? (int)sizeof(FoldLDS<TYR>) : (int)sizeof(FoldLDS<TYS>);
 }
 
+constexpr int DOWN_SHARED_WAVES = 4;
+
+constexpr int DOWN_MAX_WAVES = 12;
+
 template <int TYR, int LPUR, int TYS, int LPUS>
-__global__ void __launch_bounds__(MOE_THREADS) k_moe_down(MoeArgs a) {
+__global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     if (a.status && (a.status->first_bad_input != ~0ull || a.status->first_bad_swiglu != ~0ull)) return;
     const int wid = threadIdx.x >> 6;
@@ -184,45 +232,56 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_down(MoeArgs a) {
     const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
     const int r0 = blockIdx.x * a.tile_d;
     const int r1 = r0 + a.tile_d < a.hidden ? r0 + a.tile_d : a.hidden;
-    constexpr int GB = GridLDS<TYR>::BYTES > GridLDS<TYS>::BYTES ? GridLDS<TYR>::BYTES : GridLDS<TYS>::BYTES;
     uint8_t *s_grid_r = smem;
     uint8_t *s_grid_s = smem + align16(GridLDS<TYR>::BYTES);
-    uint8_t *s_q8 = smem + align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES);
-    const int q8_bytes = align16((n * nbr + (a.has_shared ? nbs : 0)) * 292);
-    uint8_t *s_foldp = s_q8 + q8_bytes;
-    float *s_y = reinterpret_cast<float *>(s_foldp + MOE_WAVES * down_fold_bytes<TYR, TYS>());
-    (void)GB;
+    uint8_t *s_foldp = s_grid_s + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES);
+    const int nw = blockDim.x >> 6;
+    float *s_y = reinterpret_cast<float *>(s_foldp + nw * down_fold_bytes<TYR, TYS>());
+    uint8_t *s_q8 = reinterpret_cast<uint8_t *>(s_y + (MOE_MAX_ROUTED + 1) * a.tile_d);   // [n * nbr + nbs] blocks
 
-    // Stage the Q8_K inputs: routed slots 0..n-1, then the shared slot.
-    const int rbytes = nbr * 292;
-    for (int m = 0; m < n; ++m)
-        for (int i = threadIdx.x; i < rbytes / 4; i += MOE_THREADS)
-            reinterpret_cast<uint32_t *>(s_q8 + m * rbytes)[i] =
-                reinterpret_cast<const uint32_t *>(a.q8h + (long long)m * a.q8_stride)[i];
-    if (a.has_shared)
-        for (int i = threadIdx.x; i < nbs * 73; i += MOE_THREADS)
-            reinterpret_cast<uint32_t *>(s_q8 + n * rbytes)[i] =
-                reinterpret_cast<const uint32_t *>(a.q8h + (long long)MOE_SHARED_SLOT * a.q8_stride)[i];
     fill_grid<TYR>(s_grid_r);
     if (TYS != TYR) fill_grid<TYS>(s_grid_s);
+    // Q8_K of every expert's h into LDS (quantize_row_q8_k_into of the down
+    // projection's input, gemv.rs:161-163): chunks of up to four blocks of one
+    // slot per wave step.
+    {
+        const int cr = (nbr + 3) / 4, cs = (nbs + 3) / 4;
+        const int chunks = n * cr + (a.has_shared ? cs : 0);
+        for (int c = wid; c < chunks; c += nw) {
+            if (c < n * cr) {
+                const int m = c / cr, b0 = 4 * (c - m * cr);
+                quantize_blocks_wave(a.h + (long long)m * a.h_stride, s_q8 + m * nbr * 292, b0, nbr);
+            } else {
+                const int b0 = 4 * (c - n * cr);
+                quantize_blocks_wave(a.h + (long long)MOE_SHARED_SLOT * a.h_stride, s_q8 + n * nbr * 292, b0, nbs);
+            }
+        }
+    }
     __syncthreads();
 
+    // Tasks: routed experts 0..n-1, then DOWN_SHARED_WAVES interleaved parts of
+    // the shared expert; wave w takes tasks w, w + nw, ...
     const int ystride = a.tile_d;
-    auto routed_view = [&](int m) { return a.experts[route_id(a, m)].down; };
-    down_rows<TYR, LPUR>(routed_view, n, nbr, s_q8, rbytes, r0, r1, s_grid_r,
-                         *reinterpret_cast<FoldLDS<TYR> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>()), s_y, ystride, 0);
-    if (a.has_shared) {
-        auto shared_view = [&](int) { return a.shared.down; };
-        down_rows<TYS, LPUS>(shared_view, 1, nbs, s_q8 + n * rbytes, 0, r0, r1, TYS == TYR ? s_grid_r : s_grid_s,
-                             *reinterpret_cast<FoldLDS<TYS> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>()), s_y, ystride,
-                             n);
+    const int tasks = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
+    for (int t = wid; t < tasks; t += nw) {
+        if (t < n) {
+            down_wave<TYR, LPUR>(a.experts[route_id(a, t)].down, s_q8 + t * nbr * 292, nbr, r0, r1, 0, 1,
+                                 s_grid_r,
+                                 *reinterpret_cast<FoldLDS<TYR> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>()),
+                                 s_y + t * ystride);
+        } else {
+            down_wave<TYS, LPUS>(a.shared.down, s_q8 + n * nbr * 292, nbs, r0, r1, t - n,
+                                 DOWN_SHARED_WAVES, TYS == TYR ? s_grid_r : s_grid_s,
+                                 *reinterpret_cast<FoldLDS<TYS> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>()),
+                                 s_y + n * ystride);
+        }
     }
     __syncthreads();
 
     // Ordered combine: output.fill(0), then dest += coef * dot per expert in
     // ascending id order, then the shared expert at 1.0 (moe.rs:141-146).
     const int last = a.has_shared ? n : n - 1;
-    for (int t = threadIdx.x; t < r1 - r0; t += MOE_THREADS) {
+    for (int t = threadIdx.x; t < r1 - r0; t += blockDim.x) {
         float acc = 0.0f;
         int bad = -1;
         for (int s = 0; s < n && s <= a.stop_step; ++s) {
@@ -259,17 +318,18 @@ static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b)
 
 // Type combinations with a fused instantiation: routed gate/up IQ2_S with a
 // Q4_K or IQ2_S shared expert; routed down IQ3_S or IQ2_S with a Q5_K, IQ3_S
-// or IQ2_S shared down.  Lanes per unit: 2 for IQ types, 4 for K-quants.
+// or IQ2_S shared down.  Two lanes per (row, block) unit.
 template <int TY>
 constexpr int moe_lpu() {
-    return Traits<TY>::KQ ? 4 : 2;
+    return 2;
 }
 
 template <int TYR, int TYS>
 static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
     const int nb = a.hidden / 256;
     const int lds = gate_up_lds<TYR>(nb) > gate_up_lds<TYS>(nb) ? gate_up_lds<TYR>(nb) : gate_up_lds<TYS>(nb);
-    const int grid = (a.has_shared ? a.tiles_s : 0) + a.n_launch * a.tiles_r;
+    // tiles_s / tiles_r: workgroups of the shared / routed streams.
+    const int grid = (a.has_shared && !a.skip_shared_gate_up ? a.tiles_s : 0) + (a.n_launch > 0 ? a.tiles_r : 0);
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL((k_moe_gate_up<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>), dim3(grid), dim3(MOE_THREADS), lds, s,
                        a);
@@ -278,13 +338,31 @@ static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
 
 template <int TYR, int TYS>
 static hipError_t down_typed(const MoeArgs &a, hipStream_t s) {
-    const int n = a.route_dev ? MOE_MAX_ROUTED : a.route.n;
-    const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
+    const int n = a.route_dev ? a.n_launch : a.route.n;
+    const int waves = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
+    const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
+    const int q8 = (n * (a.ffn_r / 256) + (a.has_shared ? a.ffn_s / 256 : 0)) * 292;
     const int lds = align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES) +
-                    align16((n * nbr + (a.has_shared ? nbs : 0)) * 292) + MOE_WAVES * down_fold_bytes<TYR, TYS>() +
-                    (MOE_MAX_ROUTED + 1) * a.tile_d * 4;
+                    nw * down_fold_bytes<TYR, TYS>() + (MOE_MAX_ROUTED + 1) * a.tile_d * 4 + align16(q8);
     hipLaunchKernelGGL((k_moe_down<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>), dim3(cdiv(a.hidden, a.tile_d)),
-                       dim3(MOE_THREADS), lds, s, a);
+                       dim3(64 * nw), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s) {
+    const int nb = a.hidden / 256;
+    const int rw = (a.router.n_experts + 63) / 64;
+    const int ts = a.shared.gate.type;
+    const int grid = rw + a.tiles_s;
+    if (ts == T_Q4_K) {
+        hipLaunchKernelGGL((k_moe_router_shared<T_Q4_K, moe_lpu<T_Q4_K>()>), dim3(grid), dim3(MOE_THREADS),
+                           gate_up_lds<T_Q4_K>(nb), s, a);
+    } else if (ts == T_IQ2_S) {
+        hipLaunchKernelGGL((k_moe_router_shared<T_IQ2_S, moe_lpu<T_IQ2_S>()>), dim3(grid), dim3(MOE_THREADS),
+                           gate_up_lds<T_IQ2_S>(nb), s, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -1,0 +1,160 @@
+// lbh_router.h — top-k selection of one token from finished router logits,
+// shared by the router kernels and the MoE gate/up prologue.
+#pragma once
+#include "lbh_internal.h"
+#include "lbh_math.h"
+
+namespace lbh {
+
+__device__ __forceinline__ float sigmoid_ref(float v) { return 1.0f / (1.0f + expf_libm(-v)); }  // routing.rs:109-111
+
+// Total order of selection keys: larger score first, then smaller id.
+// Scores are finite (checked) floats; +0.0 and -0.0 compare equal as in f32.
+__device__ __forceinline__ unsigned long long sel_key(float score, uint32_t id) {
+    const float s = score == 0.0f ? 0.0f : score;        // -0.0 == +0.0
+    uint32_t b = __float_as_uint(s);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);     // monotone float -> uint
+    return ((unsigned long long)b << 32) | (0xffffffffu - id);
+}
+
+// One wave: lanes are experts e0 + lane.
+__device__ __forceinline__ void router_chain_wave(const RouterArgs &a, int e0) {
+    const int lane = threadIdx.x & 63;
+    const int e = e0 + lane;
+    const int n = a.n_experts;
+    const bool on = e < n;
+    const float4 *wt = reinterpret_cast<const float4 *>(a.w);
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+    const int steps = a.hidden / 4;   // multiple of 64
+    constexpr int P = 8;
+    float4 cur[P], nxt[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) cur[k] = on ? wt[(long long)k * n + e] : make_float4(0, 0, 0, 0);
+    float sum = 0.0f;
+    for (int j = 0; j < steps; j += P) {
+        if (j + P < steps) {
+#pragma unroll
+            for (int k = 0; k < P; ++k) nxt[k] = on ? wt[(long long)(j + P + k) * n + e] : make_float4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const float4 xv = x4[j + k];
+            sum = __fadd_rn(sum, __fmul_rn(cur[k].x, xv.x));
+            sum = __fadd_rn(sum, __fmul_rn(cur[k].y, xv.y));
+            sum = __fadd_rn(sum, __fmul_rn(cur[k].z, xv.z));
+            sum = __fadd_rn(sum, __fmul_rn(cur[k].w, xv.w));
+        }
+#pragma unroll
+        for (int k = 0; k < P; ++k) cur[k] = nxt[k];
+    }
+    if (on) a.logits[e] = sum;
+}
+
+// Called by all 64 lanes of one wave; every lane returns the same route.
+// bad: ~0 when valid, else (first invalid expert << 2) | field
+// (0 logit, 1 bias, 2 selection score: the checks of routing.rs:72-77).
+__device__ __forceinline__ void select_route(const RouterArgs &a, MoeRoute &out, unsigned long long &bad) {
+    const int lane = threadIdx.x & 63;
+    constexpr int SLOTS = 4;   // up to 256 experts
+    unsigned long long key[SLOTS];
+    float weight[SLOTS];
+    bad = ~0ull;
+#pragma unroll
+    for (int k = 0; k < SLOTS; ++k) {
+        const int e = lane + 64 * k;
+        key[k] = 0;
+        weight[k] = 0.0f;
+        if (e < a.n_experts) {
+            const float l = a.logits[e];
+            float score = l;
+            if (a.mode == 1) {
+                const float b = a.bias[e];
+                const float w = sigmoid_ref(l);
+                score = __fadd_rn(w, b);
+                weight[k] = w;
+                const unsigned long long code = !isfinite(l) ? 0ull : !isfinite(b) ? 1ull : !isfinite(score) ? 2ull : 3ull;
+                if (code < 3) bad = min(bad, ((unsigned long long)e << 2) | code);
+            } else if (!isfinite(l)) {
+                bad = min(bad, (unsigned long long)e << 2);
+            }
+            key[k] = sel_key(score, (uint32_t)e);   // never 0: 0 marks empty / taken
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long o = __shfl_xor(bad, off, 64);
+        bad = o < bad ? o : bad;
+    }
+
+    // top_k rounds of a wave arg-max; winners come out in rank order.
+    uint32_t win_id[MOE_MAX_ROUTED];
+    float win_score[MOE_MAX_ROUTED], win_w[MOE_MAX_ROUTED];
+#pragma unroll
+    for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
+        win_id[r] = 0, win_score[r] = 0.0f, win_w[r] = 0.0f;
+        if (r >= a.top_k) continue;
+        unsigned long long best = key[0];
+        int bk = 0;
+#pragma unroll
+        for (int k = 1; k < SLOTS; ++k)
+            if (key[k] > best) best = key[k], bk = k;
+        unsigned long long m = best;
+        for (int off = 32; off >= 1; off >>= 1) {
+            const unsigned long long o = __shfl_xor(m, off, 64);
+            m = o > m ? o : m;
+        }
+        const uint32_t id = 0xffffffffu - (uint32_t)(m & 0xffffffffull);
+        const int owner = (int)(id & 63);
+        const int slot = (int)(id >> 6);
+        const float wv = __shfl(weight[bk], owner, 64);
+        win_id[r] = id;
+        win_w[r] = wv;
+        win_score[r] = a.mode == 1 ? 0.0f : a.logits[id];
+        if (lane == owner) {
+#pragma unroll
+            for (int k = 0; k < SLOTS; ++k)
+                if (k == slot) key[k] = 0;
+        }
+    }
+    float coef[MOE_MAX_ROUTED];
+    if (a.mode == 1) {
+        float wsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < MOE_MAX_ROUTED; ++r)
+            if (r < a.top_k) wsum = __fadd_rn(wsum, win_w[r]);
+        const float floor_ = 0.000061035156f;   // 2^-14, routing.rs:5
+        if (!(wsum >= floor_)) wsum = floor_;
+#pragma unroll
+        for (int r = 0; r < MOE_MAX_ROUTED; ++r) coef[r] = __fmul_rn(__fdiv_rn(win_w[r], wsum), a.weight_scale);
+    } else {
+        const float mx = win_score[0];
+        float ev[MOE_MAX_ROUTED];
+        float s = 0.0f;
+#pragma unroll
+        for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
+            ev[r] = expf_libm(__fsub_rn(win_score[r], mx));
+            if (r < a.top_k) s = __fadd_rn(s, ev[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < MOE_MAX_ROUTED; ++r) coef[r] = __fdiv_rn(ev[r], s);
+    }
+    // Output ascending by id (routing.rs:105): position = winners with a smaller id.
+    out.n = a.top_k;
+    out.pad = 0;
+#pragma unroll
+    for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
+        out.ids[r] = 0;
+        out.coefs[r] = 0.0f;
+    }
+#pragma unroll
+    for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
+        if (r >= a.top_k) continue;
+        int pos = 0;
+#pragma unroll
+        for (int q = 0; q < MOE_MAX_ROUTED; ++q) pos += (q < a.top_k && win_id[q] < win_id[r]) ? 1 : 0;
+#pragma unroll
+        for (int q = 0; q < MOE_MAX_ROUTED; ++q)
+            if (q == pos) out.ids[q] = win_id[r], out.coefs[q] = coef[r];
+    }
+}
+
+}  // namespace lbh

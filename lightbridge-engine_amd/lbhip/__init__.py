@@ -331,8 +331,9 @@ class MoeLayer:
         self._keep = (experts, shared)
         self.n_experts = n
 
-    def set_tiles(self, tile_r: int = 32, tile_s: int = 32, tile_d: int = 16) -> None:
-        st = lib().lbh_moe_set_tiles(self.handle, tile_r, tile_s, tile_d)
+    def set_tiles(self, wg_routed: int, wg_shared: int, tile_d: int = 16) -> None:
+        """Workgroups of the routed / shared gate-up streams, output rows per down workgroup."""
+        st = lib().lbh_moe_set_tiles(self.handle, wg_routed, wg_shared, tile_d)
         if st:
             raise KernelError(LbhError(status=st))
 
