@@ -1,18 +1,29 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized-dot hot path on one MI355X.
 
-Workload "matvec": one routed-expert decode pass for one
-token — Q8_K-quantize x[4096] -> IQ2_S gate matvec 1536x4096 -> Q8_K-quantize
-h[1536] -> IQ3_S down matvec 4096x1536.  Weights are random-from-seed
-(synthetic data, no checkpoint).  Inputs are resident in HBM before timing;
-every step reads a different copy of the weights (> 512 MB of copies in
-rotation, twice the 256 MB Infinity Cache) so the bytes come from HBM.
-Launches are captured in a HIP graph (torch.cuda.CUDAGraph) and replayed.
+Headline workload: one routed expert's decode pass for
+one token -- Q8_K(x[4096]) + IQ2_S gate matvec 1536x4096, then Q8_K(h[1536]) +
+IQ3_S down matvec 4096x1536, each a single fused kernel.  `value` is the
+algorithmic bytes of that step (weights + Q8_K activations + f32 outputs)
+divided by the step time, in GB/s.
 
-Prints ONE JSON line (rank 0).  `value` = algorithmic bytes moved per step /
-step time, in GB/s.  `roofline` reports the dominant kernel measured alone.
-`cpu_baseline` times the oracle's AVX2 restatement of the reference CPU path on
-this host's cores for a bounded sample of the same step.
+Secondary workloads in the same JSON line:
+  configs[0]  Q4_K x Q8_K matvec 4096x4096 (the reference's CPU-runnable case);
+  configs[2]  the full MoE FFN block of one token: 192 routed experts (IQ2_S
+              gate/up 1536x4096, IQ3_S down 4096x1536), top-8 of an F32 4096x192
+              router with softmax weights, a Q4_K/Q5_K shared expert with ffn
+              4096; reported with the routing given (moe_routed_by_id_into's
+              boundary) and with the device router in the step.
+
+Weights are random-from-seed (synthetic; no checkpoint).  Inputs are resident
+in HBM before timing; launches are captured in HIP graphs and replayed; every
+matvec step reads a different copy of the weights (> 512 MB in rotation, twice
+the 256 MB Infinity Cache) and the MoE steps cycle through 1.3 GB of experts,
+so weight bytes come from HBM.  `roofline` is the dominant kernel of the
+headline step, timed alone with HIP events on the stream it runs on.
+`cpu_baseline` times the CPU oracle (a C restatement of the reference's AVX2
+path, rows over a thread pool as the reference's rayon pool) on this host for a
+bounded sample of the same work.
 """
 from __future__ import annotations
 
@@ -30,57 +41,270 @@ for p in (ROOT, ROOT / "lightbridge-engine_amd"):
         sys.path.insert(0, str(p))
 
 HBM_PEAK_GBS = 8000.0
-HIDDEN, FFN = 4096, 1536
-# Algorithmic bytes (weights + Q8_K activation + f32 output) per matvec.
-GATE_BYTES = FFN * (HIDDEN // 256) * 82 + (HIDDEN // 256) * 292 + FFN * 4     # 2,026,048
-DOWN_BYTES = HIDDEN * (FFN // 256) * 110 + (FFN // 256) * 292 + HIDDEN * 4     # 2,721,496
+HIDDEN, FFN, N_EXPERTS, TOP_K = 4096, 1536, 192, 8
+Q8 = lambda k: k // 256 * 292  # noqa: E731
+GATE_BYTES = FFN * (HIDDEN // 256) * 82 + Q8(HIDDEN) + FFN * 4          # 2,026,048
+DOWN_BYTES = HIDDEN * (FFN // 256) * 110 + Q8(FFN) + HIDDEN * 4         # 2,721,496
 STEP_BYTES = GATE_BYTES + DOWN_BYTES
+Q4K_BYTES = HIDDEN * (HIDDEN // 256) * 144 + Q8(HIDDEN) + HIDDEN * 4    # 9,458,240
+MOE_WEIGHT_BYTES = (TOP_K * (2 * FFN * 16 * 82 + HIDDEN * 6 * 110) + 2 * HIDDEN * 16 * 144
+                    + HIDDEN * 16 * 176 + N_EXPERTS * HIDDEN * 4)      # 87,425,024 per token
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--steps", type=int, default=2000, help="timed steps of the headline workload")
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--copies", type=int, default=0, help="weight copies in rotation (0 = enough for 512 MB)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--lpu", type=int, default=0, help="lanes per (row, block) unit (0 = library default)")
+    ap.add_argument("--moe-tokens", type=int, default=256, help="timed tokens of the MoE block workloads")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE block workload")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on each CPU baseline sample")
+    ap.add_argument("--lpu", type=int, default=0, help="matvec lanes per (row, block) unit (0 = library default)")
     return ap.parse_args()
 
 
-def cpu_baseline(w_gate, w_down, x, seconds: float):
-    """Oracle AVX2 path (restating the reference's vec_dot_q8_k_cpu + rayon rows):
-    the same step on host cores, bounded to ~`seconds` of work."""
+class Timer:
+    """HIP-graph replay timing on one stream (events recorded on that stream)."""
+
+    def __init__(self, torch, stream):
+        self.torch, self.stream = torch, stream
+
+    def graph(self, fn):
+        torch, s = self.torch, self.stream
+        with torch.cuda.stream(s):
+            fn()
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                fn()
+        return g
+
+    def time(self, g, reps):
+        torch, s = self.torch, self.stream
+        with torch.cuda.stream(s):
+            g.replay()
+            s.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(reps):
+                g.replay()
+            e1.record(s)
+            e1.synchronize()
+        return e0.elapsed_time(e1) * 1e-3   # seconds
+
+
+def cpu_threads():
+    from oracle import lb_oracle as orc
+    return min(orc.default_threads(), 16)
+
+
+def cpu_matvec_step(w_gate, w_down, seconds):
+    """Oracle AVX2 path for the headline step: gemv_into (quantize + row dots) of
+    the gate, then of the down projection on its output."""
     import numpy as np
     from oracle import lb_oracle as orc
-
-    threads = min(orc.default_threads(), 16)
+    threads = cpu_threads()
     ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
     mg = orc.make_matrix(22, FFN, HIDDEN, w_gate)
     md = orc.make_matrix(21, HIDDEN, FFN, w_down)
-    h = np.random.default_rng(5).standard_normal(FFN).astype(np.float32)
-    orc.gemv(ex, mg, x)
+    x = np.random.default_rng(5).standard_normal(HIDDEN).astype(np.float32)
+    h = orc.gemv(ex, mg, x)
     n, t0 = 0, time.perf_counter()
     while True:
-        orc.gemv(ex, mg, x)          # quantize x + gate rows
-        orc.gemv(ex, md, h)          # quantize h + down rows
+        h = orc.gemv(ex, mg, x)
+        orc.gemv(ex, md, h)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
+        if (el >= seconds and n >= 3) or el >= 4 * seconds:
             break
-    gbs = STEP_BYTES * n / el / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} steps of the same workload (quantize+IQ2_S gate+quantize+IQ3_S down) in {el:.1f} s, "
-                      f"oracle AVX2 restatement, {threads} threads of {os.cpu_count()} logical CPUs",
-            "ms_per_step": round(el / n * 1e3, 4)}
+    return {"value": round(STEP_BYTES * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(el / n * 1e3, 4),
+            "sample": f"{n} steps of the headline step (Q8_K + IQ2_S gate 1536x4096, Q8_K + IQ3_S down "
+                      f"4096x1536) in {el:.2f} s; oracle AVX2 restatement, rows over {threads} threads "
+                      f"(ceil(nproc/2), the reference's default) of {os.cpu_count()} logical CPUs"}
+
+
+def cpu_q4k(w, seconds):
+    import numpy as np
+    from oracle import lb_oracle as orc
+    threads = cpu_threads()
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
+    m = orc.make_matrix(12, HIDDEN, HIDDEN, w)
+    x = np.random.default_rng(6).standard_normal(HIDDEN).astype(np.float32)
+    orc.gemv(ex, m, x)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.gemv(ex, m, x)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 3) or el >= 4 * seconds:
+            break
+    return {"value": round(Q4K_BYTES * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n} Q4_K 4096x4096 gemv_into calls in {el:.2f} s, {threads} threads"}
+
+
+def cpu_moe(experts_np, shared_np, router_w, xs, seconds):
+    """Oracle MoE block per token: router logits + softmax top-8, then
+    moe_routed_by_id_into with its preflight pass (the reference's structure) and
+    the single-pass variant."""
+    import numpy as np
+    from oracle import lb_oracle as orc
+    threads = cpu_threads()
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
+    orc_exp = [orc.make_expert(orc.make_matrix(22, FFN, HIDDEN, g), orc.make_matrix(22, FFN, HIDDEN, u),
+                               orc.make_matrix(21, HIDDEN, FFN, d)) for g, u, d in experts_np]
+    sg, su, sd = shared_np
+    orc_sh = orc.make_expert(orc.make_matrix(12, HIDDEN, HIDDEN, sg), orc.make_matrix(12, HIDDEN, HIDDEN, su),
+                             orc.make_matrix(13, HIDDEN, HIDDEN, sd))
+    out = {}
+    for preflight in (True, False):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            x = xs[n % len(xs)]
+            ids, coefs = orc.route_softmax_topk(orc.router_logits_f32(router_w, x), TOP_K)
+            orc.moe_routed_by_id(ex, ids, coefs, orc_exp, orc_sh, x, preflight=preflight)
+            n += 1
+            el = time.perf_counter() - t0
+            if (el >= seconds / 2 and n >= 2) or el >= 2 * seconds:
+                break
+        out["preflight" if preflight else "single_pass"] = (n / el, n, el)
+    best = max(v[0] for v in out.values())
+    return {"value": round(best, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "faithful_with_preflight_tokens_per_s": round(out["preflight"][0], 3),
+            "single_pass_tokens_per_s": round(out["single_pass"][0], 3),
+            "sample": f"{out['preflight'][1]} + {out['single_pass'][1]} tokens through the 192-expert block "
+                      f"(router + top-8 + experts + shared) in {out['preflight'][2] + out['single_pass'][2]:.2f} s, "
+                      f"{threads} threads; value is the faster (single-pass) variant"}
+
+
+def bench_matvec_step(args, be, timer, torch, np, synth):
+    w_gate = synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, seed=101)
+    w_down = synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, seed=102)
+    copies = max(2, math.ceil(512e6 / (w_gate.nbytes + w_down.nbytes)) + 4)
+    gate_dev = torch.from_numpy(w_gate.reshape(-1)).cuda()
+    down_dev = torch.from_numpy(w_down.reshape(-1)).cuda()
+    gates = [be.upload(synth.IQ2_S, FFN, HIDDEN, gate_dev) for _ in range(copies)]
+    downs = [be.upload(synth.IQ3_S, HIDDEN, FFN, down_dev) for _ in range(copies)]
+    del gate_dev, down_dev
+    xs = torch.from_numpy(np.stack([synth.random_activations(HIDDEN, seed=200 + i) for i in range(copies)])).cuda()
+    q8x = torch.zeros((copies, Q8(HIDDEN)), dtype=torch.uint8, device="cuda")
+    hs = torch.zeros((copies, FFN), dtype=torch.float32, device="cuda")
+    q8h = torch.zeros((copies, Q8(FFN)), dtype=torch.uint8, device="cuda")
+    ys = torch.zeros((copies, HIDDEN), dtype=torch.float32, device="cuda")
+
+    def step_all():
+        for c in range(copies):
+            be.gemv_f32(gates[c], xs[c], hs[c], q8x[c])      # Q8_K(x) + IQ2_S gate, one launch
+            be.gemv_f32(downs[c], hs[c], ys[c], q8h[c])      # Q8_K(h) + IQ3_S down, one launch
+
+    g = timer.graph(step_all)
+    reps_w = max(1, args.warmup // copies)
+    reps = max(1, math.ceil(args.steps / copies))
+    timer.time(g, reps_w)
+    t = timer.time(g, reps)
+    steps = reps * copies
+    ms_per_step = t / steps * 1e3
+    g_gate = timer.graph(lambda: [be.gemv_f32(gates[c], xs[c], hs[c]) for c in range(copies)])
+    g_down = timer.graph(lambda: [be.gemv_f32(downs[c], hs[c], ys[c]) for c in range(copies)])
+    n_k = max(1, 2000 // copies)
+    gate_us = timer.time(g_gate, n_k) / (n_k * copies) * 1e6
+    down_us = timer.time(g_down, n_k) / (n_k * copies) * 1e6
+
+    # parity spot check of the last step against the oracle (not timed)
+    from oracle import lb_oracle as orc
+    c = (steps - 1) % copies
+    y_ref = orc.gemv_prequantized(orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, 8, True),
+                                  orc.make_matrix(synth.IQ3_S, HIDDEN, FFN, w_down), q8h[c].cpu().numpy())
+    parity = bool(np.array_equal(ys[c].cpu().numpy().view(np.uint32), y_ref.view(np.uint32)))
+    for m in gates + downs:
+        m.close()
+    return dict(w_gate=w_gate, w_down=w_down, copies=copies, steps=steps, warmup=reps_w * copies,
+                ms_per_step=ms_per_step, gate_us=gate_us, down_us=down_us, parity=parity)
+
+
+def bench_q4k(args, be, timer, torch, np, synth):
+    w = synth.random_matrix(synth.Q4_K, HIDDEN, HIDDEN, seed=111)
+    copies = math.ceil(600e6 / w.nbytes)
+    wd = torch.from_numpy(w.reshape(-1)).cuda()
+    ms = [be.upload(synth.Q4_K, HIDDEN, HIDDEN, wd) for _ in range(copies)]
+    del wd
+    xs = torch.randn(copies, HIDDEN, device="cuda")
+    ys = torch.zeros(copies, HIDDEN, device="cuda")
+    g = timer.graph(lambda: [be.gemv_f32(ms[c], xs[c], ys[c]) for c in range(copies)])
+    timer.time(g, 3)
+    reps = max(3, 1000 // copies)
+    us = timer.time(g, reps) / (reps * copies) * 1e6
+    for m in ms:
+        m.close()
+    return w, {"workload": "configs[0]: Q4_K x Q8_K matvec 4096x4096, batch 1 (fused Q8_K + matvec kernel)",
+               "us_per_matvec": round(us, 3), "GB/s": round(Q4K_BYTES / us / 1e3, 2),
+               "roofline_frac": round(Q4K_BYTES / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies}
+
+
+def bench_moe(args, be, timer, torch, np, synth, lbhip):
+    g = torch.from_numpy(synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, 301).reshape(-1)).cuda()
+    u = torch.from_numpy(synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, 302).reshape(-1)).cuda()
+    d = torch.from_numpy(synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, 303).reshape(-1)).cuda()
+    # 192 distinct experts: block-rotated copies of three seeded matrices.
+    gate_t = [torch.roll(g, 82 * e) for e in range(N_EXPERTS)]
+    up_t = [torch.roll(u, 82 * e) for e in range(N_EXPERTS)]
+    down_t = [torch.roll(d, 110 * e) for e in range(N_EXPERTS)]
+    experts = [(be.upload(synth.IQ2_S, FFN, HIDDEN, gate_t[e]), be.upload(synth.IQ2_S, FFN, HIDDEN, up_t[e]),
+                be.upload(synth.IQ3_S, HIDDEN, FFN, down_t[e])) for e in range(N_EXPERTS)]
+    shared_np = (synth.random_matrix(synth.Q4_K, HIDDEN, HIDDEN, 304), synth.random_matrix(synth.Q4_K, HIDDEN, HIDDEN, 305),
+                 synth.random_matrix(synth.Q5_K, HIDDEN, HIDDEN, 306))
+    shared = (be.upload(synth.Q4_K, HIDDEN, HIDDEN, shared_np[0]), be.upload(synth.Q4_K, HIDDEN, HIDDEN, shared_np[1]),
+              be.upload(synth.Q5_K, HIDDEN, HIDDEN, shared_np[2]))
+    moe = be.moe_create(experts, shared)
+    router_w = synth.router_weights(N_EXPERTS, HIDDEN, 307)
+    router = lbhip.Router(be, router_w)
+    T = args.moe_tokens
+    xs_np = [synth.random_activations(HIDDEN, seed=400 + i) for i in range(T)]
+    xs = torch.from_numpy(np.stack(xs_np)).cuda()
+    ys = torch.zeros(T, HIDDEN, device="cuda")
+    routes = [router.route_into(xs[i], TOP_K) for i in range(T)]   # device router, before timing
+    hit = len({int(e) for r in routes for e in r[0]})
+
+    g_host = timer.graph(lambda: [be.moe_forward(moe, routes[i][0], routes[i][1], xs[i], ys[i]) for i in range(T)])
+    timer.time(g_host, 1)
+    reps = 3
+    us_host = timer.time(g_host, reps) / (reps * T) * 1e6
+    g_dev = timer.graph(lambda: [lbhip.moe_block_forward(be, moe, router, xs[i], ys[i], TOP_K) for i in range(T)])
+    timer.time(g_dev, 1)
+    us_dev = timer.time(g_dev, reps) / (reps * T) * 1e6
+
+    # parity spot check (not timed): token 0 through the oracle
+    from oracle import lb_oracle as orc
+    torch.cuda.synchronize()
+    host = lambda t: t.cpu().numpy()  # noqa: E731
+    experts_np = [(host(gate_t[e]), host(up_t[e]), host(down_t[e])) for e in range(N_EXPERTS)]
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, cpu_threads(), True)
+    orc_exp = [orc.make_expert(orc.make_matrix(22, FFN, HIDDEN, a), orc.make_matrix(22, FFN, HIDDEN, b),
+                               orc.make_matrix(21, HIDDEN, FFN, c)) for a, b, c in experts_np]
+    orc_sh = orc.make_expert(orc.make_matrix(12, HIDDEN, HIDDEN, shared_np[0]),
+                             orc.make_matrix(12, HIDDEN, HIDDEN, shared_np[1]),
+                             orc.make_matrix(13, HIDDEN, HIDDEN, shared_np[2]))
+    want_ids, want_coefs = orc.route_softmax_topk(orc.router_logits_f32(router_w, xs_np[T - 1]), TOP_K)
+    want = orc.moe_routed_by_id(ex, want_ids, want_coefs, orc_exp, orc_sh, xs_np[T - 1])
+    parity = bool(np.array_equal(host(ys[T - 1]).view(np.uint32), want.view(np.uint32)))
+    res = {"workload": "configs[2]: MoE FFN block, 1 token: 192 experts (IQ2_S gate/up 1536x4096, IQ3_S down "
+                       "4096x1536), top-8 softmax of an F32 4096x192 router, Q4_K/Q5_K shared expert ffn 4096",
+           "tokens_timed": T * reps, "distinct_experts_hit": hit,
+           "routing_given": {"us_per_token": round(us_host, 2), "tokens_per_s": round(1e6 / us_host, 1),
+                             "GB/s": round((MOE_WEIGHT_BYTES - N_EXPERTS * HIDDEN * 4) / us_host / 1e3, 1)},
+           "with_device_router": {"us_per_token": round(us_dev, 2), "tokens_per_s": round(1e6 / us_dev, 1),
+                                  "GB/s": round(MOE_WEIGHT_BYTES / us_dev / 1e3, 1)},
+           "algorithmic_weight_bytes_per_token": MOE_WEIGHT_BYTES,
+           "parity_last_token_bit_exact": parity}
+    return res, experts_np, shared_np, router_w, xs_np
 
 
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs on a "
-              f"single MI355X; see DESIGN.md for how the path shards)", file=sys.stderr)
+              f"single MI355X; DESIGN.md describes how the path shards)", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -90,117 +314,60 @@ def main():
 
     be = lbhip.HipBackend(0)
     be.set_tuning(be.TUNE_GEMV_LPU, args.lpu)
-    w_gate = synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, seed=101)
-    w_down = synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, seed=102)
-    copies = args.copies or max(2, math.ceil(512e6 / (w_gate.nbytes + w_down.nbytes)) + 4)
-    gate_dev = torch.from_numpy(w_gate.reshape(-1)).cuda()
-    down_dev = torch.from_numpy(w_down.reshape(-1)).cuda()
-    gates = [be.upload(synth.IQ2_S, FFN, HIDDEN, gate_dev) for _ in range(copies)]
-    downs = [be.upload(synth.IQ3_S, HIDDEN, FFN, down_dev) for _ in range(copies)]
-    del gate_dev, down_dev
-
-    x = synth.random_activations(HIDDEN, seed=103)
-    xs = torch.from_numpy(np.stack([synth.random_activations(HIDDEN, seed=200 + i) for i in range(copies)])).cuda()
-    q8x = torch.zeros((copies, HIDDEN // 256 * 292), dtype=torch.uint8, device="cuda")
-    hs = torch.zeros((copies, FFN), dtype=torch.float32, device="cuda")
-    q8h = torch.zeros((copies, FFN // 256 * 292), dtype=torch.uint8, device="cuda")
-    ys = torch.zeros((copies, HIDDEN), dtype=torch.float32, device="cuda")
-
-    def step(i):
-        c = i % copies
-        be.gemv_f32(gates[c], xs[c], hs[c], q8x[c])      # Q8_K(x) + IQ2_S gate, one launch
-        be.gemv_f32(downs[c], hs[c], ys[c], q8h[c])      # Q8_K(h) + IQ3_S down, one launch
-
-    # Capture one rotation (copies steps) per graph; replay it.
-    per_graph = copies
     stream = torch.cuda.Stream()
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        be.set_stream(stream)
-        for i in range(per_graph):   # eager warm-up on the capture stream
-            step(i)
-        stream.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for i in range(per_graph):
-                step(i)
-        # dominant kernel alone: the IQ3_S down matvec over every copy
-        g_down = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_down, stream=stream):
-            for i in range(per_graph):
-                be.gemv_f32(downs[i], hs[i], ys[i])
-        g_gate = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g_gate, stream=stream):
-            for i in range(per_graph):
-                be.gemv_f32(gates[i], xs[i], hs[i])
+    be.set_stream(stream)
+    timer = Timer(torch, stream)
 
-        reps_w = max(1, args.warmup // per_graph)
-        reps = max(1, math.ceil(args.steps / per_graph))
-        for _ in range(reps_w):
-            g.replay()
-        stream.synchronize()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0.record(stream)
-        for _ in range(reps):
-            g.replay()
-        t1.record(stream)
-        t1.synchronize()
-        ms_total = t0.elapsed_time(t1)
-        steps = reps * per_graph
-        ms_per_step = ms_total / steps
+    mv = bench_matvec_step(args, be, timer, torch, np, synth)
+    w_q4k, q4k = bench_q4k(args, be, timer, torch, np, synth)
+    moe = None
+    if not args.no_moe:
+        moe, experts_np, shared_np, router_w, xs_np = bench_moe(args, be, timer, torch, np, synth, lbhip)
 
-        def kernel_avg_us(graph):
-            graph.replay()
-            stream.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            n_rep = max(1, 2000 // per_graph)
-            e0.record(stream)
-            for _ in range(n_rep):
-                graph.replay()
-            e1.record(stream)
-            e1.synchronize()
-            return e0.elapsed_time(e1) * 1e3 / (n_rep * per_graph)
-
-        down_us = kernel_avg_us(g_down)
-        gate_us = kernel_avg_us(g_gate)
-
-    # parity spot check of the last step against the oracle (not timed)
-    from oracle import lb_oracle as orc
-    c = (steps - 1) % copies
-    q8h_last = q8h[c].cpu().numpy()
-    y_ref = orc.gemv_prequantized(orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, 8, True),
-                                  orc.make_matrix(synth.IQ3_S, HIDDEN, FFN, w_down), q8h_last)
-    parity = bool(np.array_equal(ys[c].cpu().numpy().view(np.uint32), y_ref.view(np.uint32)))
-
-    value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
-    down_gbs = DOWN_BYTES / (down_us * 1e-6) / 1e9
+    value = STEP_BYTES / (mv["ms_per_step"] * 1e-3) / 1e9
+    if mv["down_us"] >= mv["gate_us"]:
+        dom = ("k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)", mv["down_us"], DOWN_BYTES)
+    else:
+        dom = ("k_gemv<IQ2_S, fused Q8_K> (gate 1536x4096)", mv["gate_us"], GATE_BYTES)
+    achieved = dom[2] / (dom[1] * 1e-6) / 1e9
     line = {
         "metric": "quant matvec HBM GB/s (% of MI355X peak); MoE-block decode tokens/s",
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": reps_w * per_graph,
-        "ms_per_step": round(ms_per_step, 6),
+        "steps": mv["steps"],
+        "warmup": mv["warmup"],
+        "ms_per_step": round(mv["ms_per_step"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8xi8->i32, f32 fold",
-        "data": "synthetic (random-from-seed weights and activations)",
-        "config": {"workload": "configs[1]: IQ2_S gate 1536x4096 + IQ3_S down 4096x1536, batch 1 (1 token)",
-                   "weight_copies_in_rotation": copies,
-                   "rotation_bytes": copies * (w_gate.nbytes + w_down.nbytes),
-                   "step": "Q8_K(x)+IQ2_S gate -> Q8_K(h)+IQ3_S down (2 fused kernels, HIP graph)", "lpu": args.lpu,
-                   "algorithmic_bytes_per_step": STEP_BYTES},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)",
-                     "achieved": round(down_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(down_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "avg_launch_us": round(down_us, 3), "algorithmic_bytes_per_launch": DOWN_BYTES},
-        "kernels_us": {"iq2s_gate": round(gate_us, 3), "iq3s_down": round(down_us, 3)},
-        "parity_last_step_bit_exact": parity,
+        "dtype": "i8xi8->i32 integer dots, f32 scale fold",
+        "data": "synthetic (random-from-seed weights and activations; no checkpoint)",
+        "config": {"workload": "configs[1]: IQ2_S gate 1536x4096 + IQ3_S down 4096x1536 matvecs, batch 1 "
+                               "(one routed expert's decode pass, one token)",
+                   "step": "Q8_K(x)+IQ2_S gate -> Q8_K(h)+IQ3_S down: 2 fused kernels per step, HIP graph",
+                   "weight_copies_in_rotation": mv["copies"],
+                   "rotation_bytes": mv["copies"] * (mv["w_gate"].nbytes + mv["w_down"].nbytes),
+                   "algorithmic_bytes_per_step": STEP_BYTES, "lpu": args.lpu},
+        "roofline": {"bound": "hbm", "kernel": dom[0], "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2]},
+        "kernels_us": {"iq2s_gate": round(mv["gate_us"], 3), "iq3s_down": round(mv["down_us"], 3)},
+        "parity_last_step_bit_exact": mv["parity"],
+        "q4k_matvec": q4k,
     }
+    if moe is not None:
+        line["moe_block"] = moe
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(w_gate, w_down, x, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds)
+        cq = cpu_q4k(w_q4k, args.cpu_seconds / 2)
+        q4k["cpu_baseline"] = cq
+        q4k["speedup_vs_cpu"] = round(q4k["GB/s"] / cq["value"], 1)
+        if moe is not None:
+            cm = cpu_moe(experts_np, shared_np, router_w, xs_np, args.cpu_seconds)
+            moe["cpu_baseline"] = cm
+            moe["speedup_vs_cpu"] = round(moe["with_device_router"]["tokens_per_s"] / cm["value"], 1)
+            moe["speedup_vs_cpu_routing_given"] = round(moe["routing_given"]["tokens_per_s"] / cm["value"], 1)
     print(json.dumps(line), flush=True)
 
 
