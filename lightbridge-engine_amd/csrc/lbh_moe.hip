@@ -159,15 +159,15 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
                               wg_r * MOE_WAVES, smem);
 }
 
-// Block decode, first launch: router chains (one wave per 64 experts, in the
-// first workgroups) beside the shared expert's gate/up stream, which does not
-// depend on the routing.
+// Block decode, first launch: router chains (RT_EXPERTS experts per
+// workgroup, in the first workgroups) beside the shared expert's gate/up
+// stream, which does not depend on the routing.
 template <int TYS, int LPUS>
 __global__ void __launch_bounds__(MOE_THREADS) k_moe_router_shared(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int rw = (a.router.n_experts + 63) / 64;
+    const int rw = (a.router.n_experts + RT_EXPERTS - 1) / RT_EXPERTS;
     if ((int)blockIdx.x < rw) {
-        if (threadIdx.x < 64) router_chain_wave(a.router, blockIdx.x * 64);
+        router_chain_wg(a.router, blockIdx.x * RT_EXPERTS, smem);
         return;
     }
     gate_up_stream<TYS, LPUS>(a, SharedSlot{a, a.route.n}, 1, a.ffn_s, (blockIdx.x - rw) * MOE_WAVES,
@@ -351,15 +351,15 @@ static hipError_t down_typed(const MoeArgs &a, hipStream_t s) {
 
 hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s) {
     const int nb = a.hidden / 256;
-    const int rw = (a.router.n_experts + 63) / 64;
+    const int rw = (a.router.n_experts + RT_EXPERTS - 1) / RT_EXPERTS;
     const int ts = a.shared.gate.type;
     const int grid = rw + a.tiles_s;
+    const int lq = gate_up_lds<T_Q4_K>(nb) > RT_LDS ? gate_up_lds<T_Q4_K>(nb) : RT_LDS;
+    const int li = gate_up_lds<T_IQ2_S>(nb) > RT_LDS ? gate_up_lds<T_IQ2_S>(nb) : RT_LDS;
     if (ts == T_Q4_K) {
-        hipLaunchKernelGGL((k_moe_router_shared<T_Q4_K, moe_lpu<T_Q4_K>()>), dim3(grid), dim3(MOE_THREADS),
-                           gate_up_lds<T_Q4_K>(nb), s, a);
+        hipLaunchKernelGGL((k_moe_router_shared<T_Q4_K, moe_lpu<T_Q4_K>()>), dim3(grid), dim3(MOE_THREADS), lq, s, a);
     } else if (ts == T_IQ2_S) {
-        hipLaunchKernelGGL((k_moe_router_shared<T_IQ2_S, moe_lpu<T_IQ2_S>()>), dim3(grid), dim3(MOE_THREADS),
-                           gate_up_lds<T_IQ2_S>(nb), s, a);
+        hipLaunchKernelGGL((k_moe_router_shared<T_IQ2_S, moe_lpu<T_IQ2_S>()>), dim3(grid), dim3(MOE_THREADS), li, s, a);
     } else {
         return hipErrorInvalidValue;
     }

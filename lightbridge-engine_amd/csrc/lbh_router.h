@@ -17,37 +17,87 @@ __device__ __forceinline__ unsigned long long sel_key(float score, uint32_t id) 
     return ((unsigned long long)b << 32) | (0xffffffffu - id);
 }
 
-// One wave: lanes are experts e0 + lane.
-__device__ __forceinline__ void router_chain_wave(const RouterArgs &a, int e0) {
-    const int lane = threadIdx.x & 63;
-    const int e = e0 + lane;
+// Router chains of RT_EXPERTS experts [e0, e0 + RT_EXPERTS) by one
+// 256-thread workgroup.  Wave 0 runs the chains (lane = expert); waves 1-3
+// stream the weights into a ring of RT_SLOTS chunks in LDS (RT_STEPS steps of
+// four inputs each), producer wave w owning the chunks congruent to w - 1
+// mod 3.  Slots change hands through workgroup-scope release/acquire flags:
+// ready[slot] = index of the chunk it holds, done = last chunk consumed.
+// Each wait is bounded, so no wave can wait forever.
+constexpr int RT_EXPERTS = 8;
+constexpr int RT_STEPS = 64;
+constexpr int RT_SLOTS = 4;
+constexpr int RT_LDS = RT_SLOTS * RT_STEPS * RT_EXPERTS * 16 + 64;
+
+__device__ __forceinline__ int lds_acquire(const int *p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_release(int *p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uint8_t *lds) {
+    float4 *ring = reinterpret_cast<float4 *>(lds);
+    int *ready = reinterpret_cast<int *>(lds + RT_SLOTS * RT_STEPS * RT_EXPERTS * 16);
+    int *done = ready + RT_SLOTS;
+    const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
     const int n = a.n_experts;
-    const bool on = e < n;
-    const float4 *wt = reinterpret_cast<const float4 *>(a.w);
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-    const int steps = a.hidden / 4;   // multiple of 64
-    constexpr int P = 8;
-    float4 cur[P], nxt[P];
+    const int nch = a.hidden / (4 * RT_STEPS);   // hidden is a multiple of 256
+    constexpr long long SPIN = 1ll << 22;
+    if (tid < RT_SLOTS) ready[tid] = -1;
+    if (tid == 0) *done = -1;
+    __syncthreads();
+
+    if (wid >= 1 && wid <= 3) {
+        const float4 *wt = reinterpret_cast<const float4 *>(a.w);
+        const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+        for (int c = wid - 1; c < nch; c += 3) {
+            for (long long k = 0; k < SPIN && lds_acquire(done) < c - RT_SLOTS; ++k) __builtin_amdgcn_s_sleep(1);
+            float4 v[RT_STEPS * RT_EXPERTS / 64], xv[RT_STEPS * RT_EXPERTS / 64];
 #pragma unroll
-    for (int k = 0; k < P; ++k) cur[k] = on ? wt[(long long)k * n + e] : make_float4(0, 0, 0, 0);
-    float sum = 0.0f;
-    for (int j = 0; j < steps; j += P) {
-        if (j + P < steps) {
+            for (int k = 0; k < RT_STEPS * RT_EXPERTS / 64; ++k) {
+                const int idx = lane + 64 * k;
+                const int step = idx / RT_EXPERTS, e = e0 + idx % RT_EXPERTS;
+                v[k] = e < n ? wt[(long long)(c * RT_STEPS + step) * n + e] : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[k] = x4[c * RT_STEPS + step];
+            }
+            // The ring holds the products w[i] * x[i] (each rounded once, as the
+            // reference's `weight * input_value`), so the chain only adds.
+            float4 *slot = ring + (c % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
 #pragma unroll
-            for (int k = 0; k < P; ++k) nxt[k] = on ? wt[(long long)(j + P + k) * n + e] : make_float4(0, 0, 0, 0);
+            for (int k = 0; k < RT_STEPS * RT_EXPERTS / 64; ++k) {
+                float4 p;
+                p.x = __fmul_rn(v[k].x, xv[k].x), p.y = __fmul_rn(v[k].y, xv[k].y);
+                p.z = __fmul_rn(v[k].z, xv[k].z), p.w = __fmul_rn(v[k].w, xv[k].w);
+                slot[lane + 64 * k] = p;
+            }
+            if (lane == 0) lds_release(&ready[c % RT_SLOTS], c);
         }
+    } else if (wid == 0) {
+        const int l = lane < RT_EXPERTS ? lane : 0;
+        float sum = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+            for (long long k = 0; k < SPIN && lds_acquire(&ready[c % RT_SLOTS]) != c; ++k) __builtin_amdgcn_s_sleep(1);
+            const float4 *slot = ring + (c % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
+            // Rolling eight-step read-ahead over the fully unrolled chunk: every
+            // index is a compile-time constant, so reads stay in registers.
+            constexpr int P = 8;
+            float4 buf[P];
 #pragma unroll
-        for (int k = 0; k < P; ++k) {
-            const float4 xv = x4[j + k];
-            sum = __fadd_rn(sum, __fmul_rn(cur[k].x, xv.x));
-            sum = __fadd_rn(sum, __fmul_rn(cur[k].y, xv.y));
-            sum = __fadd_rn(sum, __fmul_rn(cur[k].z, xv.z));
-            sum = __fadd_rn(sum, __fmul_rn(cur[k].w, xv.w));
+            for (int k = 0; k < P; ++k) buf[k] = slot[k * RT_EXPERTS + l];
+#pragma unroll
+            for (int j = 0; j < RT_STEPS; ++j) {
+                const float4 p = buf[j % P];
+                if (j + P < RT_STEPS) buf[j % P] = slot[(j + P) * RT_EXPERTS + l];
+                sum = __fadd_rn(sum, p.x);
+                sum = __fadd_rn(sum, p.y);
+                sum = __fadd_rn(sum, p.z);
+                sum = __fadd_rn(sum, p.w);
+            }
+            if (lane == 0) lds_release(done, c);
         }
-#pragma unroll
-        for (int k = 0; k < P; ++k) cur[k] = nxt[k];
+        if (lane < RT_EXPERTS && e0 + lane < n) a.logits[e0 + lane] = sum;
     }
-    if (on) a.logits[e] = sum;
 }
 
 // Called by all 64 lanes of one wave; every lane returns the same route.

@@ -4,9 +4,10 @@
 // src/gemv.rs:286-303): the reference sums w[i] * x[i] strictly in order, each
 // product and sum separately rounded, so each logit is one sequential chain of
 // `hidden` dependent adds.  One lane owns one expert: the weights are stored
-// transposed and interleaved by four (wt[j][e][0..3] = w[e][4j..4j+3]) so a
-// wave's lanes read one contiguous 1 KiB line per step, the loads run eight
-// steps ahead and the products are formed off the add chain.  Selection
+// transposed and interleaved by four (wt[j][e][0..3] = w[e][4j..4j+3]); per
+// workgroup one wave runs eight experts' chains out of an LDS ring that three
+// producer waves keep filled (lbh_router.h), the products formed off the add
+// chain.  Selection
 // (select_route) is a device function shared by the standalone router kernel
 // and the MoE gate/up kernel's prologue:
 //   mode 0  softmax over the top k by (logit desc, id asc), renormalised
@@ -19,7 +20,10 @@
 
 namespace lbh {
 
-__global__ void __launch_bounds__(64) k_router_logits(RouterArgs a) { router_chain_wave(a, blockIdx.x * 64); }
+__global__ void __launch_bounds__(256) k_router_logits(RouterArgs a) {
+    __shared__ __align__(16) uint8_t lds[RT_LDS];
+    router_chain_wg(a, blockIdx.x * RT_EXPERTS, lds);
+}
 
 // Selection of one token from the finished logits, by wave 0 of the block;
 // lane 0 writes the result (and the first invalid lane to *bad_out).
@@ -35,7 +39,7 @@ __global__ void __launch_bounds__(64) k_router_select(RouterArgs a) {
 
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t s) {
     if (a.n_experts < 1 || a.n_experts > 256 || a.hidden % 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_router_logits, dim3((a.n_experts + 63) / 64), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(k_router_logits, dim3((a.n_experts + RT_EXPERTS - 1) / RT_EXPERTS), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -43,7 +47,7 @@ hipError_t launch_router(const RouterArgs &a, hipStream_t s) {
     if (a.n_experts < 1 || a.n_experts > 256 || a.top_k < 1 || a.top_k > MOE_MAX_ROUTED || a.top_k > a.n_experts ||
         a.hidden % 256)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_router_logits, dim3((a.n_experts + 63) / 64), dim3(64), 0, s, a);
+    hipLaunchKernelGGL(k_router_logits, dim3((a.n_experts + RT_EXPERTS - 1) / RT_EXPERTS), dim3(256), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k_router_select, dim3(1), dim3(64), 0, s, a);
