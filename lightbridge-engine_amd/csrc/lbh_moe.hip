@@ -110,10 +110,12 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
     }
 }
 
+// Routed experts of one launch: their gate/up views staged in LDS by the
+// workgroup prologue (a per-item lookup through the device table would put
+// dependent scalar loads in front of every item's weight loads).
 struct RoutedSlots {
-    const MoeArgs &a;
-    const uint32_t *ids;   // LDS copy of the routed ids
-    __device__ const ExpertDev &operator()(int m) const { return a.experts[ids[m]]; }
+    const ExpertDev *views;   // LDS: [n] (gate, up) views; down unused here
+    __device__ const ExpertDev &operator()(int m) const { return views[m]; }
     __device__ int slot(int m) const { return m; }
     __device__ int order(int m) const { return m; }
 };
@@ -130,6 +132,7 @@ template <int TYR, int LPUR, int TYS, int LPUS>
 __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ uint32_t s_ids[MOE_MAX_ROUTED];
+    __shared__ ExpertDev s_views[MOE_MAX_ROUTED];
     if (a.status && a.status->first_bad_input != ~0ull) return;
     const int wg_s = a.has_shared && !a.skip_shared_gate_up ? a.tiles_s : 0;
     if ((int)blockIdx.x < wg_s) {
@@ -154,8 +157,10 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
         s_ids[threadIdx.x] = route_id(a, threadIdx.x < route_n(a) ? threadIdx.x : 0);
     }
     __syncthreads();
+    if (threadIdx.x < a.n_launch) s_views[threadIdx.x] = a.experts[s_ids[threadIdx.x]];
+    __syncthreads();
     const int wg_r = gridDim.x - wg_s;
-    gate_up_stream<TYR, LPUR>(a, RoutedSlots{a, s_ids}, a.n_launch, a.ffn_r, (blockIdx.x - wg_s) * MOE_WAVES,
+    gate_up_stream<TYR, LPUR>(a, RoutedSlots{s_views}, a.n_launch, a.ffn_r, (blockIdx.x - wg_s) * MOE_WAVES,
                               wg_r * MOE_WAVES, smem);
 }
 
@@ -328,8 +333,11 @@ template <int TYR, int TYS>
 static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
     const int nb = a.hidden / 256;
     const int lds = gate_up_lds<TYR>(nb) > gate_up_lds<TYS>(nb) ? gate_up_lds<TYR>(nb) : gate_up_lds<TYS>(nb);
-    // tiles_s / tiles_r: workgroups of the shared / routed streams.
-    const int grid = (a.has_shared && !a.skip_shared_gate_up ? a.tiles_s : 0) + (a.n_launch > 0 ? a.tiles_r : 0);
+    // tiles_s / tiles_r: workgroups of the shared / routed streams; when the
+    // shared expert already ran (block decode) the routed stream takes both.
+    const bool shared_here = a.has_shared && !a.skip_shared_gate_up;
+    const int grid = (shared_here ? a.tiles_s : 0) +
+                     (a.n_launch > 0 ? a.tiles_r + (a.skip_shared_gate_up ? a.tiles_s : 0) : 0);
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL((k_moe_gate_up<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>), dim3(grid), dim3(MOE_THREADS), lds, s,
                        a);
