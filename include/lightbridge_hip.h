@@ -210,6 +210,50 @@ lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *moe, const uint32_t 
 lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, const float *coefs, size_t n_routed,
                            const float *x_dev, float *y_dev);
 
+/* ---- batched MoE decode ----------------------------------------------------------
+ * The reference decodes one token at a time: Hy3ScalarModel::evaluate_inner
+ * (crates/bridge-runtime/src/hy3_scalar.rs:504-650) calls moe_routed_by_id_into
+ * (crates/bridge-kernels-reference/src/moe.rs:64-147) per token.  These entry points
+ * take a batch of tokens in one call; token t's output is bit-identical to that
+ * call on token t.  The batch's (token, routed expert) pairs are sorted by expert
+ * on the device, so each selected expert's weights stream from HBM once per chunk
+ * of its tokens. */
+
+/* [sync] Allocates the scratch of batched calls of up to max_tokens tokens (<= 256)
+ * with up to top_k routed experts each (the reference allocates its SwiGluScratch
+ * once, activation.rs:146-168; no allocation happens per call). */
+lbh_status lbh_moe_reserve_batch(lbh_moe *moe, size_t max_tokens, size_t top_k, lbh_error *err);
+
+/* Launch-shape knob of the batched kernels: tokens staged per chunk (1..16) and
+ * rows per workgroup of the routed/shared gate-up and down streams. */
+lbh_status lbh_moe_set_batch_tiles(lbh_moe *moe, int32_t tokens_per_chunk, int32_t rows_gate_up_routed,
+                                   int32_t rows_gate_up_shared, int32_t rows_down_routed, int32_t rows_down_shared);
+
+/* [async] Batched form of lbh_moe_forward: ids_dev / coefs_dev are device arrays
+ * [n_tokens][top_k] (each token's ids ascending and distinct), x_dev [n_tokens][hidden],
+ * y_dev [n_tokens][hidden].  Unchecked; a routing with an id >= n_experts or a token
+ * naming an expert twice leaves y unchanged. */
+lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids_dev, const float *coefs_dev,
+                                 size_t n_tokens, size_t top_k, const float *x_dev, float *y_dev);
+
+/* [sync] Checked form with host routing: every token's ids/coefs are validated with
+ * the rules and error variants of moe_routed_by_id_into (moe.rs:73-129; err->row =
+ * the token), then x must be finite (NonFiniteValue, index = lane, row = token); on
+ * any error y is unchanged.  Non-finite intermediate values (SwiGLU, accumulation)
+ * are not reported by the batched form: they propagate into y. */
+lbh_status lbh_moe_routed_by_id_batch_into(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, const float *coefs,
+                                           size_t n_tokens, size_t top_k, const float *input_dev, size_t input_len,
+                                           float *output_dev, size_t output_len, lbh_error *err);
+
+/* [async] route_experts_into over a batch of finished router logits
+ * (crates/bridge-model-hy3/src/routing.rs:25-107 for mode 1; mode 0 is the
+ * softmax top-k of lbh_router_route_into): logits_dev [n_tokens][n_experts]
+ * (n_experts <= 256) -> ids_dev / coefs_dev [n_tokens][top_k], ids ascending.
+ * bias_dev (mode 1) is the selection bias [n_experts].  Unchecked: logits finite. */
+lbh_status lbh_route_experts_batch(lbh_ctx *ctx, const float *logits_dev, size_t n_tokens, size_t n_experts,
+                                   size_t top_k, int32_t mode, float weight_scale, const float *bias_dev,
+                                   uint32_t *ids_dev, float *coefs_dev);
+
 /* ---- router -------------------------------------------------------------------
  * F32 router [hidden, n_experts] (GGML; n_experts rows of `hidden` floats) resident
  * in HBM, n_experts <= 256.  bias (optional) is the selection bias exp_probs_b. */

@@ -460,6 +460,14 @@ struct lbh_moe {
     MoeStatus *status;
     MoeStatus *status_host;
     int wg_r, wg_s, tile_d;   // gate/up workgroups (routed, shared stream); down rows per workgroup
+    // Batched decode scratch (lbh_moe_reserve_batch): capacity and one allocation.
+    size_t cap_tokens, cap_k;
+    uint8_t *batch_mem;
+    BatchArgs batch;          // scratch pointers; per-call fields are filled in per call
+    uint32_t *batch_ids;      // device copies of host routing (checked entry)
+    float *batch_coefs;
+    int32_t *plan_host;       // pinned
+    int tc, rt_gu_r, rt_gu_s, rt_d_r, rt_d_s;
 };
 
 namespace {
@@ -468,6 +476,8 @@ void free_moe(lbh_moe *m) {
     if (!m) return;
     DeviceGuard g(m->device);
     if (m->experts_dev) (void)hipFree(m->experts_dev);
+    if (m->batch_mem) (void)hipFree(m->batch_mem);
+    if (m->plan_host) (void)hipHostFree(m->plan_host);
     if (m->h) (void)hipFree(m->h);
     if (m->status) (void)hipFree(m->status);
     if (m->status_host) (void)hipHostFree(m->status_host);
@@ -565,6 +575,11 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
         m->wg_r = total - m->wg_s > 1 ? total - m->wg_s : 1;
     }
     m->tile_d = 16;
+    m->tc = 8;
+    m->rt_gu_r = 128;
+    m->rt_gu_s = 128;
+    m->rt_d_r = 320;
+    m->rt_d_s = 128;
     const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
     m->h_stride = (int)max_ffn;
     const size_t slots = MOE_MAX_ROUTED + 1;
@@ -722,6 +737,206 @@ lbh_status lbh_debug_expf(lbh_ctx *ctx, const float *in, float *out, size_t n, i
 
 void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, const float *up) {
     for (size_t i = 0; i < n; ++i) out[i] = swiglu ? swiglu_ref(in[i], up[i]) : expf_libm(in[i]);
+}
+
+}  // extern "C"
+
+// ================================================================== batched MoE decode
+
+namespace {
+
+BatchArgs batch_args(const lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_tokens, size_t top_k,
+                     const float *x, float *y) {
+    BatchArgs a = m->batch;
+    a.experts = m->experts_dev;
+    a.shared = m->shared;
+    a.has_shared = m->has_shared;
+    a.hidden = (int32_t)m->hidden;
+    a.ffn_r = (int32_t)m->ffn_r;
+    a.ffn_s = (int32_t)(m->has_shared ? m->ffn_s : m->ffn_r);
+    a.n_experts = (int32_t)m->n_experts;
+    a.n_tokens = (int32_t)n_tokens;
+    a.top_k = (int32_t)top_k;
+    a.ids = ids;
+    a.coefs = coefs;
+    a.x = x;
+    a.y = y;
+    const long long pairs = (long long)n_tokens * (long long)top_k;
+    const long long hit = pairs < (long long)m->n_experts ? pairs : (long long)m->n_experts;
+    // Chunks per expert are ceil(count / tc): at most pairs / tc + (experts hit).
+    long long mc = pairs / m->tc + hit;
+    a.max_chunks = (int32_t)(mc < pairs ? mc : pairs);
+    a.tc = m->tc;
+    a.rt_gu_r = m->rt_gu_r;
+    a.rt_gu_s = m->rt_gu_s;
+    a.rt_d_r = m->rt_d_r;
+    a.rt_d_s = m->rt_d_s;
+    a.type_gate_r = m->type_gate_r;
+    a.type_down_r = m->type_down_r;
+    return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lbh_error *err) {
+    if (!m) return fail(err, LBH_NULL_ARGUMENT);
+    if (max_tokens == 0 || max_tokens > (size_t)BATCH_MAX_TOKENS)
+        return fail(err, LBH_UNSUPPORTED_SHAPE, 0, 0, BATCH_MAX_TOKENS, max_tokens);
+    if (top_k == 0 || top_k > (size_t)MOE_MAX_ROUTED || top_k > m->n_experts)
+        return fail(err, LBH_UNSUPPORTED_SHAPE, 0, 1, MOE_MAX_ROUTED, top_k);
+    if (m->n_experts > (size_t)BATCH_MAX_EXPERTS) return fail(err, LBH_UNSUPPORTED_SHAPE, 0, 2, BATCH_MAX_EXPERTS, m->n_experts);
+    const int tsg = m->has_shared ? m->shared.gate.type : LBH_IQ2_S;
+    const int tsd = m->has_shared ? m->shared.down.type : LBH_IQ3_S;
+    if (!batch_types_supported(m->type_gate_r, m->type_down_r, tsg, tsd)) return fail(err, LBH_UNSUPPORTED_TYPE, m->type_gate_r);
+    DeviceGuard g(m->device);
+    if (m->batch_mem) {
+        (void)hipFree(m->batch_mem);
+        m->batch_mem = nullptr;
+    }
+    const size_t T = max_tokens, P = max_tokens * top_k;
+    const size_t nbh = m->hidden / 256, nbr = m->ffn_r / 256, ffn_s = m->has_shared ? m->ffn_s : m->ffn_r;
+    const size_t nbs = ffn_s / 256;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += (bytes + 255) & ~(size_t)255;
+        return o;
+    };
+    const size_t o_plan = take(16), o_ce = take(P * 4), o_cp = take(P * 4), o_cn = take(P * 4);
+    const size_t o_pt = take(P * 4), o_po = take(P * 4);
+    const size_t o_q8x = take(T * nbh * 292), o_q8xr = take(T * nbh * 292);
+    const size_t o_hr = take(P * m->ffn_r * 4), o_hs = take(T * ffn_s * 4);
+    const size_t o_q8hr = take(P * nbr * 292), o_q8hs = take(T * nbs * 292);
+    const size_t o_dr = take(P * m->hidden * 4), o_ds = take(T * m->hidden * 4);
+    const size_t o_ids = take(P * 4), o_coefs = take(P * 4);
+    hipError_t e = hipMalloc(&m->batch_mem, off);
+    if (e == hipSuccess) e = hipMemset(m->batch_mem, 0, off);
+    if (e == hipSuccess && !m->plan_host) e = hipHostMalloc(&m->plan_host, 16, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        if (m->batch_mem) (void)hipFree(m->batch_mem);
+        m->batch_mem = nullptr;
+        m->cap_tokens = m->cap_k = 0;
+        return hip_fail(err, e);
+    }
+    uint8_t *b = m->batch_mem;
+    BatchArgs &a = m->batch;
+    a = BatchArgs{};
+    a.plan = reinterpret_cast<int32_t *>(b + o_plan);
+    a.chunk_expert = reinterpret_cast<int32_t *>(b + o_ce);
+    a.chunk_p0 = reinterpret_cast<int32_t *>(b + o_cp);
+    a.chunk_n = reinterpret_cast<int32_t *>(b + o_cn);
+    a.pair_token = reinterpret_cast<int32_t *>(b + o_pt);
+    a.pair_of = reinterpret_cast<int32_t *>(b + o_po);
+    a.q8x = b + o_q8x;
+    a.q8x_rm = b + o_q8xr;
+    a.h_r = reinterpret_cast<float *>(b + o_hr);
+    a.h_s = reinterpret_cast<float *>(b + o_hs);
+    a.q8h_r = b + o_q8hr;
+    a.q8h_s = b + o_q8hs;
+    a.d_r = reinterpret_cast<float *>(b + o_dr);
+    a.d_s = reinterpret_cast<float *>(b + o_ds);
+    m->batch_ids = reinterpret_cast<uint32_t *>(b + o_ids);
+    m->batch_coefs = reinterpret_cast<float *>(b + o_coefs);
+    m->cap_tokens = max_tokens;
+    m->cap_k = top_k;
+    return ok(err);
+}
+
+lbh_status lbh_moe_set_batch_tiles(lbh_moe *m, int32_t tokens_per_chunk, int32_t rows_gate_up_routed,
+                                   int32_t rows_gate_up_shared, int32_t rows_down_routed, int32_t rows_down_shared) {
+    if (!m) return LBH_NULL_ARGUMENT;
+    if (tokens_per_chunk < 1 || tokens_per_chunk > BATCH_MAX_TC) return LBH_INVALID_PARAMETER;
+    const int v[4] = {rows_gate_up_routed, rows_gate_up_shared, rows_down_routed, rows_down_shared};
+    for (int i = 0; i < 4; ++i)
+        if (v[i] < 1 || v[i] > 65536) return LBH_INVALID_PARAMETER;
+    BatchArgs probe = batch_args(m, nullptr, nullptr, 1, 1, nullptr, nullptr);
+    probe.tc = tokens_per_chunk;
+    for (int st = 0; st < 5; ++st)
+        if (batch_lds_bytes(probe, st) > 160 * 1024) return LBH_UNSUPPORTED_SHAPE;
+    m->tc = tokens_per_chunk;
+    m->rt_gu_r = v[0], m->rt_gu_s = v[1], m->rt_d_r = v[2], m->rt_d_s = v[3];
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_tokens,
+                                 size_t top_k, const float *x, float *y) {
+    if (!ctx || !m || !ids || !coefs || !x || !y) return LBH_NULL_ARGUMENT;
+    if (n_tokens == 0 || top_k == 0) return LBH_DIMENSION_MISMATCH;
+    if (!m->batch_mem || n_tokens > m->cap_tokens || top_k > m->cap_k) return LBH_SCRATCH_TOO_SMALL;
+    DeviceGuard g(ctx->device);
+    if (launch_moe_batch(batch_args(m, ids, coefs, n_tokens, top_k, x, y), ctx->stream) != hipSuccess)
+        return LBH_HIP_ERROR;
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_routed_by_id_batch_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs,
+                                           size_t n_tokens, size_t top_k, const float *input, size_t input_len,
+                                           float *output, size_t output_len, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    if (top_k == 0) return fail(err, LBH_DIMENSION_MISMATCH, 0, 3, 1, 0);
+    if (n_tokens == 0) return fail(err, LBH_DIMENSION_MISMATCH, 0, 4, 1, 0);
+    if (input_len != n_tokens * m->hidden) return fail(err, LBH_DIMENSION_MISMATCH, 0, 0, n_tokens * m->hidden, input_len);
+    if (output_len != n_tokens * m->hidden)
+        return fail(err, LBH_DIMENSION_MISMATCH, 0, 1, n_tokens * m->hidden, output_len);
+    if (!ids || !coefs || !input || !output) return fail(err, LBH_NULL_ARGUMENT);
+    if (!m->batch_mem || n_tokens > m->cap_tokens || top_k > m->cap_k)
+        return fail(err, LBH_SCRATCH_TOO_SMALL, 0, 0, m->cap_tokens * m->cap_k, n_tokens * top_k);
+    // Each token's routing under the rules of moe_routed_by_id_into (moe.rs:94-129).
+    for (size_t t = 0; t < n_tokens; ++t) {
+        const uint32_t *id = ids + t * top_k;
+        const float *cf = coefs + t * top_k;
+        for (size_t i = 0; i < top_k; ++i) {
+            uint32_t bits;
+            std::memcpy(&bits, &cf[i], 4);
+            if ((bits & 0x7f800000u) == 0x7f800000u) return fail(err, LBH_NON_FINITE_VALUE, 0, 0, 0, 0, bits, 6, t);
+            if (i > 0 && id[i] == id[i - 1]) return fail(err, LBH_DUPLICATE_ROUTED_EXPERT, 0, id[i], 0, 0, 0, 0, t);
+            if (i > 0 && id[i] < id[i - 1])
+                return fail(err, LBH_ROUTED_EXPERT_ORDER, 0, id[i], id[i - 1], id[i], 0, 0, t);
+            if (id[i] >= m->n_experts) return fail(err, LBH_INVALID_PARAMETER, 0, id[i], m->n_experts, id[i], 0, 0, t);
+        }
+    }
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+    HIP_TRY(launch_find_nonfinite(input, (long long)input_len, &ctx->status->first_bad_input, ctx->stream));
+    lbh_status st = read_status(ctx, err);
+    if (st) return st;
+    if (ctx->status_host->first_bad_input != ~0ull) {
+        const unsigned long long i = ctx->status_host->first_bad_input;
+        return fail(err, LBH_NON_FINITE_VALUE, m->type_gate_r, i % m->hidden, 0, 0, read_f32_bits(ctx, input + i), 0,
+                    i / m->hidden);
+    }
+    HIP_TRY(hipMemcpyAsync(m->batch_ids, ids, n_tokens * top_k * 4, hipMemcpyHostToDevice, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(m->batch_coefs, coefs, n_tokens * top_k * 4, hipMemcpyHostToDevice, ctx->stream));
+    const BatchArgs a = batch_args(m, m->batch_ids, m->batch_coefs, n_tokens, top_k, input, output);
+    HIP_TRY(launch_moe_batch(a, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(m->plan_host, a.plan, 8, hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    if (m->plan_host[1]) return fail(err, LBH_INVALID_PARAMETER, 0, (uint64_t)m->plan_host[1]);
+    return ok(err);
+}
+
+lbh_status lbh_route_experts_batch(lbh_ctx *ctx, const float *logits, size_t n_tokens, size_t n_experts, size_t top_k,
+                                   int32_t mode, float weight_scale, const float *bias, uint32_t *ids, float *coefs) {
+    if (!ctx || !logits || !ids || !coefs || (mode == 1 && !bias)) return LBH_NULL_ARGUMENT;
+    if (mode != 0 && mode != 1) return LBH_INVALID_PARAMETER;
+    if (n_tokens == 0 || n_experts == 0 || n_experts > 256 || top_k == 0 || top_k > n_experts ||
+        top_k > (size_t)MOE_MAX_ROUTED)
+        return LBH_UNSUPPORTED_SHAPE;
+    RouteBatchArgs a{};
+    a.r.bias = bias;
+    a.r.n_experts = (int32_t)n_experts;
+    a.r.top_k = (int32_t)top_k;
+    a.r.mode = mode;
+    a.r.weight_scale = weight_scale;
+    a.logits = logits;
+    a.ids = ids;
+    a.coefs = coefs;
+    a.n_tokens = (int32_t)n_tokens;
+    DeviceGuard g(ctx->device);
+    return launch_route_batch(a, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
 
 }  // extern "C"

@@ -1,0 +1,795 @@
+// lbh_batch.hip — batched decode of a batch of tokens through the MoE layer.
+//
+// Per token the result is bit-identical to moe_routed_by_id_into
+// (crates/bridge-kernels-reference/src/moe.rs:64-147), which the reference
+// runs one token at a time (crates/bridge-runtime/src/hy3_scalar.rs:504-650).
+// Here the batch's (token, routed expert) pairs are sorted by expert, so each
+// selected expert's weights stream from HBM once per chunk of its tokens and
+// are decoded once into registers for all of them:
+//
+//   k_mb_prep     counting sort of the pairs by expert (ascending token order
+//                 inside an expert) into a chunk table; Q8_K of every token;
+//   k_mb_gate_up  per (chunk, row tile): the chunk's Q8_K activations staged
+//                 in LDS, gate and up rows decoded once, integer dots against
+//                 every staged token, per-(row, token) folds in the
+//                 reference's block order, SwiGLU -> h;
+//   k_mb_quant_h  Q8_K of every h row (the down projections' inputs,
+//                 gemv.rs:161-163);
+//   k_mb_down     per (chunk, row tile): the down rows against every staged h;
+//   k_mb_combine  per token and output row, in the reference's order:
+//                 y = ((0 + c_0 d_0) + c_1 d_1) + ... + 1.0 * d_shared.
+//
+// The shared expert is one more "expert" that every token selects.
+#include "lbh_internal.h"
+#include "lbh_math.h"
+#include "lbh_router.h"
+#include "lbh_rows.h"
+
+namespace lbh {
+
+constexpr int MB_THREADS = 256;
+constexpr int MB_WAVES = MB_THREADS / 64;
+
+// A staged Q8_K block in LDS: d at 0, qs at 16, bsums at 272 (16-byte aligned
+// quants so a lane's slice is a run of 16-byte reads).
+constexpr int Q8L = 304;
+
+__host__ __device__ constexpr int al16(int v) { return (v + 15) & ~15; }
+
+// ------------------------------------------------------------ activations
+
+template <int G>
+__device__ __forceinline__ void load_act_lds(const uint8_t *blk, int p, ActIQ<G> &a) {
+    a.d8 = __uint_as_float(*reinterpret_cast<const uint32_t *>(blk));
+    const uint4 *q = reinterpret_cast<const uint4 *>(blk + 16 + 32 * G * p);
+#pragma unroll
+    for (int i = 0; i < 2 * G; ++i) {
+        const uint4 v = q[i];
+        a.q[4 * i] = v.x, a.q[4 * i + 1] = v.y, a.q[4 * i + 2] = v.z, a.q[4 * i + 3] = v.w;
+    }
+}
+
+// K-quant consumers read residue-major qs (dword t of a 32-byte group holds
+// bytes t, t + 8, t + 16, t + 24): the ActKQ layout, so no transpose here.
+template <int G>
+__device__ __forceinline__ void load_act_lds(const uint8_t *blk, int p, ActKQ<G> &a) {
+    a.d8 = __uint_as_float(*reinterpret_cast<const uint32_t *>(blk));
+    const uint4 *q = reinterpret_cast<const uint4 *>(blk + 16 + 64 * G * p);
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+        const uint4 v0 = q[2 * j], v1 = q[2 * j + 1];
+        a.t[j][0] = v0.x, a.t[j][1] = v0.y, a.t[j][2] = v0.z, a.t[j][3] = v0.w;
+        a.t[j][4] = v1.x, a.t[j][5] = v1.y, a.t[j][6] = v1.z, a.t[j][7] = v1.w;
+    }
+    const uint32_t *bs = reinterpret_cast<const uint32_t *>(blk + 272 + 8 * G * p);
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+        const uint32_t w = bs[j];
+        a.bsp[j] = (int32_t)(int16_t)(w & 0xffff) + (int32_t)(int16_t)(w >> 16);
+    }
+}
+
+// ------------------------------------------------------- decoded weights
+//
+// IQ2_S / IQ3_S: the slice's signed int8 weights and the integer scale of
+// each 16-element half group (IQ2_S: 1 + 2 * nibble per half, q8_k.rs:355-362;
+// IQ3_S: 2 * nibble + 1 for the whole group, q8_k.rs:389-427), so the block
+// sum is sum over halves of scale * dot(16 weights, 16 quants): the same
+// integer as the reference's (integer addition is exact in any order).
+template <int LPU>
+struct DecIQ {
+    static constexpr int G = 8 / LPU;
+    uint32_t w[8 * G];
+    int32_t s[2 * G];
+    float d;
+};
+
+// Q4_K / Q5_K: unsigned quants of each sub-block j in residue-major dwords,
+// sub-block scale and min (scale_min, k_quants.rs:231-240), d and dmin.
+template <int LPU>
+struct DecKQ {
+    static constexpr int G = 4 / LPU;
+    uint32_t q[2 * G][8];
+    int32_t sc[2 * G], mn[2 * G];
+    float d, dmin;
+};
+
+template <int TY, int LPU>
+using DecOf = typename std::conditional<Traits<TY>::KQ, DecKQ<LPU>, DecIQ<LPU>>::type;
+
+template <int LPU>
+__device__ __forceinline__ void decode(const WSlice<T_IQ2_S, LPU> &w, const void *gridp, int, DecIQ<LPU> &o) {
+    constexpr int G = 8 / LPU;
+    const uint2 *grid = reinterpret_cast<const uint2 *>(gridp);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+        const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
+#pragma unroll
+        for (int lg = 0; lg < 4; ++lg) {
+            const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
+            const uint2 code = grid[idx];
+            const uint32_t s = byte_of(w.sg[g], lg);
+            const uint32_t sel_lo = (((s & 15u) * 0x810204u) & 0x04040404u) | code.x;
+            const uint32_t sel_hi = (((s >> 4) * 0x810204u) & 0x04040404u) | code.y;
+            o.w[8 * g + 2 * lg] = perm(IQ2S_NEG, IQ2S_POS, sel_lo);
+            o.w[8 * g + 2 * lg + 1] = perm(IQ2S_NEG, IQ2S_POS, sel_hi);
+        }
+        o.s[2 * g] = (int32_t)(1 + 2 * (sc & 15u));
+        o.s[2 * g + 1] = (int32_t)(1 + 2 * (sc >> 4));
+    }
+    o.d = f16_to_f32(w.d);
+}
+
+template <int LPU>
+__device__ __forceinline__ void decode(const WSlice<T_IQ3_S, LPU> &w, const void *gridp, int, DecIQ<LPU> &o) {
+    constexpr int G = 8 / LPU;
+    const uint2 *grid = reinterpret_cast<const uint2 *>(gridp);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+        const int32_t sc = (int32_t)(2 * ((w.sc >> (4 * g)) & 15u) + 1);
+#pragma unroll
+        for (int lg = 0; lg < 4; ++lg) {
+            const uint32_t qq = w.qs[2 * g + (lg >> 1)];
+            const int sh = 16 * (lg & 1);
+            const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
+            const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
+            const uint32_t s = byte_of(w.sg[g], lg);
+            const uint2 g1 = grid[i1], g2 = grid[i2];
+            o.w[8 * g + 2 * lg] = apply_signs(g1.x, g1.y, s & 15u);
+            o.w[8 * g + 2 * lg + 1] = apply_signs(g2.x, g2.y, s >> 4);
+        }
+        o.s[2 * g] = sc;
+        o.s[2 * g + 1] = sc;
+    }
+    o.d = f16_to_f32(w.d);
+}
+
+template <int TY, int LPU>
+__device__ __forceinline__ void decode(const WSliceKQ<TY, LPU> &w, const void *, int p, DecKQ<LPU> &o) {
+    constexpr int G = 4 / LPU;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int gg = G * p + g;
+        int32_t sc0, mn0, sc1, mn1;
+        scale_min_of(w.hdr.y, w.hdr.z, w.hdr.w, 2 * gg, sc0, mn0);
+        scale_min_of(w.hdr.y, w.hdr.z, w.hdr.w, 2 * gg + 1, sc1, mn1);
+        o.sc[2 * g] = sc0, o.mn[2 * g] = mn0, o.sc[2 * g + 1] = sc1, o.mn[2 * g + 1] = mn1;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t lo = w.q[g][t] & 0x0f0f0f0fu;
+            uint32_t hi = (w.q[g][t] >> 4) & 0x0f0f0f0fu;
+            if constexpr (TY == T_Q5_K) {
+                lo |= ((w.qh[t] >> (2 * gg)) & 0x01010101u) << 4;
+                hi |= ((w.qh[t] >> (2 * gg + 1)) & 0x01010101u) << 4;
+            }
+            o.q[2 * g][t] = lo;
+            o.q[2 * g + 1][t] = hi;
+        }
+    }
+    o.d = f16_to_f32(w.hdr.x & 0xffffu);
+    o.dmin = f16_to_f32(w.hdr.x >> 16);
+}
+
+// Integer stage of one token against a decoded slice: IQ -> v[0] = the
+// slice's share of the block sum; K-quants -> v[0..7] lane sums, v[8] the
+// minimum sum (q8_k.rs:288-312, :337-364, :380-428).
+template <int LPU>
+__device__ __forceinline__ void token_ints(const DecIQ<LPU> &o, const ActIQ<8 / LPU> &a, int32_t *v) {
+    constexpr int G = 8 / LPU;
+    int32_t bs = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        int32_t p0 = 0, p1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) p0 = dot4(o.w[8 * g + k], a.q[8 * g + k], p0);
+#pragma unroll
+        for (int k = 4; k < 8; ++k) p1 = dot4(o.w[8 * g + k], a.q[8 * g + k], p1);
+        bs = mul24(o.s[2 * g], p0) + bs;
+        bs = mul24(o.s[2 * g + 1], p1) + bs;
+    }
+    v[0] = bs;
+}
+
+template <int LPU>
+__device__ __forceinline__ void token_ints(const DecKQ<LPU> &o, const ActKQ<4 / LPU> &a, int32_t *v) {
+    constexpr int G = 4 / LPU;
+    int32_t ms = 0;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) v[t] = 0;
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[t] = mul24(o.sc[j], dot4(o.q[j][t], a.t[j][t], 0)) + v[t];
+        ms = mul24(o.mn[j], a.bsp[j]) + ms;
+    }
+    v[8] = ms;
+}
+
+// ------------------------------------------------------------ one wave step
+//
+// The decoded rows of NM matrices (rpw rows, one per slot) against n staged
+// tokens.  Tokens go in fold batches of FB: the integer stage of every token
+// of a batch writes its per-block f32 terms to the wave's LDS table, then the
+// wave's lanes fold the (matrix, token, row, chain) chains in parallel, each
+// chain in the reference's sequential block order (lbh_rows.h fold_terms),
+// and lanes (token, row) combine the chains (K-quants: sum = minimum chain,
+// then += lane chains 0..7, q8_k.rs:314-326; IQ2_S: x 0.125, q8_k.rs:369) and
+// call out(token, slot, values[NM]).  Every lane of the wave must call it.
+template <int TY, int LPU, int NM, int FB, class Out>
+__device__ __forceinline__ void batch_step(const DecOf<TY, LPU> (&dec)[NM], bool on, const LaneMap<LPU> &L, int nb,
+                                           const uint8_t *s_act, int n, float *terms, float *chains, Out out) {
+    using Tr = Traits<TY>;
+    constexpr int NCH = Tr::NCH;
+    const int tstr = nb + 1;
+    const int lane = threadIdx.x & 63;
+    const int rpw = L.rpw;
+    for (int i0 = 0; i0 < n; i0 += FB) {
+        const int nf = n - i0 < FB ? n - i0 : FB;
+        for (int f = 0; f < nf; ++f) {
+            ActOf<TY, LPU> act;
+            load_act_lds(s_act + ((i0 + f) * nb + L.b) * Q8L, L.part, act);
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                int32_t v[NCH];
+                token_ints(dec[m], act, v);
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) v[c] = unit_reduce<LPU>(v[c]);
+                if (on && L.part == 0) {
+                    float *t = terms + (((m * FB + f) * rpw + L.slot) * NCH) * tstr + L.b;
+                    if constexpr (Tr::KQ) {
+                        const float s = __fmul_rn(dec[m].d, act.d8);
+                        const float ms = __fmul_rn(dec[m].dmin, act.d8);
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) t[c * tstr] = __fmul_rn(s, (float)v[c]);
+                        t[8 * tstr] = __fmul_rn(ms, (float)v[8]);
+                    } else {
+                        t[0] = __fmul_rn(__fmul_rn(dec[m].d, act.d8), (float)v[0]);
+                    }
+                }
+            }
+        }
+        wave_sync();
+        const int tasks = NM * nf * rpw * NCH;
+        for (int k = lane; k < tasks; k += 64) {
+            const int c = k % NCH;
+            int r = k / NCH;
+            const int slot = r % rpw;
+            r /= rpw;
+            const int f = r % nf, m = r / nf;
+            const int idx = ((m * FB + f) * rpw + slot) * NCH + c;
+            chains[idx] = fold_terms(terms + idx * tstr, nb, Tr::KQ && c == 8);
+        }
+        wave_sync();
+        for (int k = lane; k < nf * rpw; k += 64) {
+            const int f = k % nf, slot = k / nf;
+            float res[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) {
+                const float *ch = chains + ((m * FB + f) * rpw + slot) * NCH;
+                float s;
+                if constexpr (Tr::KQ) {
+                    s = ch[8];
+#pragma unroll
+                    for (int l = 0; l < 8; ++l) s = __fadd_rn(s, ch[l]);
+                } else {
+                    s = ch[0];
+                    if (TY == T_IQ2_S) s = __fmul_rn(0.125f, s);
+                }
+                res[m] = s;
+            }
+            out(i0 + f, slot, res);
+        }
+        wave_sync();
+    }
+}
+
+// Fold batch per type: IQ chains are short work per token, so their folds
+// wait for up to eight tokens; K-quants carry nine chains per row and fold
+// after every token (a small term table).
+template <int TY>
+constexpr int fold_batch() {
+    return Traits<TY>::KQ ? 1 : 8;
+}
+
+// LDS floats of one wave's term table and chain results.
+template <int TY, int NM>
+__host__ __device__ constexpr int wave_fold_floats(int rpw, int nb) {
+    return NM * fold_batch<TY>() * rpw * Traits<TY>::NCH * (nb + 2);
+}
+
+__host__ __device__ constexpr int rows_per_step(int lpu, int nb) { return (64 / lpu) / nb; }
+
+// Rows [r0, r1) of NM matrices against the n tokens staged in s_act.  The
+// wave's first weight loads are issued before `prologue` (codebook fill and
+// activation staging, ended by a workgroup barrier), so their latency
+// overlaps it; then a software pipeline keeps the next step's loads in flight.
+template <int TY, int LPU, int NM, class Prologue, class Out>
+__device__ __forceinline__ void batch_rows(const MatView (&mv)[NM], int r0, int r1, const uint8_t *s_act, int n,
+                                           const void *grid, float *fold_lds, Prologue prologue, Out out) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int nb = mv[0].nb;
+    const LaneMap<LPU> L(lane, nb);
+    using W = WOf<TY, LPU>;
+    Planes P[NM];
+    uint32_t po[NM];
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+        P[m] = make_planes(mv[m].planes, mv[m].units, mv[m].bytes);
+        po[m] = part_offset<TY, LPU>(P[m], L.part);
+    }
+    const int rpw = L.rpw;
+    float *terms = fold_lds + wid * wave_fold_floats<TY, NM>(rpw, nb);
+    float *chains = terms + NM * fold_batch<TY>() * rpw * Traits<TY>::NCH * (nb + 1);
+    const int steps = (r1 - r0 + rpw - 1) / rpw;
+    // Lanes past the tile (or past the wave's last whole row) load and decode
+    // the tile's last row: every register is defined, and `on` gates the writes.
+    auto issue = [&](int j, W (&w)[NM]) {
+        if (j < steps) {
+            int r = r0 + j * rpw + L.slot;
+            r = L.lane_on && r < r1 ? r : r1 - 1;
+#pragma unroll
+            for (int m = 0; m < NM; ++m) load_slice(P[m], (uint32_t)(r * nb + L.b), po[m], L.part, w[m]);
+        }
+    };
+    auto process = [&](int j, const W (&w)[NM]) {
+        const int r = r0 + j * rpw + L.slot;
+        const bool on = L.lane_on && r < r1;
+        DecOf<TY, LPU> dec[NM];
+#pragma unroll
+        for (int m = 0; m < NM; ++m) decode(w[m], grid, L.part, dec[m]);
+        batch_step<TY, LPU, NM, fold_batch<TY>()>(dec, on, L, nb, s_act, n, terms, chains,
+                                                  [&](int i, int slot, const float *res) {
+                                                      const int rr = r0 + j * rpw + slot;
+                                                      if (rr < r1) out(i, rr, res);
+                                                  });
+    };
+    int j = wid;
+    W wa[NM], wb[NM];
+    issue(j, wa);
+    prologue();
+    while (j < steps) {
+        issue(j + MB_WAVES, wb);
+        process(j, wa);
+        j += MB_WAVES;
+        if (j >= steps) break;
+        issue(j + MB_WAVES, wa);
+        process(j, wb);
+        j += MB_WAVES;
+    }
+}
+
+// Copies n x nb GGML Q8_K blocks (block (i, b) at src_of(i) + 292 * b) into
+// the padded LDS layout, all threads of the workgroup.
+template <class Src>
+__device__ __forceinline__ void stage_q8(uint8_t *s_act, int n, int nb, Src src_of) {
+    const int total = n * nb * 73;
+    for (int k = threadIdx.x; k < total; k += blockDim.x) {
+        const int blk = k / 73, w = k - blk * 73;
+        const int i = blk / nb, b = blk - i * nb;
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(src_of(i) + b * 292 + 4 * w);
+        const int off = w == 0 ? 0 : w <= 64 ? 16 + 4 * (w - 1) : 272 + 4 * (w - 65);
+        *reinterpret_cast<uint32_t *>(s_act + blk * Q8L + off) = v;
+    }
+}
+
+// LDS layout of a stream workgroup: [staged activations][codebook][fold tables].
+template <int TY, int NM>
+__host__ __device__ constexpr int stream_lds(int tc, int nb, int lpu) {
+    return al16(tc * nb * Q8L) + al16(GridLDS<TY>::BYTES) + MB_WAVES * 4 * wave_fold_floats<TY, NM>(rows_per_step(lpu, nb), nb);
+}
+
+template <int TY>
+constexpr int mb_lpu() {
+    return 2;
+}
+
+// ------------------------------------------------------------------ kernels
+
+// Sort of the batch's pairs by expert (workgroup 0) and Q8_K of every token
+// (the other workgroups, four blocks per wave).
+__device__ __forceinline__ void quantize_rows_out(const float *x, long long nblocks, long long first, uint8_t *plain,
+                                                  uint8_t *rm, uint8_t *lds_wave) {
+    // Four blocks per call into the wave's LDS, then out to global memory: the
+    // GGML bytes, and (rm != NULL) the copy with residue-major qs.
+    const int lane = threadIdx.x & 63;
+    const long long cnt = nblocks - first < 4 ? nblocks - first : 4;
+    quantize_blocks_wave(x + first * 256, lds_wave, 0, cnt);
+    wave_sync();
+    const int dw = (int)cnt * 73;
+    for (int k = lane; k < dw; k += 64) {
+        const int blk = k / 73, w = k - blk * 73;
+        const uint8_t *sb = lds_wave + blk * 292;
+        const uint32_t v = *reinterpret_cast<const uint32_t *>(sb + 4 * w);
+        if (plain) *reinterpret_cast<uint32_t *>(plain + (first + blk) * 292 + 4 * w) = v;
+        if (rm) {
+            uint32_t r = v;
+            if (w >= 1 && w <= 64) {
+                const int q = w - 1, g = q >> 3, t = q & 7;
+                const uint8_t *src = sb + 4 + 32 * g + t;
+                r = (uint32_t)src[0] | ((uint32_t)src[8] << 8) | ((uint32_t)src[16] << 16) | ((uint32_t)src[24] << 24);
+            }
+            *reinterpret_cast<uint32_t *>(rm + (first + blk) * 292 + 4 * w) = r;
+        }
+    }
+    wave_sync();
+}
+
+__global__ void __launch_bounds__(MB_THREADS) k_mb_prep(BatchArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x;
+    if (blockIdx.x > 0) {
+        const int nb = a.hidden / 256;
+        const long long nblocks = (long long)a.n_tokens * nb;
+        const long long first = ((long long)(blockIdx.x - 1) * MB_WAVES + (tid >> 6)) * 4;
+        if (first < nblocks)
+            quantize_rows_out(a.x, nblocks, first, a.q8x, a.has_shared && (a.shared.gate.type == T_Q4_K ||
+                                                                           a.shared.gate.type == T_Q5_K)
+                                                              ? a.q8x_rm
+                                                              : nullptr,
+                              smem + (tid >> 6) * 4 * 292);
+        return;
+    }
+    const int NE = a.n_experts, T = a.n_tokens, K = a.top_k, TC = a.tc;
+    const int W = (T + 31) / 32;
+    uint32_t *bm = reinterpret_cast<uint32_t *>(smem);              // [NE][W] token bitmaps
+    int32_t *cnt = reinterpret_cast<int32_t *>(bm + NE * W);       // [NE]
+    int32_t *off = cnt + NE;                                       // [NE] first sorted pair
+    int32_t *coff = off + NE;                                      // [NE] first chunk
+    int32_t *part = coff + NE;                                     // [2][MB_THREADS] scan partials
+    int32_t *flags = part + 2 * MB_THREADS;
+    for (int i = tid; i < NE * W; i += MB_THREADS) bm[i] = 0;
+    if (tid == 0) flags[0] = 0;
+    __syncthreads();
+    for (int p = tid; p < T * K; p += MB_THREADS) {
+        const int t = p / K;
+        const uint32_t e = a.ids[p];
+        if (e >= (uint32_t)NE) {
+            atomicOr(&flags[0], 1);
+            continue;
+        }
+        const uint32_t bit = 1u << (t & 31);
+        const uint32_t old = atomicOr(&bm[e * W + (t >> 5)], bit);
+        if (old & bit) atomicOr(&flags[0], 2);
+    }
+    __syncthreads();
+    // Per-expert counts and chunk counts; each thread owns a run of experts.
+    const int per = (NE + MB_THREADS - 1) / MB_THREADS;
+    const int e0 = tid * per, e1 = e0 + per < NE ? e0 + per : NE;
+    int sc = 0, sk = 0;
+    for (int e = e0; e < e1; ++e) {
+        int c = 0;
+        for (int w = 0; w < W; ++w) c += __popc(bm[e * W + w]);
+        cnt[e] = c;
+        sc += c;
+        sk += (c + TC - 1) / TC;
+    }
+    part[tid] = sc;
+    part[MB_THREADS + tid] = sk;
+    __syncthreads();
+    // Inclusive scan of the partials (Hillis-Steele), then exclusive offsets.
+    for (int d = 1; d < MB_THREADS; d <<= 1) {
+        const int v0 = tid >= d ? part[tid - d] : 0;
+        const int v1 = tid >= d ? part[MB_THREADS + tid - d] : 0;
+        __syncthreads();
+        part[tid] += v0;
+        part[MB_THREADS + tid] += v1;
+        __syncthreads();
+    }
+    {
+        int o = part[tid] - sc, ko = part[MB_THREADS + tid] - sk;
+        for (int e = e0; e < e1; ++e) {
+            off[e] = o;
+            coff[e] = ko;
+            o += cnt[e];
+            ko += (cnt[e] + TC - 1) / TC;
+        }
+    }
+    __syncthreads();
+    const bool bad = flags[0] != 0;
+    if (!bad) {
+        for (int p = tid; p < T * K; p += MB_THREADS) {
+            const int t = p / K;
+            const uint32_t e = a.ids[p];
+            int rank = __popc(bm[e * W + (t >> 5)] & ((1u << (t & 31)) - 1u));
+            for (int w = 0; w < (t >> 5); ++w) rank += __popc(bm[e * W + w]);
+            const int pos = off[e] + rank;
+            a.pair_token[pos] = t;
+            a.pair_of[p] = pos;
+        }
+        for (int e = e0; e < e1; ++e) {
+            const int c = cnt[e];
+            for (int j = 0; j * TC < c; ++j) {
+                const int ch = coff[e] + j;
+                a.chunk_expert[ch] = e;
+                a.chunk_p0[ch] = off[e] + j * TC;
+                a.chunk_n[ch] = c - j * TC < TC ? c - j * TC : TC;
+            }
+        }
+    }
+    if (tid == 0) {
+        a.plan[0] = bad ? 0 : part[2 * MB_THREADS - 1];
+        a.plan[1] = flags[0];
+    }
+}
+
+// Gate/up, SwiGLU (activation.rs:170-178) -> h, one launch per stream:
+// SHARED: workgroup (token chunk, row tile) of the shared expert; else
+// workgroup (routed chunk, row tile), idle past the sort's chunk count.
+template <int TY, bool SHARED>
+__global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if (a.plan[1]) return;
+    const int nb = a.hidden / 256;
+    constexpr int LPU = mb_lpu<TY>();
+    uint8_t *s_act = smem;
+    uint8_t *grid = smem + al16(a.tc * nb * Q8L);
+    float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
+    if constexpr (SHARED) {
+        const int tiles = (a.ffn_s + a.rt_gu_s - 1) / a.rt_gu_s;
+        const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
+        const int t0 = c * a.tc;
+        const int n = a.n_tokens - t0 < a.tc ? a.n_tokens - t0 : a.tc;
+        const int r0 = tile * a.rt_gu_s, r1 = r0 + a.rt_gu_s < a.ffn_s ? r0 + a.rt_gu_s : a.ffn_s;
+        const uint8_t *src = Traits<TY>::KQ ? a.q8x_rm : a.q8x;
+        const MatView mv[2] = {a.shared.gate, a.shared.up};
+        batch_rows<TY, LPU, 2>(
+            mv, r0, r1, s_act, n, grid, fold,
+            [&]() {
+                fill_grid<TY>(grid);
+                stage_q8(s_act, n, nb, [&](int i) { return src + (long long)(t0 + i) * nb * 292; });
+                __syncthreads();
+            },
+            [&](int i, int r, const float *res) {
+                a.h_s[(long long)(t0 + i) * a.ffn_s + r] = swiglu_ref(res[0], res[1]);
+            });
+    } else {
+        const int tiles = (a.ffn_r + a.rt_gu_r - 1) / a.rt_gu_r;
+        const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
+        if (c >= a.plan[0]) return;
+        const int e = a.chunk_expert[c], p0 = a.chunk_p0[c], n = a.chunk_n[c];
+        const int r0 = tile * a.rt_gu_r, r1 = r0 + a.rt_gu_r < a.ffn_r ? r0 + a.rt_gu_r : a.ffn_r;
+        const MatView mv[2] = {a.experts[e].gate, a.experts[e].up};
+        batch_rows<TY, LPU, 2>(
+            mv, r0, r1, s_act, n, grid, fold,
+            [&]() {
+                fill_grid<TY>(grid);
+                stage_q8(s_act, n, nb, [&](int i) { return a.q8x + (long long)a.pair_token[p0 + i] * nb * 292; });
+                __syncthreads();
+            },
+            [&](int i, int r, const float *res) {
+                a.h_r[(long long)(p0 + i) * a.ffn_r + r] = swiglu_ref(res[0], res[1]);
+            });
+    }
+}
+
+// Q8_K of every h row (quantize_row_q8_k_into of each down projection's
+// input): routed rows [0, pairs), then the shared rows.
+__global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shared_rm) {
+    __shared__ __align__(16) uint8_t lds[MB_WAVES * 4 * 292];
+    if (a.plan[1]) return;
+    const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
+    const long long br = (long long)a.n_tokens * a.top_k * nbr;
+    const long long bs = a.has_shared ? (long long)a.n_tokens * nbs : 0;
+    const long long chunk = ((long long)blockIdx.x * MB_WAVES + (threadIdx.x >> 6)) * 4;
+    uint8_t *lw = lds + (threadIdx.x >> 6) * 4 * 292;
+    // Chunks of four never straddle the two ranges: br is a multiple of 4
+    // whenever a chunk would (chunk starts are multiples of 4).
+    if (chunk < br) {
+        quantize_rows_out(a.h_r, br, chunk, a.q8h_r, nullptr, lw);
+    } else if (chunk - ((br + 3) & ~3ll) < bs && chunk >= ((br + 3) & ~3ll)) {
+        const long long f = chunk - ((br + 3) & ~3ll);
+        quantize_rows_out(a.h_s, bs, f, shared_rm ? nullptr : a.q8h_s, shared_rm ? a.q8h_s : nullptr, lw);
+    }
+}
+
+// Down rows -> d, one launch per stream (as k_mb_gate_up).
+template <int TY, bool SHARED>
+__global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if (a.plan[1]) return;
+    constexpr int LPU = mb_lpu<TY>();
+    uint8_t *s_act = smem;
+    if constexpr (SHARED) {
+        const int nb = a.ffn_s / 256;
+        const int tiles = (a.hidden + a.rt_d_s - 1) / a.rt_d_s;
+        const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
+        const int t0 = c * a.tc;
+        const int n = a.n_tokens - t0 < a.tc ? a.n_tokens - t0 : a.tc;
+        const int r0 = tile * a.rt_d_s, r1 = r0 + a.rt_d_s < a.hidden ? r0 + a.rt_d_s : a.hidden;
+        uint8_t *grid = smem + al16(a.tc * nb * Q8L);
+        float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
+        const MatView mv[1] = {a.shared.down};
+        batch_rows<TY, LPU, 1>(
+            mv, r0, r1, s_act, n, grid, fold,
+            [&]() {
+                fill_grid<TY>(grid);
+                stage_q8(s_act, n, nb, [&](int i) { return a.q8h_s + (long long)(t0 + i) * nb * 292; });
+                __syncthreads();
+            },
+            [&](int i, int r, const float *res) { a.d_s[(long long)(t0 + i) * a.hidden + r] = res[0]; });
+    } else {
+        const int nb = a.ffn_r / 256;
+        const int tiles = (a.hidden + a.rt_d_r - 1) / a.rt_d_r;
+        const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
+        if (c >= a.plan[0]) return;
+        const int e = a.chunk_expert[c], p0 = a.chunk_p0[c], n = a.chunk_n[c];
+        const int r0 = tile * a.rt_d_r, r1 = r0 + a.rt_d_r < a.hidden ? r0 + a.rt_d_r : a.hidden;
+        uint8_t *grid = smem + al16(a.tc * nb * Q8L);
+        float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
+        const MatView mv[1] = {a.experts[e].down};
+        batch_rows<TY, LPU, 1>(
+            mv, r0, r1, s_act, n, grid, fold,
+            [&]() {
+                fill_grid<TY>(grid);
+                stage_q8(s_act, n, nb, [&](int i) { return a.q8h_r + (long long)(p0 + i) * nb * 292; });
+                __syncthreads();
+            },
+            [&](int i, int r, const float *res) { a.d_r[(long long)(p0 + i) * a.hidden + r] = res[0]; });
+    }
+}
+
+// Ordered combine of one token's routed outputs in its slot (ascending id)
+// order, then the shared expert at 1.0 (moe.rs:141-146).
+__global__ void __launch_bounds__(MB_THREADS) k_mb_combine(BatchArgs a) {
+    if (a.plan[1]) return;
+    const long long total = (long long)a.n_tokens * a.hidden;
+    for (long long k = (long long)blockIdx.x * MB_THREADS + threadIdx.x; k < total;
+         k += (long long)gridDim.x * MB_THREADS) {
+        const int t = (int)(k / a.hidden), r = (int)(k - (long long)t * a.hidden);
+        float acc = 0.0f;
+        for (int s = 0; s < a.top_k; ++s) {
+            const int p = a.pair_of[t * a.top_k + s];
+            acc = __fadd_rn(acc, __fmul_rn(a.coefs[t * a.top_k + s], a.d_r[(long long)p * a.hidden + r]));
+        }
+        if (a.has_shared) acc = __fadd_rn(acc, __fmul_rn(1.0f, a.d_s[(long long)t * a.hidden + r]));
+        a.y[k] = acc;
+    }
+}
+
+// Top-k selection of every token of a batch from finished logits, one wave per token.
+__global__ void __launch_bounds__(64) k_route_batch(RouteBatchArgs a) {
+    const int t = blockIdx.x;
+    RouterArgs r = a.r;
+    r.logits = const_cast<float *>(a.logits) + (long long)t * r.n_experts;
+    MoeRoute out;
+    unsigned long long bad;
+    select_route(r, out, bad);
+    // out is the same in every lane: lane s writes slot s.
+#pragma unroll
+    for (int s = 0; s < MOE_MAX_ROUTED; ++s) {
+        if (s < r.top_k && (int)threadIdx.x == s) {
+            a.ids[(long long)t * r.top_k + s] = out.ids[s];
+            a.coefs[(long long)t * r.top_k + s] = out.coefs[s];
+        }
+    }
+    if (threadIdx.x == 0 && a.status && bad != ~0ull) atomicMin(a.status, ((unsigned long long)t << 32) | bad);
+}
+
+// ---------------------------------------------------------------- launchers
+
+static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
+
+// LDS bytes of a stream launch of type ty (nm matrices, nb blocks per row).
+static int stream_lds_of(int ty, int nm, int tc, int nb) {
+    switch (ty) {
+    case T_IQ2_S: return nm == 2 ? stream_lds<T_IQ2_S, 2>(tc, nb, 2) : stream_lds<T_IQ2_S, 1>(tc, nb, 2);
+    case T_IQ3_S: return nm == 2 ? stream_lds<T_IQ3_S, 2>(tc, nb, 2) : stream_lds<T_IQ3_S, 1>(tc, nb, 2);
+    case T_Q4_K: return nm == 2 ? stream_lds<T_Q4_K, 2>(tc, nb, 2) : stream_lds<T_Q4_K, 1>(tc, nb, 2);
+    case T_Q5_K: return nm == 2 ? stream_lds<T_Q5_K, 2>(tc, nb, 2) : stream_lds<T_Q5_K, 1>(tc, nb, 2);
+    default: return 1 << 30;
+    }
+}
+
+// stage 0: sort + quantize; 1/2: routed / shared gate-up; 3/4: routed / shared down.
+int batch_lds_bytes(const BatchArgs &a, int stage) {
+    const int nbh = a.hidden / 256, nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
+    switch (stage) {
+    case 0: {
+        const int W = (a.n_tokens + 31) / 32;
+        const int sort = (a.n_experts * W + 3 * a.n_experts + 2 * MB_THREADS + 4) * 4;
+        return sort > MB_WAVES * 4 * 292 ? sort : MB_WAVES * 4 * 292;
+    }
+    case 1: return stream_lds_of(a.type_gate_r, 2, a.tc, nbh);
+    case 2: return a.has_shared ? stream_lds_of(a.shared.gate.type, 2, a.tc, nbh) : 0;
+    case 3: return stream_lds_of(a.type_down_r, 1, a.tc, nbr);
+    default: return a.has_shared ? stream_lds_of(a.shared.down.type, 1, a.tc, nbs) : 0;
+    }
+}
+
+template <class K>
+static hipError_t allow_lds(K kernel, int lds) {
+    if (lds <= 64 * 1024) return hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+}
+
+template <int TY, bool SHARED>
+static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
+    hipError_t e = allow_lds(k_mb_gate_up<TY, SHARED>, lds);
+    if (e != hipSuccess) return e;
+    const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.ffn_s, a.rt_gu_s) : a.max_chunks * cdiv(a.ffn_r, a.rt_gu_r);
+    hipLaunchKernelGGL((k_mb_gate_up<TY, SHARED>), dim3(grid), dim3(MB_THREADS), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int TY, bool SHARED>
+static hipError_t down_typed(const BatchArgs &a, int lds, hipStream_t s) {
+    hipError_t e = allow_lds(k_mb_down<TY, SHARED>, lds);
+    if (e != hipSuccess) return e;
+    const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.hidden, a.rt_d_s) : a.max_chunks * cdiv(a.hidden, a.rt_d_r);
+    hipLaunchKernelGGL((k_mb_down<TY, SHARED>), dim3(grid), dim3(MB_THREADS), lds, s, a);
+    return hipGetLastError();
+}
+
+template <bool SHARED>
+static hipError_t gate_up_any(int ty, const BatchArgs &a, int lds, hipStream_t s) {
+    switch (ty) {
+    case T_IQ2_S: return gate_up_typed<T_IQ2_S, SHARED>(a, lds, s);
+    case T_Q4_K: return gate_up_typed<T_Q4_K, SHARED>(a, lds, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <bool SHARED>
+static hipError_t down_any(int ty, const BatchArgs &a, int lds, hipStream_t s) {
+    switch (ty) {
+    case T_IQ2_S: return down_typed<T_IQ2_S, SHARED>(a, lds, s);
+    case T_IQ3_S: return down_typed<T_IQ3_S, SHARED>(a, lds, s);
+    case T_Q5_K: return down_typed<T_Q5_K, SHARED>(a, lds, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+bool batch_types_supported(int gate_r, int down_r, int gate_s, int down_s) {
+    return gate_r == T_IQ2_S && (down_r == T_IQ3_S || down_r == T_IQ2_S) && (gate_s == T_IQ2_S || gate_s == T_Q4_K) &&
+           (down_s == T_IQ2_S || down_s == T_IQ3_S || down_s == T_Q5_K);
+}
+
+hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
+    if (a.n_tokens < 1 || a.n_tokens > BATCH_MAX_TOKENS || a.top_k < 1 || a.top_k > MOE_MAX_ROUTED ||
+        a.n_experts < 1 || a.n_experts > BATCH_MAX_EXPERTS || a.tc < 1 || a.tc > BATCH_MAX_TC)
+        return hipErrorInvalidValue;
+    const int tsg = a.has_shared ? a.shared.gate.type : T_IQ2_S;
+    const int tsd = a.has_shared ? a.shared.down.type : T_IQ3_S;
+    if (!batch_types_supported(a.type_gate_r, a.type_down_r, tsg, tsd)) return hipErrorInvalidValue;
+    int lds[5];
+    for (int i = 0; i < 5; ++i) {
+        lds[i] = batch_lds_bytes(a, i);
+        if (lds[i] > 160 * 1024) return hipErrorInvalidValue;
+    }
+    const int nbh = a.hidden / 256;
+    hipError_t e = allow_lds(k_mb_prep, lds[0]);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_mb_prep, dim3(1 + cdiv((long long)a.n_tokens * nbh, 4 * MB_WAVES)), dim3(MB_THREADS), lds[0],
+                       s, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (a.has_shared && (e = gate_up_any<true>(tsg, a, lds[2], s)) != hipSuccess) return e;
+    if ((e = gate_up_any<false>(a.type_gate_r, a, lds[1], s)) != hipSuccess) return e;
+
+    const bool rm = tsd == T_Q4_K || tsd == T_Q5_K;
+    const long long br = (long long)a.n_tokens * a.top_k * (a.ffn_r / 256);
+    const long long bs = a.has_shared ? (long long)a.n_tokens * (a.ffn_s / 256) : 0;
+    hipLaunchKernelGGL(k_mb_quant_h, dim3(cdiv(((br + 3) & ~3ll) + bs, 4 * MB_WAVES)), dim3(MB_THREADS), 0, s, a,
+                       rm ? 1 : 0);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+
+    if (a.has_shared && (e = down_any<true>(tsd, a, lds[4], s)) != hipSuccess) return e;
+    if ((e = down_any<false>(a.type_down_r, a, lds[3], s)) != hipSuccess) return e;
+
+    const long long total = (long long)a.n_tokens * a.hidden;
+    int g = cdiv(total, MB_THREADS);
+    g = g > 4096 ? 4096 : g;
+    hipLaunchKernelGGL(k_mb_combine, dim3(g), dim3(MB_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_batch(const RouteBatchArgs &a, hipStream_t s) {
+    if (a.n_tokens < 1 || a.r.n_experts < 1 || a.r.n_experts > 256 || a.r.top_k < 1 || a.r.top_k > MOE_MAX_ROUTED ||
+        a.r.top_k > a.r.n_experts)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_batch, dim3(a.n_tokens), dim3(64), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace lbh

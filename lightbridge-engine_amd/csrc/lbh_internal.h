@@ -112,6 +112,60 @@ struct MoeArgs {
     RouterArgs router;
 };
 
+// ------------------------------------------------------ batched MoE decode
+
+constexpr int BATCH_MAX_TOKENS = 256;
+constexpr int BATCH_MAX_EXPERTS = 1024;
+constexpr int BATCH_MAX_TC = 16;      // tokens staged per chunk
+
+// Scratch and shape of one batched call (all pointers device memory).
+struct BatchArgs {
+    const ExpertDev *experts;   // device table [n_experts]
+    ExpertDev shared;
+    int32_t has_shared;
+    int32_t hidden, ffn_r, ffn_s, n_experts;
+    int32_t n_tokens, top_k;
+    const uint32_t *ids;        // [n_tokens][top_k]
+    const float *coefs;         // [n_tokens][top_k]
+    const float *x;             // [n_tokens][hidden]
+    float *y;                   // [n_tokens][hidden]
+    // plan written by the sort: plan[0] = routed chunks (0 when the routing is
+    // invalid), plan[1] = invalid-routing flags (1: id out of range, 2: repeated id)
+    int32_t *plan;
+    int32_t *chunk_expert, *chunk_p0, *chunk_n;   // [max_chunks]
+    int32_t *pair_token;        // sorted pair -> token
+    int32_t *pair_of;           // token * top_k + slot -> sorted pair
+    uint8_t *q8x;               // [n_tokens][hidden / 256] Q8_K blocks of x
+    uint8_t *q8x_rm;            // the same with residue-major qs (K-quant consumers)
+    float *h_r;                 // [pairs][ffn_r]  SwiGLU outputs, sorted pair order
+    float *h_s;                 // [n_tokens][ffn_s]
+    uint8_t *q8h_r;             // [pairs][ffn_r / 256] Q8_K of h_r
+    uint8_t *q8h_s;             // [n_tokens][ffn_s / 256] Q8_K of h_s (residue-major for K-quants)
+    float *d_r;                 // [pairs][hidden] routed down outputs
+    float *d_s;                 // [n_tokens][hidden] shared down outputs
+    int32_t max_chunks;         // routed chunks the launches cover
+    int32_t tc;                 // tokens per chunk (1..BATCH_MAX_TC)
+    int32_t rt_gu_r, rt_gu_s;   // gate/up rows per workgroup (routed, shared)
+    int32_t rt_d_r, rt_d_s;     // down rows per workgroup (routed, shared)
+    int32_t type_gate_r, type_down_r;
+};
+
+// Batch selection: top-k of each token's finished logits (select_route).
+struct RouteBatchArgs {
+    RouterArgs r;               // n_experts, top_k, mode, weight_scale, bias
+    const float *logits;        // [n_tokens][n_experts]
+    uint32_t *ids;              // [n_tokens][top_k]
+    float *coefs;
+    unsigned long long *status; // optional: (token << 32 | expert << 2 | field), min over the batch
+    int32_t n_tokens;
+    int32_t pad;
+};
+
+hipError_t launch_route_batch(const RouteBatchArgs &a, hipStream_t s);
+hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s);
+int batch_lds_bytes(const BatchArgs &a, int stage);
+bool batch_types_supported(int gate_r, int down_r, int gate_s, int down_s);
+
 hipError_t launch_router(const RouterArgs &a, hipStream_t s);
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t s);
 hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s);

@@ -111,6 +111,11 @@ def lib() -> C.CDLL:
             "lbh_router_destroy": ([p], i32),
             "lbh_router_route_into": ([p, p, p, sz, sz, i32, C.c_float, p, p, p, E], i32),
             "lbh_moe_block_forward": ([p, p, p, p, sz, i32, C.c_float, p], i32),
+            "lbh_moe_reserve_batch": ([p, sz, sz, E], i32),
+            "lbh_moe_set_batch_tiles": ([p, i32, i32, i32, i32, i32], i32),
+            "lbh_moe_forward_batch": ([p, p, p, p, sz, sz, p, p], i32),
+            "lbh_moe_routed_by_id_batch_into": ([p, p, p, p, sz, sz, p, sz, p, sz, E], i32),
+            "lbh_route_experts_batch": ([p, p, sz, sz, sz, i32, C.c_float, p, p, p], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -252,6 +257,35 @@ class HipBackend:
         _call(lib().lbh_moe_routed_by_id_into, self.ctx, moe.handle, C.c_void_p(ids.ctypes.data),
               C.c_void_p(coefs.ctypes.data), ids.size, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel())
 
+    def moe_forward_batch(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
+        """Batched decode (asynchronous, unchecked): ids/coefs device tensors
+        [n_tokens, top_k] (uint32 as int32 storage / float32), x and y [n_tokens, hidden]."""
+        n, k = ids.shape
+        st = lib().lbh_moe_forward_batch(self.ctx, moe.handle, _dev_ptr(ids), _dev_ptr(coefs), n, k, _dev_ptr(x),
+                                         _dev_ptr(y))
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def moe_routed_by_id_batch_into(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
+        """Checked batched decode with host routing [n_tokens, top_k] (each token as
+        moe_routed_by_id_into, crates/bridge-kernels-reference/src/moe.rs:64-147)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        coefs = np.ascontiguousarray(coefs, dtype=np.float32)
+        n, k = ids.shape
+        _call(lib().lbh_moe_routed_by_id_batch_into, self.ctx, moe.handle, C.c_void_p(ids.ctypes.data),
+              C.c_void_p(coefs.ctypes.data), n, k, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel())
+
+    def route_experts_batch(self, logits, top_k: int, ids, coefs, mode: int = 0, weight_scale: float = 1.0,
+                            bias=None) -> None:
+        """Top-k selection of every token from device logits [n_tokens, n_experts]
+        (route_experts_into, crates/bridge-model-hy3/src/routing.rs:25-107, for mode 1)."""
+        n, ne = logits.shape
+        st = lib().lbh_route_experts_batch(self.ctx, _dev_ptr(logits), n, ne, top_k, mode, weight_scale,
+                                           _dev_ptr(bias) if bias is not None else None, _dev_ptr(ids),
+                                           _dev_ptr(coefs))
+        if st:
+            raise KernelError(LbhError(status=st))
+
     def moe_forward(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
         """Unchecked, asynchronous form (graph capturable)."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
@@ -330,6 +364,17 @@ class MoeLayer:
         self.be, self.handle = be, h
         self._keep = (experts, shared)
         self.n_experts = n
+
+    def reserve_batch(self, max_tokens: int, top_k: int) -> None:
+        """Scratch of batched calls (allocated once)."""
+        _call(lib().lbh_moe_reserve_batch, self.handle, max_tokens, top_k)
+
+    def set_batch_tiles(self, tokens_per_chunk: int = 8, rows_gate_up_routed: int = 128,
+                        rows_gate_up_shared: int = 128, rows_down_routed: int = 320, rows_down_shared: int = 128) -> None:
+        st = lib().lbh_moe_set_batch_tiles(self.handle, tokens_per_chunk, rows_gate_up_routed, rows_gate_up_shared,
+                                           rows_down_routed, rows_down_shared)
+        if st:
+            raise KernelError(LbhError(status=st))
 
     def set_tiles(self, wg_routed: int, wg_shared: int, tile_d: int = 16) -> None:
         """Workgroups of the routed / shared gate-up streams, output rows per down workgroup."""
