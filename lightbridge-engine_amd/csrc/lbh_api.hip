@@ -24,6 +24,7 @@ struct lbh_ctx {
     DevStatus *status;        // device
     DevStatus *status_host;   // pinned mirror
     GemvTuning tuning;
+    int gemm_shape;           // workgroup shape of the K-quant GEMM (0: 2x2 waves)
 };
 
 struct lbh_matrix {
@@ -32,6 +33,8 @@ struct lbh_matrix {
     size_t rows, k, nb;
     uint8_t *planes;
     size_t bytes;
+    uint8_t *gemm_a;     // MFMA-ready copy for token batches (lbh_matrix_prepare_gemm), or NULL
+    float2 *gemm_dm;
 };
 
 namespace {
@@ -192,6 +195,10 @@ lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
         if (value < 0) return LBH_INVALID_PARAMETER;
         ctx->tuning.max_blocks = value ? value : 8 * ctx->cu_count;
         return LBH_OK;
+    case LBH_TUNE_GEMM_SHAPE:
+        if (value < 0 || value > 3) return LBH_INVALID_PARAMETER;
+        ctx->gemm_shape = value;
+        return LBH_OK;
     default: return LBH_INVALID_PARAMETER;
     }
 }
@@ -307,6 +314,8 @@ lbh_status lbh_matrix_destroy(lbh_matrix *m) {
     if (!m) return LBH_NULL_ARGUMENT;
     DeviceGuard g(m->device);
     (void)hipFree(m->planes);  // hipFree waits for work that may still read the planes
+    if (m->gemm_a) (void)hipFree(m->gemm_a);
+    if (m->gemm_dm) (void)hipFree(m->gemm_dm);
     delete m;
     return LBH_OK;
 }
@@ -737,6 +746,80 @@ lbh_status lbh_debug_expf(lbh_ctx *ctx, const float *in, float *out, size_t n, i
 
 void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, const float *up) {
     for (size_t i = 0; i < n; ++i) out[i] = swiglu ? swiglu_ref(in[i], up[i]) : expf_libm(in[i]);
+}
+
+}  // extern "C"
+
+// ================================================================== K-quant GEMM (token batches)
+
+namespace {
+
+MatGemm gemm_view(const lbh_matrix *m, float *y, int ldy) {
+    MatGemm g;
+    g.a = m->gemm_a;
+    g.dm = m->gemm_dm;
+    g.y = y;
+    g.rows = (int32_t)m->rows;
+    g.ldy = ldy;
+    return g;
+}
+
+hipError_t prepare_gemm(lbh_matrix *m, hipStream_t s) {
+    if (m->gemm_a) return hipSuccess;
+    const int rows = (int)m->rows, nb = (int)m->nb;
+    hipError_t e = hipMalloc(&m->gemm_a, gemm_a_bytes(rows, nb));
+    if (e == hipSuccess) e = hipMalloc(&m->gemm_dm, gemm_dm_bytes(rows, nb));
+    if (e == hipSuccess) e = launch_prep_a(view_of(m), m->gemm_a, m->gemm_dm, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        if (m->gemm_a) (void)hipFree(m->gemm_a);
+        if (m->gemm_dm) (void)hipFree(m->gemm_dm);
+        m->gemm_a = nullptr;
+        m->gemm_dm = nullptr;
+    }
+    return e;
+}
+
+}  // namespace
+
+extern "C" {
+
+lbh_status lbh_matrix_prepare_gemm(lbh_ctx *ctx, lbh_matrix *m, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    if (m->type != LBH_Q4_K && m->type != LBH_Q5_K) return fail(err, LBH_UNSUPPORTED_TYPE, m->type);
+    if (m->device != ctx->device) return fail(err, LBH_INVALID_PARAMETER);
+    DeviceGuard g(ctx->device);
+    HIP_TRY(prepare_gemm(m, ctx->stream));
+    return ok(err);
+}
+
+size_t lbh_gemm_workspace_bytes(size_t n_tokens, size_t k) {
+    if (n_tokens == 0 || k == 0 || k % 256) return 0;
+    return gemm_b_bytes((int)n_tokens, (int)(k / 256));
+}
+
+lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t n_tokens, float *y,
+                         void *workspace, size_t workspace_len) {
+    if (!ctx || !m || !q8 || !y || !workspace) return LBH_NULL_ARGUMENT;
+    if (!m->gemm_a) return LBH_INVALID_PARAMETER;   // lbh_matrix_prepare_gemm first
+    if (n_tokens == 0 || n_tokens > (size_t)1 << 20) return LBH_UNSUPPORTED_SHAPE;
+    const int nb = (int)m->nb;
+    const size_t need = gemm_b_bytes((int)n_tokens, nb);
+    if (workspace_len < need) return LBH_SCRATCH_TOO_SMALL;
+    DeviceGuard g(ctx->device);
+    GemmArgs a{};
+    uint8_t *bt = static_cast<uint8_t *>(workspace);
+    const size_t tiles = (n_tokens + 31) / 32;
+    a.b = bt;
+    a.d8 = reinterpret_cast<const float *>(bt + tiles * nb * 9216);
+    a.nb = nb;
+    a.n_tokens = (int32_t)n_tokens;
+    a.n_mat = 1;
+    a.shape = ctx->gemm_shape;
+    a.mat[0] = gemm_view(m, y, (int)m->rows);
+    if (launch_prep_b(q8, (int)n_tokens, nb, bt, const_cast<float *>(a.d8), ctx->stream) != hipSuccess)
+        return LBH_HIP_ERROR;
+    return launch_kq_gemm(a, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
 
 }  // extern "C"

@@ -161,6 +161,33 @@ struct RouteBatchArgs {
     int32_t pad;
 };
 
+// ------------------------------------------------ K-quant GEMM on i8 MFMA
+
+constexpr int GEMM_MAX_MATS = 3;
+
+// One matrix of a GEMM launch: its MFMA-ready copy (A tiles, d/dmin) and output.
+struct MatGemm {
+    const uint8_t *a;      // [ceil(rows / 16)][nb] tiles of 9 KiB
+    const float2 *dm;      // [ceil(rows / 16) * 16][nb] (d, dmin)
+    float *y;              // y[t * ldy + r]
+    int32_t rows;
+    int32_t ldy;
+};
+
+struct GemmArgs {
+    MatGemm mat[GEMM_MAX_MATS];   // matrices sharing K and the activations
+    const uint8_t *b;             // [ceil(n_tokens / 32)][nb] tiles of 9 KiB
+    const float *d8;              // [ceil(n_tokens / 32)][nb][32]
+    int32_t n_mat, nb, n_tokens, shape;
+};
+
+size_t gemm_a_bytes(int rows, int nb);
+size_t gemm_dm_bytes(int rows, int nb);
+size_t gemm_b_bytes(int n_tokens, int nb);
+hipError_t launch_prep_a(const MatView &m, uint8_t *a, float2 *dm, hipStream_t s);
+hipError_t launch_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b, float *d8, hipStream_t s);
+hipError_t launch_kq_gemm(const GemmArgs &g, hipStream_t s);
+
 hipError_t launch_route_batch(const RouteBatchArgs &a, hipStream_t s);
 hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s);
 int batch_lds_bytes(const BatchArgs &a, int stage);

@@ -112,6 +112,9 @@ def lib() -> C.CDLL:
             "lbh_router_route_into": ([p, p, p, sz, sz, i32, C.c_float, p, p, p, E], i32),
             "lbh_moe_block_forward": ([p, p, p, p, sz, i32, C.c_float, p], i32),
             "lbh_moe_reserve_batch": ([p, sz, sz, E], i32),
+            "lbh_matrix_prepare_gemm": ([p, p, E], i32),
+            "lbh_gemm_workspace_bytes": ([sz, sz], sz),
+            "lbh_gemm_q8_k": ([p, p, p, sz, p, p, sz], i32),
             "lbh_moe_set_batch_tiles": ([p, i32, i32, i32, i32, i32], i32),
             "lbh_moe_forward_batch": ([p, p, p, p, sz, sz, p, p], i32),
             "lbh_moe_routed_by_id_batch_into": ([p, p, p, p, sz, sz, p, sz, p, sz, E], i32),
@@ -170,7 +173,7 @@ class HipBackend:
         self._stream = stream
         lib().lbh_ctx_set_stream(self.ctx, C.c_void_p(stream.cuda_stream))
 
-    TUNE_GEMV_LPU, TUNE_GEMV_MAX_BLOCKS = 1, 2
+    TUNE_GEMV_LPU, TUNE_GEMV_MAX_BLOCKS, TUNE_GEMM_SHAPE = 1, 2, 3
 
     def set_tuning(self, key: int, value: int) -> None:
         """Launch-shape knob (lanes per unit, workgroup cap); 0 restores the default."""
@@ -231,6 +234,18 @@ class HipBackend:
         st = lib().lbh_gemv_f32(self.ctx, m.handle, _dev_ptr(x), q8p, _dev_ptr(y), coef, 1 if accumulate else 0)
         if st:
             raise KernelError(LbhError(status=st))
+
+    def gemm_q8_k(self, m: "DeviceMatrix", q8, n_tokens: int, y, workspace) -> None:
+        """y[t, r] = vec_dot_q8_k(row r, token t) for a batch of Q8_K rows on the i8
+        matrix cores (the matrix must be prepared with DeviceMatrix.prepare_gemm)."""
+        st = lib().lbh_gemm_q8_k(self.ctx, m.handle, _dev_ptr(q8), n_tokens, _dev_ptr(y), _dev_ptr(workspace),
+                                 workspace.numel() * workspace.element_size())
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    @staticmethod
+    def gemm_workspace_bytes(n_tokens: int, k: int) -> int:
+        return lib().lbh_gemm_workspace_bytes(n_tokens, k)
 
     def block_sums(self, m: "DeviceMatrix", q8, out) -> None:
         st = lib().lbh_gemv_block_sums(self.ctx, m.handle, _dev_ptr(q8), _dev_ptr(out))
@@ -412,6 +427,10 @@ class DeviceMatrix:
                   C.byref(h))
         self.handle = h
         self.nbytes = lib().lbh_matrix_bytes(h)
+
+    def prepare_gemm(self) -> None:
+        """Build the MFMA-ready copy used by gemm_q8_k (Q4_K / Q5_K)."""
+        _call(lib().lbh_matrix_prepare_gemm, self.be.ctx, self.handle)
 
     def read_ggml(self) -> np.ndarray:
         out = np.zeros(self.nbytes, np.uint8)
