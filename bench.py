@@ -49,6 +49,9 @@ STEP_BYTES = GATE_BYTES + DOWN_BYTES
 Q4K_BYTES = HIDDEN * (HIDDEN // 256) * 144 + Q8(HIDDEN) + HIDDEN * 4    # 9,458,240
 MOE_WEIGHT_BYTES = (TOP_K * (2 * FFN * 16 * 82 + HIDDEN * 6 * 110) + 2 * HIDDEN * 16 * 144
                     + HIDDEN * 16 * 176 + N_EXPERTS * HIDDEN * 4)      # 87,425,024 per token
+EXPERT_BYTES = 2 * FFN * 16 * 82 + HIDDEN * 6 * 110                    # 6,733,824 per routed expert
+SHARED_BYTES = 2 * HIDDEN * 16 * 144 + HIDDEN * 16 * 176               # 30,408,704
+BATCH_TOKENS = 64
 
 
 def parse():
@@ -61,6 +64,7 @@ def parse():
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE block workload")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on each CPU baseline sample")
     ap.add_argument("--lpu", type=int, default=0, help="matvec lanes per (row, block) unit (0 = library default)")
+    ap.add_argument("--batch-reps", type=int, default=8, help="timed replays of the 8-step configs[3] graph")
     return ap.parse_args()
 
 
@@ -152,11 +156,7 @@ def cpu_moe(experts_np, shared_np, router_w, xs, seconds):
     from oracle import lb_oracle as orc
     threads = cpu_threads()
     ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
-    orc_exp = [orc.make_expert(orc.make_matrix(22, FFN, HIDDEN, g), orc.make_matrix(22, FFN, HIDDEN, u),
-                               orc.make_matrix(21, HIDDEN, FFN, d)) for g, u, d in experts_np]
-    sg, su, sd = shared_np
-    orc_sh = orc.make_expert(orc.make_matrix(12, HIDDEN, HIDDEN, sg), orc.make_matrix(12, HIDDEN, HIDDEN, su),
-                             orc.make_matrix(13, HIDDEN, HIDDEN, sd))
+    orc_exp, orc_sh = _oracle_layer(experts_np, shared_np)
     out = {}
     for preflight in (True, False):
         n, t0 = 0, time.perf_counter()
@@ -211,16 +211,13 @@ def bench_matvec_step(args, be, timer, torch, np, synth):
     gate_us = timer.time(g_gate, n_k) / (n_k * copies) * 1e6
     down_us = timer.time(g_down, n_k) / (n_k * copies) * 1e6
 
-    # parity spot check of the last step against the oracle (not timed)
-    from oracle import lb_oracle as orc
     c = (steps - 1) % copies
-    y_ref = orc.gemv_prequantized(orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, 8, True),
-                                  orc.make_matrix(synth.IQ3_S, HIDDEN, FFN, w_down), q8h[c].cpu().numpy())
-    parity = bool(np.array_equal(ys[c].cpu().numpy().view(np.uint32), y_ref.view(np.uint32)))
+    torch.cuda.synchronize()
+    check = (q8h[c].cpu().numpy(), ys[c].cpu().numpy())
     for m in gates + downs:
         m.close()
     return dict(w_gate=w_gate, w_down=w_down, copies=copies, steps=steps, warmup=reps_w * copies,
-                ms_per_step=ms_per_step, gate_us=gate_us, down_us=down_us, parity=parity)
+                ms_per_step=ms_per_step, gate_us=gate_us, down_us=down_us, check=check)
 
 
 def bench_q4k(args, be, timer, torch, np, synth):
@@ -274,20 +271,9 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
     timer.time(g_dev, 1)
     us_dev = timer.time(g_dev, reps) / (reps * T) * 1e6
 
-    # parity spot check (not timed): token 0 through the oracle
-    from oracle import lb_oracle as orc
     torch.cuda.synchronize()
     host = lambda t: t.cpu().numpy()  # noqa: E731
     experts_np = [(host(gate_t[e]), host(up_t[e]), host(down_t[e])) for e in range(N_EXPERTS)]
-    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, cpu_threads(), True)
-    orc_exp = [orc.make_expert(orc.make_matrix(22, FFN, HIDDEN, a), orc.make_matrix(22, FFN, HIDDEN, b),
-                               orc.make_matrix(21, HIDDEN, FFN, c)) for a, b, c in experts_np]
-    orc_sh = orc.make_expert(orc.make_matrix(12, HIDDEN, HIDDEN, shared_np[0]),
-                             orc.make_matrix(12, HIDDEN, HIDDEN, shared_np[1]),
-                             orc.make_matrix(13, HIDDEN, HIDDEN, shared_np[2]))
-    want_ids, want_coefs = orc.route_softmax_topk(orc.router_logits_f32(router_w, xs_np[T - 1]), TOP_K)
-    want = orc.moe_routed_by_id(ex, want_ids, want_coefs, orc_exp, orc_sh, xs_np[T - 1])
-    parity = bool(np.array_equal(host(ys[T - 1]).view(np.uint32), want.view(np.uint32)))
     res = {"workload": "configs[2]: MoE FFN block, 1 token: 192 experts (IQ2_S gate/up 1536x4096, IQ3_S down "
                        "4096x1536), top-8 softmax of an F32 4096x192 router, Q4_K/Q5_K shared expert ffn 4096",
            "tokens_timed": T * reps, "distinct_experts_hit": hit,
@@ -295,9 +281,179 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
                              "GB/s": round((MOE_WEIGHT_BYTES - N_EXPERTS * HIDDEN * 4) / us_host / 1e3, 1)},
            "with_device_router": {"us_per_token": round(us_dev, 2), "tokens_per_s": round(1e6 / us_dev, 1),
                                   "GB/s": round(MOE_WEIGHT_BYTES / us_dev / 1e3, 1)},
-           "algorithmic_weight_bytes_per_token": MOE_WEIGHT_BYTES,
-           "parity_last_token_bit_exact": parity}
-    return res, experts_np, shared_np, router_w, xs_np
+           "algorithmic_weight_bytes_per_token": MOE_WEIGHT_BYTES}
+    state = dict(experts_np=experts_np, shared_np=shared_np, router_w=router_w, xs_np=xs_np,
+                 last_y=host(ys[T - 1]), moe=moe, router=router, experts=experts, shared=shared)
+    return res, state
+
+
+def bench_batch(args, be, timer, torch, np, synth, state):
+    """64 tokens per step, each token's top-8 from seeded Zipf(1.1)
+    router logits (softmax top-8 selected on the device), grouped per-expert decode
+    after the device token-by-expert sort, on the same 192-expert layer."""
+    T, R = BATCH_TOKENS, 8
+    moe = state["moe"]
+    moe.reserve_batch(T, TOP_K)
+    logits = torch.from_numpy(np.stack([synth.zipf_routes(T, N_EXPERTS, TOP_K, 1.1, seed=500 + r)
+                                        for r in range(R)])).cuda()
+    xs = torch.from_numpy(np.stack([np.stack([synth.random_activations(HIDDEN, seed=600 + 64 * r + t)
+                                              for t in range(T)]) for r in range(R)])).cuda()
+    ids = torch.zeros((R, T, TOP_K), dtype=torch.int32, device="cuda")
+    coefs = torch.zeros((R, T, TOP_K), dtype=torch.float32, device="cuda")
+    ys = torch.zeros((R, T, HIDDEN), dtype=torch.float32, device="cuda")
+
+    def step(r):
+        be.route_experts_batch(logits[r], TOP_K, ids[r], coefs[r])
+        be.moe_forward_batch(moe, ids[r], coefs[r], xs[r], ys[r])
+
+    g = timer.graph(lambda: [step(r) for r in range(R)])
+    timer.time(g, 2)
+    reps = max(2, args.batch_reps)
+    us = timer.time(g, reps) / (reps * R) * 1e6
+    torch.cuda.synchronize()
+    ids_h = ids.cpu().numpy().view(np.uint32)
+    hits = [len(np.unique(ids_h[r])) for r in range(R)]
+    u = float(np.mean(hits))
+    bytes_step = u * EXPERT_BYTES + SHARED_BYTES + T * (2 * HIDDEN * 4 + N_EXPERTS * 4)
+    res = {"workload": "configs[3]: batched decode, 64 tokens: the configs[2] MoE block, per-token top-8 of seeded "
+                       "Zipf(s=1.1) router logits (softmax top-8 on the device), token-by-expert sort, grouped "
+                       "per-expert gate/up + SwiGLU + down, ordered combine",
+           "tokens_per_step": T, "steps_timed": reps * R, "us_per_step": round(us, 2),
+           "tokens_per_s": round(T / us * 1e6, 1),
+           "distinct_experts_hit_per_step": hits,
+           "algorithmic_bytes_per_step": int(bytes_step),
+           "GB/s": round(bytes_step / us / 1e3, 1), "roofline_frac": round(bytes_step / us / 1e3 / HBM_PEAK_GBS, 4),
+           "note": "the 33.5 MB shared expert is read once per step; routed experts once per chunk of 8 tokens"}
+    check = dict(ids=ids_h[0].copy(), coefs=coefs[0].cpu().numpy(), xs=xs[0].cpu().numpy(), ys=ys[0].cpu().numpy())
+    return res, check
+
+
+def cpu_batch(experts_np, shared_np, check, seconds):
+    """Oracle per token (the reference's token-serial loop) over the configs[3]
+    batch's tokens and routes: moe_routed_by_id_into single pass."""
+    import numpy as np
+    from oracle import lb_oracle as orc
+    threads = cpu_threads()
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
+    orc_exp, orc_sh = _oracle_layer(experts_np, shared_np)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        t = n % BATCH_TOKENS
+        orc.moe_routed_by_id(ex, check["ids"][t], check["coefs"][t], orc_exp, orc_sh, check["xs"][t], preflight=False)
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or el >= 2 * seconds:
+            break
+    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} tokens of the configs[3] batch (its Zipf routes) through moe_routed_by_id_into, single "
+                      f"pass, one token at a time as the reference decodes, in {el:.2f} s, {threads} threads"}
+
+
+def _oracle_layer(experts_np, shared_np):
+    from oracle import lb_oracle as orc
+    orc_exp = [orc.make_expert(orc.make_matrix(22, FFN, HIDDEN, g), orc.make_matrix(22, FFN, HIDDEN, u),
+                               orc.make_matrix(21, HIDDEN, FFN, d)) for g, u, d in experts_np]
+    sg, su, sd = shared_np
+    orc_sh = orc.make_expert(orc.make_matrix(12, HIDDEN, HIDDEN, sg), orc.make_matrix(12, HIDDEN, HIDDEN, su),
+                             orc.make_matrix(13, HIDDEN, HIDDEN, sd))
+    return orc_exp, orc_sh
+
+
+def _prefill_parity(check):
+    import numpy as np
+    from oracle import lb_oracle as orc
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, cpu_threads(), True)
+    om = orc.make_matrix(13, PF_ROWS, HIDDEN, check["w"])
+    return all(bool(np.array_equal(check["y"][t].view(np.uint32), orc.gemv_prequantized(ex, om, check["q8"][t]).view(np.uint32)))
+               for t in range(8))
+
+
+def cpu_parity(mv, moe_state, batch_check):
+    """Spot checks of the timed GPU outputs against the CPU oracle (not timed)."""
+    import numpy as np
+    from oracle import lb_oracle as orc
+    same = lambda a, b: bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))  # noqa: E731
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, cpu_threads(), True)
+    q8h, y = mv["check"]
+    out = {"configs[1]_last_step": same(y, orc.gemv_prequantized(ex, orc.make_matrix(21, HIDDEN, FFN, mv["w_down"]),
+                                                                  q8h))}
+    if moe_state is not None:
+        orc_exp, orc_sh = _oracle_layer(moe_state["experts_np"], moe_state["shared_np"])
+        x = moe_state["xs_np"][-1]
+        ids, coefs = orc.route_softmax_topk(orc.router_logits_f32(moe_state["router_w"], x), TOP_K)
+        out["configs[2]_last_token"] = same(moe_state["last_y"],
+                                             orc.moe_routed_by_id(ex, ids, coefs, orc_exp, orc_sh, x))
+        if batch_check is not None:
+            bc = batch_check
+            ok = True
+            for t in range(0, BATCH_TOKENS, 9):
+                want = orc.moe_routed_by_id(ex, bc["ids"][t], bc["coefs"][t], orc_exp, orc_sh, bc["xs"][t],
+                                            preflight=False)
+                ok = ok and same(bc["ys"][t], want)
+            out["configs[3]_tokens_0_9_18_.._63"] = ok
+    return out
+
+
+PF_TOKENS, PF_ROWS = 512, 12288
+PF_OPS = 2 * PF_TOKENS * PF_ROWS * HIDDEN                                 # 51,539,607,552
+PF_BYTES = PF_ROWS * 16 * 176 + PF_TOKENS * Q8(HIDDEN) + PF_TOKENS * PF_ROWS * 4   # 62,160,896
+MFMA_I8_PEAK_TOPS = 5000.0
+
+
+def bench_prefill(args, be, timer, torch, np, synth):
+    """Q8_K activations [512 x 4096] x Q5_K [12288 x 4096] -> f32
+    [512 x 12288] on the i8 matrix cores (lbh_gemm_q8_k: activation tiles + GEMM)."""
+    w = synth.random_matrix(synth.Q5_K, PF_ROWS, HIDDEN, seed=801)
+    copies = 4   # 4 x (34.6 MB packed + 113 MB MFMA-ready) in rotation: > the 256 MB Infinity Cache
+    wd = torch.from_numpy(w.reshape(-1)).cuda()
+    ms = [be.upload(synth.Q5_K, PF_ROWS, HIDDEN, wd) for _ in range(copies)]
+    for m in ms:
+        m.prepare_gemm()
+    del wd
+    x = torch.from_numpy(np.random.default_rng(802).standard_normal((PF_TOKENS, HIDDEN)).astype(np.float32)).cuda()
+    q8 = torch.zeros((PF_TOKENS, Q8(HIDDEN)), dtype=torch.uint8, device="cuda")
+    be.quantize_q8_k_rows(x, q8, PF_TOKENS, HIDDEN)
+    ws = torch.zeros(be.gemm_workspace_bytes(PF_TOKENS, HIDDEN), dtype=torch.uint8, device="cuda")
+    ys = torch.zeros((copies, PF_TOKENS, PF_ROWS), dtype=torch.float32, device="cuda")
+    g = timer.graph(lambda: [be.gemm_q8_k(ms[c], q8, PF_TOKENS, ys[c], ws) for c in range(copies)])
+    timer.time(g, 2)
+    reps = 10
+    us = timer.time(g, reps) / (reps * copies) * 1e6
+    torch.cuda.synchronize()
+    tops = PF_OPS / us / 1e6
+    res = {"workload": "configs[4]: prefill 512 tokens, Q8_K activations [512 x 4096] x Q5_K [12288 x 4096] -> f32 "
+                       "[512 x 12288], i8 MFMA (v_mfma_i32_32x32x32_i8) with exact per-(block, lane residue) sums",
+           "us_per_step": round(us, 2), "int8_TOPS": round(tops, 2),
+           "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
+                        "frac": round(tops / MFMA_I8_PEAK_TOPS, 4)},
+           "hbm_GB/s_algorithmic": round(PF_BYTES / us / 1e3, 1),
+           "note": "the exact per-block f32 folds (9 chains x 16 blocks per output, separately rounded) run on the "
+                   "VALU at ~38 ops per (row, token, block) and bound the kernel, not the matrix cores"}
+    check = dict(w=w, q8=q8[:8].cpu().numpy(), y=ys[copies - 1, :8].cpu().numpy())
+    for m in ms:
+        m.close()
+    return res, check
+
+
+def cpu_prefill(check, seconds):
+    """Oracle per-row dots (the reference's only path: vec_dot_q8_k row by row,
+    token by token) for a bounded sample of the prefill's tokens."""
+    import numpy as np
+    from oracle import lb_oracle as orc
+    threads = cpu_threads()
+    ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
+    om = orc.make_matrix(13, PF_ROWS, HIDDEN, check["w"])
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.gemv_prequantized(ex, om, check["q8"][n % 8])
+        n += 1
+        el = time.perf_counter() - t0
+        if (el >= seconds and n >= 2) or el >= 2 * seconds:
+            break
+    ops = 2.0 * PF_ROWS * HIDDEN * n
+    return {"value": round(ops / el / 1e12, 5), "unit": "TOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n} tokens x 12288 rows of Q5_K dots (gemv over pre-quantized Q8_K) in {el:.2f} s, "
+                      f"{threads} threads; the full 512-token step would take {512 * el / n:.2f} s"}
 
 
 def main():
@@ -320,9 +476,11 @@ def main():
 
     mv = bench_matvec_step(args, be, timer, torch, np, synth)
     w_q4k, q4k = bench_q4k(args, be, timer, torch, np, synth)
-    moe = None
+    moe = state = batch = batch_check = None
+    prefill, pf_check = bench_prefill(args, be, timer, torch, np, synth)
     if not args.no_moe:
-        moe, experts_np, shared_np, router_w, xs_np = bench_moe(args, be, timer, torch, np, synth, lbhip)
+        moe, state = bench_moe(args, be, timer, torch, np, synth, lbhip)
+        batch, batch_check = bench_batch(args, be, timer, torch, np, synth, state)
 
     value = STEP_BYTES / (mv["ms_per_step"] * 1e-3) / 1e9
     if mv["down_us"] >= mv["gate_us"]:
@@ -353,21 +511,30 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2]},
         "kernels_us": {"iq2s_gate": round(mv["gate_us"], 3), "iq3s_down": round(mv["down_us"], 3)},
-        "parity_last_step_bit_exact": mv["parity"],
         "q4k_matvec": q4k,
+        "prefill_gemm": prefill,
     }
     if moe is not None:
         line["moe_block"] = moe
+        line["moe_batch"] = batch
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds)
         cq = cpu_q4k(w_q4k, args.cpu_seconds / 2)
         q4k["cpu_baseline"] = cq
         q4k["speedup_vs_cpu"] = round(q4k["GB/s"] / cq["value"], 1)
         if moe is not None:
-            cm = cpu_moe(experts_np, shared_np, router_w, xs_np, args.cpu_seconds)
+            cm = cpu_moe(state["experts_np"], state["shared_np"], state["router_w"], state["xs_np"], args.cpu_seconds)
             moe["cpu_baseline"] = cm
             moe["speedup_vs_cpu"] = round(moe["with_device_router"]["tokens_per_s"] / cm["value"], 1)
             moe["speedup_vs_cpu_routing_given"] = round(moe["routing_given"]["tokens_per_s"] / cm["value"], 1)
+            cb = cpu_batch(state["experts_np"], state["shared_np"], batch_check, args.cpu_seconds / 2)
+            batch["cpu_baseline"] = cb
+            batch["speedup_vs_cpu"] = round(batch["tokens_per_s"] / cb["value"], 1)
+        cp = cpu_prefill(pf_check, args.cpu_seconds / 2)
+        prefill["cpu_baseline"] = cp
+        prefill["speedup_vs_cpu"] = round(prefill["int8_TOPS"] / cp["value"], 1)
+        line["parity_spot_checks_bit_exact"] = cpu_parity(mv, state, batch_check)
+        line["parity_spot_checks_bit_exact"]["configs[4]_tokens_0_7"] = _prefill_parity(pf_check)
     print(json.dumps(line), flush=True)
 
 

@@ -24,7 +24,7 @@ struct lbh_ctx {
     DevStatus *status;        // device
     DevStatus *status_host;   // pinned mirror
     GemvTuning tuning;
-    int gemm_shape;           // workgroup shape of the K-quant GEMM (0: 2x2 waves)
+    int gemm_shape;           // workgroup shape of the K-quant GEMM (0: 2 x 4 waves)
 };
 
 struct lbh_matrix {
@@ -477,6 +477,8 @@ struct lbh_moe {
     float *batch_coefs;
     int32_t *plan_host;       // pinned
     int tc, rt_gu_r, rt_gu_s, rt_d_r, rt_d_s;
+    uint8_t *shared_gemm_mem; // MFMA-ready copies of a K-quant shared expert (batched calls)
+    size_t gemm_off[6];       // (A, d/dmin) offsets of gate, up, down in shared_gemm_mem
 };
 
 namespace {
@@ -486,6 +488,7 @@ void free_moe(lbh_moe *m) {
     DeviceGuard g(m->device);
     if (m->experts_dev) (void)hipFree(m->experts_dev);
     if (m->batch_mem) (void)hipFree(m->batch_mem);
+    if (m->shared_gemm_mem) (void)hipFree(m->shared_gemm_mem);
     if (m->plan_host) (void)hipHostFree(m->plan_host);
     if (m->h) (void)hipFree(m->h);
     if (m->status) (void)hipFree(m->status);
@@ -585,10 +588,10 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
     }
     m->tile_d = 16;
     m->tc = 8;
-    m->rt_gu_r = 128;
-    m->rt_gu_s = 128;
-    m->rt_d_r = 320;
-    m->rt_d_s = 128;
+    m->rt_gu_r = 64;
+    m->rt_gu_s = 64;
+    m->rt_d_r = 160;
+    m->rt_d_s = 64;
     const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
     m->h_stride = (int)max_ffn;
     const size_t slots = MOE_MAX_ROUTED + 1;
@@ -859,6 +862,8 @@ BatchArgs batch_args(const lbh_moe *m, const uint32_t *ids, const float *coefs, 
     return a;
 }
 
+bool is_kquant(int ty) { return ty == LBH_Q4_K || ty == LBH_Q5_K; }
+
 }  // namespace
 
 extern "C" {
@@ -894,6 +899,16 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     const size_t o_q8hr = take(P * nbr * 292), o_q8hs = take(T * nbs * 292);
     const size_t o_dr = take(P * m->hidden * 4), o_ds = take(T * m->hidden * 4);
     const size_t o_ids = take(P * 4), o_coefs = take(P * 4);
+    // A K-quant shared expert runs on the matrix cores: gate/up outputs and the
+    // GEMM activation tiles of x and h_s.
+    const bool sgemm = m->has_shared && is_kquant(m->shared.gate.type) && is_kquant(m->shared.down.type);
+    size_t o_gs = 0, o_us = 0, o_bx = 0, o_bh = 0;
+    if (sgemm) {
+        o_gs = take(T * ffn_s * 4);
+        o_us = take(T * ffn_s * 4);
+        o_bx = take(gemm_b_bytes((int)T, (int)nbh));
+        o_bh = take(gemm_b_bytes((int)T, (int)nbs));
+    }
     hipError_t e = hipMalloc(&m->batch_mem, off);
     if (e == hipSuccess) e = hipMemset(m->batch_mem, 0, off);
     if (e == hipSuccess && !m->plan_host) e = hipHostMalloc(&m->plan_host, 16, hipHostMallocDefault);
@@ -923,6 +938,46 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     a.d_s = reinterpret_cast<float *>(b + o_ds);
     m->batch_ids = reinterpret_cast<uint32_t *>(b + o_ids);
     m->batch_coefs = reinterpret_cast<float *>(b + o_coefs);
+    a.shared_gemm = sgemm ? 1 : 0;
+    if (sgemm) {
+        a.g_s = reinterpret_cast<float *>(b + o_gs);
+        a.u_s = reinterpret_cast<float *>(b + o_us);
+        a.bx = b + o_bx;
+        a.d8x = reinterpret_cast<float *>(b + o_bx + (T + 31) / 32 * nbh * 9216);
+        a.bh = b + o_bh;
+        a.d8h = reinterpret_cast<float *>(b + o_bh + (T + 31) / 32 * nbs * 9216);
+        if (!m->shared_gemm_mem) {
+            // MFMA-ready copies of the shared gate, up and down (built once).
+            const MatView v[3] = {m->shared.gate, m->shared.up, m->shared.down};
+            size_t so = 0, oa[3], od[3];
+            for (int i = 0; i < 3; ++i) {
+                oa[i] = so;
+                so += (gemm_a_bytes(v[i].rows, v[i].nb) + 255) & ~(size_t)255;
+                od[i] = so;
+                so += (gemm_dm_bytes(v[i].rows, v[i].nb) + 255) & ~(size_t)255;
+            }
+            e = hipMalloc(&m->shared_gemm_mem, so);
+            for (int i = 0; i < 3 && e == hipSuccess; ++i)
+                e = launch_prep_a(v[i], m->shared_gemm_mem + oa[i], reinterpret_cast<float2 *>(m->shared_gemm_mem + od[i]),
+                                  nullptr);
+            if (e == hipSuccess) e = hipDeviceSynchronize();
+            if (e != hipSuccess) {
+                if (m->shared_gemm_mem) (void)hipFree(m->shared_gemm_mem);
+                m->shared_gemm_mem = nullptr;
+                (void)hipFree(m->batch_mem);
+                m->batch_mem = nullptr;
+                m->cap_tokens = m->cap_k = 0;
+                return hip_fail(err, e);
+            }
+            m->gemm_off[0] = oa[0], m->gemm_off[1] = od[0], m->gemm_off[2] = oa[1];
+            m->gemm_off[3] = od[1], m->gemm_off[4] = oa[2], m->gemm_off[5] = od[2];
+        }
+        uint8_t *g = m->shared_gemm_mem;
+        const int ffs = (int)ffn_s, hid = (int)m->hidden;
+        a.sg = MatGemm{g + m->gemm_off[0], reinterpret_cast<const float2 *>(g + m->gemm_off[1]), a.g_s, ffs, ffs};
+        a.su = MatGemm{g + m->gemm_off[2], reinterpret_cast<const float2 *>(g + m->gemm_off[3]), a.u_s, ffs, ffs};
+        a.sd = MatGemm{g + m->gemm_off[4], reinterpret_cast<const float2 *>(g + m->gemm_off[5]), a.d_s, hid, hid};
+    }
     m->cap_tokens = max_tokens;
     m->cap_k = top_k;
     return ok(err);
@@ -950,8 +1005,9 @@ lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, 
     if (n_tokens == 0 || top_k == 0) return LBH_DIMENSION_MISMATCH;
     if (!m->batch_mem || n_tokens > m->cap_tokens || top_k > m->cap_k) return LBH_SCRATCH_TOO_SMALL;
     DeviceGuard g(ctx->device);
-    if (launch_moe_batch(batch_args(m, ids, coefs, n_tokens, top_k, x, y), ctx->stream) != hipSuccess)
-        return LBH_HIP_ERROR;
+    BatchArgs a = batch_args(m, ids, coefs, n_tokens, top_k, x, y);
+    a.gemm_shape = ctx->gemm_shape;
+    if (launch_moe_batch(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;
 }
 
@@ -993,7 +1049,8 @@ lbh_status lbh_moe_routed_by_id_batch_into(lbh_ctx *ctx, lbh_moe *m, const uint3
     }
     HIP_TRY(hipMemcpyAsync(m->batch_ids, ids, n_tokens * top_k * 4, hipMemcpyHostToDevice, ctx->stream));
     HIP_TRY(hipMemcpyAsync(m->batch_coefs, coefs, n_tokens * top_k * 4, hipMemcpyHostToDevice, ctx->stream));
-    const BatchArgs a = batch_args(m, m->batch_ids, m->batch_coefs, n_tokens, top_k, input, output);
+    BatchArgs a = batch_args(m, m->batch_ids, m->batch_coefs, n_tokens, top_k, input, output);
+    a.gemm_shape = ctx->gemm_shape;
     HIP_TRY(launch_moe_batch(a, ctx->stream));
     HIP_TRY(hipMemcpyAsync(m->plan_host, a.plan, 8, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));

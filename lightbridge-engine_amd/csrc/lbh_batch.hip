@@ -391,11 +391,12 @@ constexpr int mb_lpu() {
 // (the other workgroups, four blocks per wave).
 __device__ __forceinline__ void quantize_rows_out(const float *x, long long nblocks, long long first, uint8_t *plain,
                                                   uint8_t *rm, uint8_t *lds_wave) {
-    // Four blocks per call into the wave's LDS, then out to global memory: the
-    // GGML bytes, and (rm != NULL) the copy with residue-major qs.
+    // Blocks [first, first + 4) (x points at block `first`) into the wave's
+    // LDS, then out to global memory: the GGML bytes, and (rm != NULL) the copy
+    // with residue-major qs.
     const int lane = threadIdx.x & 63;
     const long long cnt = nblocks - first < 4 ? nblocks - first : 4;
-    quantize_blocks_wave(x + first * 256, lds_wave, 0, cnt);
+    quantize_blocks_wave(x, lds_wave, 0, cnt);
     wave_sync();
     const int dw = (int)cnt * 73;
     for (int k = lane; k < dw; k += 64) {
@@ -423,11 +424,9 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_prep(BatchArgs a) {
         const int nb = a.hidden / 256;
         const long long nblocks = (long long)a.n_tokens * nb;
         const long long first = ((long long)(blockIdx.x - 1) * MB_WAVES + (tid >> 6)) * 4;
+        const bool rm = a.has_shared && !a.shared_gemm && (a.shared.gate.type == T_Q4_K || a.shared.gate.type == T_Q5_K);
         if (first < nblocks)
-            quantize_rows_out(a.x, nblocks, first, a.q8x, a.has_shared && (a.shared.gate.type == T_Q4_K ||
-                                                                           a.shared.gate.type == T_Q5_K)
-                                                              ? a.q8x_rm
-                                                              : nullptr,
+            quantize_rows_out(a.x + first * 256, nblocks, first, a.q8x, rm ? a.q8x_rm : nullptr,
                               smem + (tid >> 6) * 4 * 292);
         return;
     }
@@ -565,22 +564,40 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
 }
 
 // Q8_K of every h row (quantize_row_q8_k_into of each down projection's
-// input): routed rows [0, pairs), then the shared rows.
-__global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shared_rm) {
+// input): routed rows [0, pairs), then the shared rows.  shared_mode 1: the
+// shared copy has residue-major qs (VALU K-quant down); 2: the shared h is
+// SwiGLU(g_s, u_s) of the matrix-core gate/up, formed here (activation.rs:170-178).
+__global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shared_mode) {
     __shared__ __align__(16) uint8_t lds[MB_WAVES * 4 * 292];
+    __shared__ __align__(16) float hbuf[MB_WAVES][4 * 256];
     if (a.plan[1]) return;
     const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const long long br = (long long)a.n_tokens * a.top_k * nbr;
+    const long long brp = (br + 3) & ~3ll;   // chunks of four never straddle the two ranges
     const long long bs = a.has_shared ? (long long)a.n_tokens * nbs : 0;
-    const long long chunk = ((long long)blockIdx.x * MB_WAVES + (threadIdx.x >> 6)) * 4;
-    uint8_t *lw = lds + (threadIdx.x >> 6) * 4 * 292;
-    // Chunks of four never straddle the two ranges: br is a multiple of 4
-    // whenever a chunk would (chunk starts are multiples of 4).
+    const long long chunk = ((long long)blockIdx.x * MB_WAVES + wid) * 4;
+    uint8_t *lw = lds + wid * 4 * 292;
     if (chunk < br) {
-        quantize_rows_out(a.h_r, br, chunk, a.q8h_r, nullptr, lw);
-    } else if (chunk - ((br + 3) & ~3ll) < bs && chunk >= ((br + 3) & ~3ll)) {
-        const long long f = chunk - ((br + 3) & ~3ll);
-        quantize_rows_out(a.h_s, bs, f, shared_rm ? nullptr : a.q8h_s, shared_rm ? a.q8h_s : nullptr, lw);
+        quantize_rows_out(a.h_r + chunk * 256, br, chunk, a.q8h_r, nullptr, lw);
+    } else if (chunk >= brp && chunk - brp < bs) {
+        const long long f = chunk - brp;
+        if (shared_mode == 2) {
+            // lane (block q = lane / 16, elements 16 (lane % 16) ..) forms the
+            // sixteen values it quantizes below
+            const long long blk = f + (lane >> 4);
+            if (blk < bs) {
+                const long long base = blk * 256 + 16 * (lane & 15);
+                float *hb = &hbuf[wid][(lane >> 4) * 256 + 16 * (lane & 15)];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) hb[i] = swiglu_ref(a.g_s[base + i], a.u_s[base + i]);
+            }
+            wave_sync();
+            quantize_rows_out(&hbuf[wid][0], bs, f, a.q8h_s, nullptr, lw);
+        } else {
+            quantize_rows_out(a.h_s + f * 256, bs, f, shared_mode ? nullptr : a.q8h_s, shared_mode ? a.q8h_s : nullptr,
+                              lw);
+        }
     }
 }
 
@@ -764,17 +781,46 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(k_mb_prep, dim3(1 + cdiv((long long)a.n_tokens * nbh, 4 * MB_WAVES)), dim3(MB_THREADS), lds[0],
                        s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (a.has_shared && (e = gate_up_any<true>(tsg, a, lds[2], s)) != hipSuccess) return e;
+    if (a.has_shared && a.shared_gemm) {
+        // shared gate/up on the matrix cores, beside nothing: they only need Q8_K(x)
+        GemmArgs gm{};
+        gm.b = a.bx;
+        gm.d8 = a.d8x;
+        gm.nb = nbh;
+        gm.n_tokens = a.n_tokens;
+        gm.shape = a.gemm_shape;
+        gm.n_mat = 2;
+        gm.mat[0] = a.sg;
+        gm.mat[1] = a.su;
+        if ((e = launch_prep_b(a.q8x, a.n_tokens, nbh, a.bx, a.d8x, s)) != hipSuccess) return e;
+        if ((e = launch_kq_gemm(gm, s)) != hipSuccess) return e;
+    } else if (a.has_shared && (e = gate_up_any<true>(tsg, a, lds[2], s)) != hipSuccess) {
+        return e;
+    }
     if ((e = gate_up_any<false>(a.type_gate_r, a, lds[1], s)) != hipSuccess) return e;
 
     const bool rm = tsd == T_Q4_K || tsd == T_Q5_K;
+    const int mode = !a.has_shared ? 0 : a.shared_gemm ? 2 : rm ? 1 : 0;
     const long long br = (long long)a.n_tokens * a.top_k * (a.ffn_r / 256);
     const long long bs = a.has_shared ? (long long)a.n_tokens * (a.ffn_s / 256) : 0;
-    hipLaunchKernelGGL(k_mb_quant_h, dim3(cdiv(((br + 3) & ~3ll) + bs, 4 * MB_WAVES)), dim3(MB_THREADS), 0, s, a,
-                       rm ? 1 : 0);
+    hipLaunchKernelGGL(k_mb_quant_h, dim3(cdiv(((br + 3) & ~3ll) + bs, 4 * MB_WAVES)), dim3(MB_THREADS), 0, s, a, mode);
     if ((e = hipGetLastError()) != hipSuccess) return e;
 
-    if (a.has_shared && (e = down_any<true>(tsd, a, lds[4], s)) != hipSuccess) return e;
+    if (a.has_shared && a.shared_gemm) {
+        const int nbs = a.ffn_s / 256;
+        GemmArgs gm{};
+        gm.b = a.bh;
+        gm.d8 = a.d8h;
+        gm.nb = nbs;
+        gm.n_tokens = a.n_tokens;
+        gm.shape = a.gemm_shape;
+        gm.n_mat = 1;
+        gm.mat[0] = a.sd;
+        if ((e = launch_prep_b(a.q8h_s, a.n_tokens, nbs, a.bh, a.d8h, s)) != hipSuccess) return e;
+        if ((e = launch_kq_gemm(gm, s)) != hipSuccess) return e;
+    } else if (a.has_shared && (e = down_any<true>(tsd, a, lds[4], s)) != hipSuccess) {
+        return e;
+    }
     if ((e = down_any<false>(a.type_down_r, a, lds[3], s)) != hipSuccess) return e;
 
     const long long total = (long long)a.n_tokens * a.hidden;

@@ -364,8 +364,8 @@ static hipError_t gemm_shape(const GemmArgs &g, hipStream_t s) {
 hipError_t launch_kq_gemm(const GemmArgs &g, hipStream_t s) {
     if (g.n_mat < 1 || g.n_mat > GEMM_MAX_MATS || g.n_tokens < 1 || g.nb < 1) return hipErrorInvalidValue;
     switch (g.shape) {
-    case 0: return gemm_shape<2, 2>(g, s);
-    case 1: return gemm_shape<2, 4>(g, s);
+    case 0: return gemm_shape<2, 4>(g, s);
+    case 1: return gemm_shape<2, 2>(g, s);
     case 2: return gemm_shape<4, 2>(g, s);
     default: return gemm_shape<1, 4>(g, s);
     }

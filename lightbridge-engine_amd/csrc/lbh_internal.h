@@ -112,6 +112,26 @@ struct MoeArgs {
     RouterArgs router;
 };
 
+// ------------------------------------------------ K-quant GEMM on i8 MFMA
+
+constexpr int GEMM_MAX_MATS = 3;
+
+// One matrix of a GEMM launch: its MFMA-ready copy (A tiles, d/dmin) and output.
+struct MatGemm {
+    const uint8_t *a;      // [ceil(rows / 16)][nb] tiles of 9 KiB
+    const float2 *dm;      // [ceil(rows / 16) * 16][nb] (d, dmin)
+    float *y;              // y[t * ldy + r]
+    int32_t rows;
+    int32_t ldy;
+};
+
+struct GemmArgs {
+    MatGemm mat[GEMM_MAX_MATS];   // matrices sharing K and the activations
+    const uint8_t *b;             // [ceil(n_tokens / 32)][nb] tiles of 9 KiB
+    const float *d8;              // [ceil(n_tokens / 32)][nb][32]
+    int32_t n_mat, nb, n_tokens, shape;
+};
+
 // ------------------------------------------------------ batched MoE decode
 
 constexpr int BATCH_MAX_TOKENS = 256;
@@ -148,6 +168,13 @@ struct BatchArgs {
     int32_t rt_gu_r, rt_gu_s;   // gate/up rows per workgroup (routed, shared)
     int32_t rt_d_r, rt_d_s;     // down rows per workgroup (routed, shared)
     int32_t type_gate_r, type_down_r;
+    // K-quant shared expert on the i8 matrix cores: gate/up -> g_s/u_s, SwiGLU
+    // fused into the h quantization, down -> d_s.
+    int32_t shared_gemm, gemm_shape;
+    MatGemm sg, su, sd;         // MFMA-ready copies of the shared gate / up / down
+    float *g_s, *u_s;           // [n_tokens][ffn_s]
+    uint8_t *bx, *bh;           // GEMM activation tiles of x and of h_s
+    float *d8x, *d8h;
 };
 
 // Batch selection: top-k of each token's finished logits (select_route).
@@ -159,26 +186,6 @@ struct RouteBatchArgs {
     unsigned long long *status; // optional: (token << 32 | expert << 2 | field), min over the batch
     int32_t n_tokens;
     int32_t pad;
-};
-
-// ------------------------------------------------ K-quant GEMM on i8 MFMA
-
-constexpr int GEMM_MAX_MATS = 3;
-
-// One matrix of a GEMM launch: its MFMA-ready copy (A tiles, d/dmin) and output.
-struct MatGemm {
-    const uint8_t *a;      // [ceil(rows / 16)][nb] tiles of 9 KiB
-    const float2 *dm;      // [ceil(rows / 16) * 16][nb] (d, dmin)
-    float *y;              // y[t * ldy + r]
-    int32_t rows;
-    int32_t ldy;
-};
-
-struct GemmArgs {
-    MatGemm mat[GEMM_MAX_MATS];   // matrices sharing K and the activations
-    const uint8_t *b;             // [ceil(n_tokens / 32)][nb] tiles of 9 KiB
-    const float *d8;              // [ceil(n_tokens / 32)][nb][32]
-    int32_t n_mat, nb, n_tokens, shape;
 };
 
 size_t gemm_a_bytes(int rows, int nb);
