@@ -52,6 +52,10 @@ MOE_WEIGHT_BYTES = (TOP_K * (2 * FFN * 16 * 82 + HIDDEN * 6 * 110) + 2 * HIDDEN 
 EXPERT_BYTES = 2 * FFN * 16 * 82 + HIDDEN * 6 * 110                    # 6,733,824 per routed expert
 SHARED_BYTES = 2 * HIDDEN * 16 * 144 + HIDDEN * 16 * 176               # 30,408,704
 BATCH_TOKENS = 64
+# HBM bytes per launch (read + write) measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain copy of
+# known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
+MEASURED_TRAFFIC = {"gate": 2355397 + 6144, "down": 2965999 + 19648, "prefill": 220835137 + 25170528}
 
 
 def parse():
@@ -65,6 +69,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on each CPU baseline sample")
     ap.add_argument("--lpu", type=int, default=0, help="matvec lanes per (row, block) unit (0 = library default)")
     ap.add_argument("--batch-reps", type=int, default=8, help="timed replays of the 8-step configs[3] graph")
+    ap.add_argument("--pmc-workloads", action="store_true",
+                    help="run a few dispatches of each workload for rocprofv3 --pmc passes and exit")
     return ap.parse_args()
 
 
@@ -425,7 +431,7 @@ def bench_prefill(args, be, timer, torch, np, synth):
                        "[512 x 12288], i8 MFMA (v_mfma_i32_32x32x32_i8) with exact per-(block, lane residue) sums",
            "us_per_step": round(us, 2), "int8_TOPS": round(tops, 2),
            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
-                        "frac": round(tops / MFMA_I8_PEAK_TOPS, 4)},
+                        "frac": round(tops / MFMA_I8_PEAK_TOPS, 4), "traffic": MEASURED_TRAFFIC["prefill"]},
            "hbm_GB/s_algorithmic": round(PF_BYTES / us / 1e3, 1),
            "note": "the exact per-block f32 folds (9 chains x 16 blocks per output, separately rounded) run on the "
                    "VALU at ~38 ops per (row, token, block) and bound the kernel, not the matrix cores"}
@@ -456,11 +462,82 @@ def cpu_prefill(check, seconds):
                       f"{threads} threads; the full 512-token step would take {512 * el / n:.2f} s"}
 
 
+def pmc_workloads():
+    """A few dispatches of every hot-path kernel at the bench shapes, for the
+    rocprofv3 --pmc passes (one counter set per run), plus a plain 64 MiB copy
+    that calibrates FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    import lbhip
+    from lbhip import synth
+    be = lbhip.HipBackend(0)
+    H, F = HIDDEN, FFN
+    # calibration copy: 64 MiB read + 64 MiB written
+    a = torch.empty(64 << 20, dtype=torch.uint8, device='cuda').fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    # configs[1] matvecs on distinct weight copies
+    wg = torch.from_numpy(synth.random_matrix(22, F, H, 101).reshape(-1)).cuda()
+    wd = torch.from_numpy(synth.random_matrix(21, H, F, 102).reshape(-1)).cuda()
+    gates = [be.upload(22, F, H, wg) for _ in range(16)]
+    downs = [be.upload(21, H, F, wd) for _ in range(16)]
+    x = torch.randn(H, device='cuda'); h = torch.zeros(F, device='cuda'); y = torch.zeros(H, device='cuda')
+    torch.cuda.synchronize()
+    for c in range(16):
+        be.gemv_f32(gates[c], x, h)
+        be.gemv_f32(downs[c], h, y)
+    torch.cuda.synchronize()
+    # configs[0] Q4_K matvec
+    wq = torch.from_numpy(synth.random_matrix(12, H, H, 111).reshape(-1)).cuda()
+    qs = [be.upload(12, H, H, wq) for _ in range(8)]
+    torch.cuda.synchronize()
+    for c in range(8):
+        be.gemv_f32(qs[c], x, y)
+    torch.cuda.synchronize()
+    # configs[2] MoE block (48 experts, top-8) and configs[3] batch
+    NE = 48
+    wu = torch.from_numpy(synth.random_matrix(22, F, H, 103).reshape(-1)).cuda()
+    experts = [(be.upload(22, F, H, torch.roll(wg, 82 * e)), be.upload(22, F, H, torch.roll(wu, 82 * e)),
+                be.upload(21, H, F, torch.roll(wd, 110 * e))) for e in range(NE)]
+    shared = (be.upload(12, H, H, synth.random_matrix(12, H, H, 304)), be.upload(12, H, H, synth.random_matrix(12, H, H, 305)),
+              be.upload(13, H, H, synth.random_matrix(13, H, H, 306)))
+    moe = be.moe_create(experts, shared)
+    router = lbhip.Router(be, synth.router_weights(NE, H, 307))
+    xs = torch.randn(8, H, device='cuda'); ys = torch.zeros(8, H, device='cuda')
+    torch.cuda.synchronize()
+    for t in range(8):
+        lbhip.moe_block_forward(be, moe, router, xs[t], ys[t], 8)
+    torch.cuda.synchronize()
+    moe.reserve_batch(64, 8)
+    logits = torch.from_numpy(synth.zipf_routes(64, NE, 8, 1.1, seed=500)).cuda()
+    ids = torch.zeros((64, 8), dtype=torch.int32, device='cuda'); coefs = torch.zeros((64, 8), device='cuda')
+    xb = torch.randn(64, H, device='cuda'); yb = torch.zeros(64, H, device='cuda')
+    for _ in range(2):
+        be.route_experts_batch(logits, 8, ids, coefs)
+        be.moe_forward_batch(moe, ids, coefs, xb, yb)
+    torch.cuda.synchronize()
+    # configs[4] prefill GEMM
+    R, T = 12288, 512
+    m5 = be.upload(13, R, H, synth.random_matrix(13, R, H, 801)); m5.prepare_gemm()
+    q8 = torch.zeros((T, 16 * 292), dtype=torch.uint8, device='cuda')
+    be.quantize_q8_k_rows(torch.randn(T, H, device='cuda'), q8, T, H)
+    ws = torch.zeros(be.gemm_workspace_bytes(T, H), dtype=torch.uint8, device='cuda')
+    yp = torch.zeros((T, R), device='cuda')
+    for _ in range(2):
+        be.gemm_q8_k(m5, q8, T, yp, ws)
+    torch.cuda.synchronize()
+    print("pmc workloads done", flush=True)
+
+
 def main():
     args = parse()
+    if args.pmc_workloads:
+        pmc_workloads()
+        return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build runs on a "
-              f"single MI355X; DESIGN.md describes how the path shards)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build runs on a "
+              f"single MI355X (the multi-GPU sharding of the path is a design, not built)", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -484,9 +561,9 @@ def main():
 
     value = STEP_BYTES / (mv["ms_per_step"] * 1e-3) / 1e9
     if mv["down_us"] >= mv["gate_us"]:
-        dom = ("k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)", mv["down_us"], DOWN_BYTES)
+        dom = ("k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)", mv["down_us"], DOWN_BYTES, MEASURED_TRAFFIC["down"])
     else:
-        dom = ("k_gemv<IQ2_S, fused Q8_K> (gate 1536x4096)", mv["gate_us"], GATE_BYTES)
+        dom = ("k_gemv<IQ2_S, fused Q8_K> (gate 1536x4096)", mv["gate_us"], GATE_BYTES, MEASURED_TRAFFIC["gate"])
     achieved = dom[2] / (dom[1] * 1e-6) / 1e9
     line = {
         "metric": "quant matvec HBM GB/s (% of MI355X peak); MoE-block decode tokens/s",
@@ -508,7 +585,7 @@ def main():
                    "rotation_bytes": mv["copies"] * (mv["w_gate"].nbytes + mv["w_down"].nbytes),
                    "algorithmic_bytes_per_step": STEP_BYTES, "lpu": args.lpu},
         "roofline": {"bound": "hbm", "kernel": dom[0], "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dom[3],
                      "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2]},
         "kernels_us": {"iq2s_gate": round(mv["gate_us"], 3), "iq3s_down": round(mv["down_us"], 3)},
         "q4k_matvec": q4k,

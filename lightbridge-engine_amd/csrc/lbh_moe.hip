@@ -326,7 +326,7 @@ static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b)
 // or IQ2_S shared down.  Two lanes per (row, block) unit.
 template <int TY>
 constexpr int moe_lpu() {
-    return 2;
+    return TY == T_Q5_K ? 4 : 2;
 }
 
 template <int TYR, int TYS>
