@@ -104,7 +104,8 @@ lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream);
 enum lbh_tuning_key {
     LBH_TUNE_GEMV_LPU = 1,         /* lanes per (row, block) unit: 1, 2 or 4 */
     LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop */
-    LBH_TUNE_GEMM_SHAPE = 3,       /* K-quant GEMM workgroup: 0 = 2x4, 1 = 2x2, 2 = 4x2, 3 = 1x4 waves (rows x tokens) */
+    LBH_TUNE_GEMM_SHAPE = 3,
+    LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 2, 3 or 4 */       /* K-quant GEMM workgroup: 0 = 2x4, 1 = 2x2, 2 = 4x2, 3 = 1x4 waves (rows x tokens) */
 };
 lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value);
 /* Compute units of the context's device. */

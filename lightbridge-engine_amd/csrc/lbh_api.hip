@@ -195,6 +195,10 @@ lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
         if (value < 0) return LBH_INVALID_PARAMETER;
         ctx->tuning.max_blocks = value ? value : 8 * ctx->cu_count;
         return LBH_OK;
+    case LBH_TUNE_GEMV_DEPTH:
+        if (value < 0 || value == 1 || value > 4) return LBH_INVALID_PARAMETER;
+        ctx->tuning.depth = value;
+        return LBH_OK;
     case LBH_TUNE_GEMM_SHAPE:
         if (value < 0 || value > 3) return LBH_INVALID_PARAMETER;
         ctx->gemm_shape = value;

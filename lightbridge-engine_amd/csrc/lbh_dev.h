@@ -128,24 +128,39 @@ __device__ __forceinline__ int32_t nearest_int(float v) {
 // lanes reduces the maximum, and the lowest lane holding it (a ballot) owns
 // the first index, since lane order is element order.  bsums[g] covers
 // exactly the 16 elements of lane g.
-__device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x, uint8_t *out, long long first,
-                                                     long long nblocks) {
-    const int lane = threadIdx.x & 63;
-    const int li = lane & 15;
-    const long long blk = first + (lane >> 4);
-    const bool valid = blk < nblocks;
+//
+// Split in two so a kernel can issue these loads before its weight loads
+// (vector loads complete in order for waiting purposes: inputs requested
+// after a burst of weight loads would wait for the whole burst).
+struct QuantIn {
     float v[16];
-    if (valid) {
-        const float4 *src = reinterpret_cast<const float4 *>(x + blk * 256 + 16 * li);
+    long long blk;
+    bool valid;
+};
+
+__device__ __forceinline__ QuantIn quantize_load(const float *__restrict__ x, long long first, long long nblocks) {
+    QuantIn q;
+    const int li = threadIdx.x & 15;
+    q.blk = first + ((threadIdx.x & 63) >> 4);
+    q.valid = q.blk < nblocks;
+    if (q.valid) {
+        const float4 *src = reinterpret_cast<const float4 *>(x + q.blk * 256 + 16 * li);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 f = src[i];
-            v[4 * i] = f.x, v[4 * i + 1] = f.y, v[4 * i + 2] = f.z, v[4 * i + 3] = f.w;
+            q.v[4 * i] = f.x, q.v[4 * i + 1] = f.y, q.v[4 * i + 2] = f.z, q.v[4 * i + 3] = f.w;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = 0.0f;
+        for (int i = 0; i < 16; ++i) q.v[i] = 0.0f;
     }
+    return q;
+}
+
+__device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out) {
+    const int lane = threadIdx.x & 63;
+    const int li = lane & 15;
+    const float *v = q.v;
     uint32_t amax_l = __float_as_uint(fabsf(v[0]));
     float max_l = v[0];
 #pragma unroll
@@ -170,16 +185,16 @@ __device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x
         const float iscale = -127.0f / maxv;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            int32_t q = nearest_int(__fmul_rn(iscale, v[i]));
-            q = q < 127 ? q : 127;
-            packed[i >> 2] |= (uint32_t)(uint8_t)(int8_t)q << (8 * (i & 3));
-            qsum += (int8_t)q;
+            int32_t qv = nearest_int(__fmul_rn(iscale, v[i]));
+            qv = qv < 127 ? qv : 127;
+            packed[i >> 2] |= (uint32_t)(uint8_t)(int8_t)qv << (8 * (i & 3));
+            qsum += (int8_t)qv;
         }
         d = 1.0f / iscale;
     }
     const int32_t next = __shfl_down(qsum, 1, 64);
-    if (valid) {
-        uint8_t *ob = out + blk * 292;
+    if (q.valid) {
+        uint8_t *ob = out + q.blk * 292;
         uint32_t *qs = reinterpret_cast<uint32_t *>(ob + 4 + 16 * li);
 #pragma unroll
         for (int i = 0; i < 4; ++i) qs[i] = packed[i];
@@ -188,6 +203,11 @@ __device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x
                 (uint32_t)(uint16_t)(int16_t)qsum | ((uint32_t)(uint16_t)(int16_t)next << 16);
         if (li == 0) *reinterpret_cast<uint32_t *>(ob) = __float_as_uint(d);
     }
+}
+
+__device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x, uint8_t *out, long long first,
+                                                     long long nblocks) {
+    quantize_store(quantize_load(x, first, nblocks), out);
 }
 
 // ------------------------------------------------------------ type traits
@@ -296,7 +316,61 @@ struct GridLDS {
 };
 
 // Fills the grid for TY into `lds` (cooperatively, all threads of the block);
-// the caller synchronises afterwards.
+// the caller synchronises afterwards.  grid_load / grid_store split it so the
+// table reads can be issued ahead of a kernel's weight loads (blocks of up to
+// 256 threads: four IQ2S entries or two IQ3S entries per thread).
+template <int TY>
+struct GridIn {
+    uint64_t e[TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 1];
+};
+
+template <int TY>
+__device__ __forceinline__ GridIn<TY> grid_load() {
+    GridIn<TY> g;
+    if constexpr (TY == T_IQ2_S) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            g.e[k] = threadIdx.x < 256 ? c_iq2s_grid[i] : 0;
+        }
+    } else if constexpr (TY == T_IQ3_S) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            g.e[k] = threadIdx.x < 256 ? c_iq3s_grid[i] : 0;
+        }
+    } else {
+        g.e[0] = 0;
+    }
+    return g;
+}
+
+template <int TY>
+__device__ __forceinline__ void grid_store(const GridIn<TY> &g, void *lds) {
+    if (threadIdx.x >= 256) return;
+    if constexpr (TY == T_IQ2_S) {
+        uint2 *out = reinterpret_cast<uint2 *>(lds);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint64_t v = g.e[k];
+            uint32_t c[2] = {0, 0};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t m = (uint32_t)(v >> (8 * e)) & 0xffu;
+                c[e >> 2] |= (m == 8 ? 0u : m == 25 ? 1u : 2u) << (8 * (e & 3));
+            }
+            out[threadIdx.x + 256 * k] = make_uint2(c[0], c[1]);
+        }
+    } else if constexpr (TY == T_IQ3_S) {
+        uint2 *out = reinterpret_cast<uint2 *>(lds);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t v = (uint32_t)g.e[k];
+            out[threadIdx.x + 256 * k] = make_uint2(v, neg_bytes(v));
+        }
+    }
+}
+
 template <int TY>
 __device__ __forceinline__ void fill_grid(void *lds) {
     if constexpr (TY == T_IQ2_S) {

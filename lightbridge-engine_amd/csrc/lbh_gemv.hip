@@ -31,7 +31,7 @@ __device__ __forceinline__ void store_y(const GemvArgs &p, int r, float v) {
         p.y[r] = v;
 }
 
-template <int TY, int LPU, bool FUSEQ>
+template <int TY, int LPU, bool FUSEQ, int D>
 __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
     constexpr int GB = GridLDS<TY>::BYTES > 0 ? GridLDS<TY>::BYTES : 16;
     __shared__ __align__(16) uint8_t s_grid[GB];
@@ -53,17 +53,33 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
         if (it < items && L.lane_on && r < rows) load_slice(P, (uint32_t)(r * NB + L.b), po, L.part, w);
     };
 
-    // The first weight loads go out before the codebook fill, the in-kernel
-    // quantization and the barrier, so their HBM latency overlaps that setup.
+    // Prologue loads first (codebook, this wave's first chunk of x), then the
+    // first step's weight loads, then the prologue's LDS stores and barrier:
+    // the small prologue loads do not wait behind the weight burst, and the
+    // weights' HBM latency overlaps the prologue.  The first weight load is
+    // unconditional (row clamped into the matrix; lanes without a row load a
+    // row another lane loads) so the wait before the stores counts exactly the
+    // weight loads issued after the prologue's; the other D - 1 steps go out
+    // after the barrier.
     int it = blockIdx.x * GEMV_WAVES + wid;
-    W wa, wb;
-    issue(it, wa);
+    const GridIn<TY> gin = grid_load<TY>();
+    QuantIn qin;
+    if constexpr (FUSEQ) qin = quantize_load(p.x, 4 * wid, NB);
+    W w[D];
+    {
+        int r = it * L.rpw + (L.lane_on ? L.slot : L.rpw - 1);
+        r = r < rows ? r : rows - 1;
+        load_slice(P, (uint32_t)(r * NB + L.b), po, L.part, w[0]);
+    }
 
-    fill_grid<TY>(s_grid);
+    grid_store<TY>(gin, s_grid);
     if constexpr (FUSEQ) {
-        for (int b0 = 4 * wid; b0 < NB; b0 += 4 * GEMV_WAVES) quantize_blocks_wave(p.x, s_q8, b0, NB);
+        quantize_store(qin, s_q8);
+        for (int b0 = 4 * wid + 4 * GEMV_WAVES; b0 < NB; b0 += 4 * GEMV_WAVES) quantize_blocks_wave(p.x, s_q8, b0, NB);
     }
     __syncthreads();
+#pragma unroll
+    for (int d = 1; d < D; ++d) issue(it + d * nw, w[d]);
     if (status_set(p.status)) return;
     if constexpr (FUSEQ) {
         if (p.q8_out && blockIdx.x == 0)
@@ -81,43 +97,53 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
         if (on && L.leader()) store_y(p, r, v);
     };
 
-    // Software pipeline, unrolled twice so the two register buffers alternate
-    // without copies: the loads of the wave's next rows are in flight while
-    // the current rows are computed.
+    // Software pipeline over a ring of D register buffers, unrolled D times so
+    // the buffers rotate without copies: the loads of the wave's next D - 1
+    // steps are in flight while the current step is computed, and the buffer
+    // just consumed is refilled with the step D ahead.
     while (it < items) {
-        issue(it + nw, wb);
-        process(it, wa);
-        it += nw;
-        if (it >= items) break;
-        issue(it + nw, wa);
-        process(it, wb);
-        it += nw;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (it >= items) break;
+            process(it, w[d]);
+            issue(it + D * nw, w[d]);
+            it += nw;
+        }
     }
 }
 
 static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
+template <int TY, int LPU, int D>
+static hipError_t launch_depth(const GemvArgs &a, int grid, hipStream_t s) {
+    if (a.x)
+        hipLaunchKernelGGL((k_gemv<TY, LPU, true, D>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_gemv<TY, LPU, false, D>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int TY, int LPU>
-static hipError_t launch_typed(const GemvArgs &a, int max_blocks, hipStream_t s) {
+static hipError_t launch_typed(const GemvArgs &a, int max_blocks, int depth, hipStream_t s) {
     const int rpw = (64 / LPU) / a.m.nb;
     const int items = cdiv(a.m.rows, rpw);
     int grid = cdiv(items, GEMV_WAVES);
     if (max_blocks > 0 && grid > max_blocks) grid = max_blocks;
-    if (a.x)
-        hipLaunchKernelGGL((k_gemv<TY, LPU, true>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
-    else
-        hipLaunchKernelGGL((k_gemv<TY, LPU, false>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
-    return hipGetLastError();
+    switch (depth) {
+    case 4: return launch_depth<TY, LPU, 4>(a, grid, s);
+    case 3: return launch_depth<TY, LPU, 3>(a, grid, s);
+    default: return launch_depth<TY, LPU, 2>(a, grid, s);
+    }
 }
 
 template <int TY>
-static hipError_t launch_lpu(const GemvArgs &a, int lpu, int max_blocks, hipStream_t s) {
+static hipError_t launch_lpu(const GemvArgs &a, int lpu, int max_blocks, int depth, hipStream_t s) {
     // A wave step must hold at least one whole row: NB * LPU <= 64.
     while (lpu > 1 && a.m.nb * lpu > 64) lpu >>= 1;
     switch (lpu) {
-    case 4: return launch_typed<TY, 4>(a, max_blocks, s);
-    case 2: return launch_typed<TY, 2>(a, max_blocks, s);
-    default: return launch_typed<TY, 1>(a, max_blocks, s);
+    case 4: return launch_typed<TY, 4>(a, max_blocks, depth, s);
+    case 2: return launch_typed<TY, 2>(a, max_blocks, depth, s);
+    default: return launch_typed<TY, 1>(a, max_blocks, depth, s);
     }
 }
 
@@ -137,11 +163,12 @@ hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
     if (nb < 1 || nb > MAX_NB || a.m.rows < 1) return hipErrorInvalidValue;
     if (!a.q8 && !a.x) return hipErrorInvalidValue;
     const int lpu = t.lpu > 0 ? t.lpu : default_lpu(a.m.type);
+    const int depth = t.depth > 0 ? t.depth : 2;
     switch (a.m.type) {
-    case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, lpu, t.max_blocks, s);
-    case T_IQ3_S: return launch_lpu<T_IQ3_S>(a, lpu, t.max_blocks, s);
-    case T_Q4_K: return launch_lpu<T_Q4_K>(a, lpu, t.max_blocks, s);
-    case T_Q5_K: return launch_lpu<T_Q5_K>(a, lpu, t.max_blocks, s);
+    case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, lpu, t.max_blocks, depth, s);
+    case T_IQ3_S: return launch_lpu<T_IQ3_S>(a, lpu, t.max_blocks, depth, s);
+    case T_Q4_K: return launch_lpu<T_Q4_K>(a, lpu, t.max_blocks, depth, s);
+    case T_Q5_K: return launch_lpu<T_Q5_K>(a, lpu, t.max_blocks, depth, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -44,6 +44,7 @@ struct GemvArgs {
 struct GemvTuning {
     int lpu;          // lanes per (row, block) unit: 1, 2 or 4
     int max_blocks;   // cap on workgroups of the persistent row loop
+    int depth;        // row steps in flight per wave (2..4)
 };
 
 // ---------------------------------------------------------------- MoE block

@@ -75,12 +75,32 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
         load_slice(PG, u, po, L.part, wg);
         load_slice(PU, u, po, L.part, wu);
     };
+    // Prologue loads (codebook, this wave's first chunk of x) go out before
+    // the first weight loads, so they do not wait behind the weight burst.
+    // The first weight load is unconditional (item and row clamped into
+    // range) so the wait before the prologue's stores counts exactly the
+    // weight loads issued after it.
     int it = first_wave + wid;
+    const GridIn<TY> gin = grid_load<TY>();
+    const QuantIn qin = quantize_load(a.x, 4 * wid, NB);
     W ga, ua, gb, ub;
-    issue(it, ga, ua);
+    {
+        const int itc = it < items ? it : items - 1;
+        const int m = itc / per, j = itc - m * per;
+        int r = j * L.rpw + (L.lane_on ? L.slot : L.rpw - 1);
+        r = r < rows ? r : rows - 1;
+        const ExpertDev &E = slot_of(m);
+        const Planes PG = make_planes(E.gate.planes, E.gate.units, E.gate.bytes);
+        const Planes PU = make_planes(E.up.planes, E.up.units, E.up.bytes);
+        const uint32_t po = part_offset<TY, LPU>(PG, L.part);
+        const uint32_t u = (uint32_t)(r * NB + L.b);
+        load_slice(PG, u, po, L.part, ga);
+        load_slice(PU, u, po, L.part, ua);
+    }
 
-    fill_grid<TY>(s_grid);
-    for (int b0 = 4 * wid; b0 < NB; b0 += 4 * MOE_WAVES) quantize_blocks_wave(a.x, s_q8, b0, NB);
+    grid_store<TY>(gin, s_grid);
+    quantize_store(qin, s_q8);
+    for (int b0 = 4 * wid + 4 * MOE_WAVES; b0 < NB; b0 += 4 * MOE_WAVES) quantize_blocks_wave(a.x, s_q8, b0, NB);
     __syncthreads();
     ActOf<TY, LPU> act;
     load_act(s_q8 + L.b * 292, L.part, act);

@@ -173,7 +173,7 @@ class HipBackend:
         self._stream = stream
         lib().lbh_ctx_set_stream(self.ctx, C.c_void_p(stream.cuda_stream))
 
-    TUNE_GEMV_LPU, TUNE_GEMV_MAX_BLOCKS, TUNE_GEMM_SHAPE = 1, 2, 3
+    TUNE_GEMV_LPU, TUNE_GEMV_MAX_BLOCKS, TUNE_GEMM_SHAPE, TUNE_GEMV_DEPTH = 1, 2, 3, 4
 
     def set_tuning(self, key: int, value: int) -> None:
         """Launch-shape knob (lanes per unit, workgroup cap); 0 restores the default."""
