@@ -580,12 +580,14 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
         m->shared.up = view_of(shared_up);
         m->shared.down = view_of(shared_down);
     }
-    // Gate/up workgroups: two per CU, split in proportion to the bytes of the
-    // top-8 routed experts and of the shared expert.
+    // Gate/up workgroups: three per CU, split in proportion to the decode
+    // work of the top-8 routed experts and of the shared expert (per byte an
+    // IQ stream issues about three times the VALU work of a K-quant one).
     {
-        const double br = 8.0 * 2.0 * (double)gate[0]->bytes;
-        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes : 0.0;
-        const int total = 2 * ctx->cu_count;
+        auto cost = [](int ty) { return ty == LBH_IQ2_S || ty == LBH_IQ3_S ? 3.0 : 1.0; };
+        const double br = 8.0 * 2.0 * (double)gate[0]->bytes * cost(tg);
+        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes * cost(shared_gate->type) : 0.0;
+        const int total = 3 * ctx->cu_count;
         m->wg_s = has_shared ? (int)(total * bs / (br + bs) + 0.5) : 0;
         if (has_shared && m->wg_s < 1) m->wg_s = 1;
         m->wg_r = total - m->wg_s > 1 ? total - m->wg_s : 1;

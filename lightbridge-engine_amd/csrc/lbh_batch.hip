@@ -109,9 +109,9 @@ __device__ __forceinline__ void decode(const WSlice<T_IQ2_S, LPU> &w, const void
         for (int lg = 0; lg < 4; ++lg) {
             const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
             const uint2 code = grid[idx];
-            const uint32_t s = byte_of(w.sg[g], lg);
-            const uint32_t sel_lo = (((s & 15u) * 0x810204u) & 0x04040404u) | code.x;
-            const uint32_t sel_hi = (((s >> 4) * 0x810204u) & 0x04040404u) | code.y;
+            const uint2 sm = grid[1024 + byte_of(w.sg[g], lg)];
+            const uint32_t sel_lo = sm.x | code.x;
+            const uint32_t sel_hi = sm.y | code.y;
             o.w[8 * g + 2 * lg] = perm(IQ2S_NEG, IQ2S_POS, sel_lo);
             o.w[8 * g + 2 * lg + 1] = perm(IQ2S_NEG, IQ2S_POS, sel_hi);
         }

@@ -312,8 +312,17 @@ static __constant__ uint32_t c_iq3s_grid[512] = {LBH_IQ3S_GRID_VALUES};
 
 template <int TY>
 struct GridLDS {
-    static constexpr int BYTES = TY == T_IQ2_S ? 1024 * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
+    // IQ2S: the 1024 code entries, then 256 sign-byte entries (sign_lut_entry).
+    static constexpr int BYTES = TY == T_IQ2_S ? (1024 + 256) * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
 };
+
+// Sign-byte table appended to the IQ2S codes: entry s = the v_perm selector
+// bits (4 in byte i when bit i is set) of the low and the high nibble of s,
+// so applying eight sign bits is one LDS read and two ORs.  Computed, not
+// loaded: nib * 0x810204 moves bit i to bit 8i + 2 with no carries.
+__device__ __forceinline__ uint2 sign_lut_entry(uint32_t s) {
+    return make_uint2(((s & 15u) * 0x810204u) & 0x04040404u, ((s >> 4) * 0x810204u) & 0x04040404u);
+}
 
 // Fills the grid for TY into `lds` (cooperatively, all threads of the block);
 // the caller synchronises afterwards.  grid_load / grid_store split it so the
@@ -361,6 +370,7 @@ __device__ __forceinline__ void grid_store(const GridIn<TY> &g, void *lds) {
             }
             out[threadIdx.x + 256 * k] = make_uint2(c[0], c[1]);
         }
+        out[1024 + threadIdx.x] = sign_lut_entry(threadIdx.x);
     } else if constexpr (TY == T_IQ3_S) {
         uint2 *out = reinterpret_cast<uint2 *>(lds);
 #pragma unroll
@@ -385,6 +395,7 @@ __device__ __forceinline__ void fill_grid(void *lds) {
             }
             g[i] = make_uint2(c[0], c[1]);
         }
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) g[1024 + i] = sign_lut_entry(i);
     } else if constexpr (TY == T_IQ3_S) {
         uint2 *g = reinterpret_cast<uint2 *>(lds);
         for (int i = threadIdx.x; i < 512; i += blockDim.x) {
@@ -479,12 +490,11 @@ __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, cons
         for (int lg = 0; lg < 4; ++lg) {
             const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
             const uint2 code = grid[idx];
-            const uint32_t s = byte_of(w.sg[g], lg);
-            // bit i of a sign nibble -> bit 8i+2 (value 4: the negated
-            // source).  The nibble must be isolated first: with all eight
-            // bits, bit 7 and bit 0 would collide at bit 9 and carry.
-            const uint32_t sel_lo = (((s & 15u) * 0x810204u) & 0x04040404u) | code.x;
-            const uint32_t sel_hi = (((s >> 4) * 0x810204u) & 0x04040404u) | code.y;
+            // selector bits of the eight sign bits: byte i takes the negated
+            // source (selector 4 + code) when sign bit i is set
+            const uint2 sm = grid[1024 + byte_of(w.sg[g], lg)];
+            const uint32_t sel_lo = sm.x | code.x;
+            const uint32_t sel_hi = sm.y | code.y;
             part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
             part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
         }
