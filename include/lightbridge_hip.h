@@ -104,8 +104,9 @@ lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream);
 enum lbh_tuning_key {
     LBH_TUNE_GEMV_LPU = 1,         /* lanes per (row, block) unit: 1, 2 or 4 */
     LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop */
-    LBH_TUNE_GEMM_SHAPE = 3,
-    LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 2, 3 or 4 */       /* K-quant GEMM workgroup: 0 = 2x4, 1 = 2x2, 2 = 4x2, 3 = 1x4 waves (rows x tokens) */
+    LBH_TUNE_GEMM_SHAPE = 3,       /* K-quant GEMM tile staging: 0 = through registers, two blocks ahead;
+                                      1 = direct buffer-to-LDS loads, one block ahead */
+    LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 2, 3 or 4 */
 };
 lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value);
 /* Compute units of the context's device. */
@@ -177,17 +178,18 @@ lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x_dev, u
  * of q8_k.rs:295-312, :337-364, :380-428.  out_dev holds rows * (k/256) * {1|9} int32. */
 lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, int32_t *out_dev);
 
-/* ---- token batches on the i8 matrix cores (prefill) -------------------------------
+/* ---- token batches on the matrix cores (prefill) ----------------------------------
  * The reference has no batched path ("grouped prefill unavailable", docs/STATUS.md:29):
  * it evaluates vec_dot_q8_k (q8_k.rs:80-89) row by row for one token at a time.
  * These entry points compute y[t][r] = vec_dot_q8_k(row r, token t) for a batch of
- * tokens with v_mfma_i32_32x32x32_i8, bit-identical to the per-row dot for Q4_K and
- * Q5_K (dot_q4_or_q5_k, q8_k.rs:247-327): the sub-block scales are folded into the
- * weights of an MFMA-ready copy of the matrix, every (block, lane residue) has its
- * own exact int32 sum, and the nine f32 chains per block run in the reference order. */
+ * tokens with v_mfma_f32_32x32x16_f16 on integer operands, bit-identical to the per-row
+ * dot for Q4_K and Q5_K (dot_q4_or_q5_k, q8_k.rs:247-327): the sub-block scales are
+ * folded into the weights of an MFMA-ready copy of the matrix (integers <= 1953, exact
+ * in f16), every (block, lane residue) sum is an exact integer below 2^24, and the
+ * nine f32 chains per block run in the reference order. */
 
-/* [sync] Builds the matrix's MFMA-ready copy (Q4_K / Q5_K only; about 3.3x the packed
- * bytes, allocated once and freed with the matrix). */
+/* [sync] Builds the matrix's MFMA-ready copy (Q4_K / Q5_K only; 3.8x (Q4_K) or 3.1x
+ * (Q5_K) the packed bytes, allocated once and freed with the matrix). */
 lbh_status lbh_matrix_prepare_gemm(lbh_ctx *ctx, lbh_matrix *m, lbh_error *err);
 
 /* Device workspace bytes of lbh_gemm_q8_k for n_tokens tokens of k elements (0 if k % 256). */

@@ -24,7 +24,7 @@ struct lbh_ctx {
     DevStatus *status;        // device
     DevStatus *status_host;   // pinned mirror
     GemvTuning tuning;
-    int gemm_shape;           // workgroup shape of the K-quant GEMM (0: 2 x 4 waves)
+    int gemm_shape;           // K-quant GEMM staging (0: registers, two blocks ahead; 1: direct to LDS)
 };
 
 struct lbh_matrix {
@@ -34,7 +34,6 @@ struct lbh_matrix {
     uint8_t *planes;
     size_t bytes;
     uint8_t *gemm_a;     // MFMA-ready copy for token batches (lbh_matrix_prepare_gemm), or NULL
-    float2 *gemm_dm;
 };
 
 namespace {
@@ -200,7 +199,7 @@ lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
         ctx->tuning.depth = value;
         return LBH_OK;
     case LBH_TUNE_GEMM_SHAPE:
-        if (value < 0 || value > 3) return LBH_INVALID_PARAMETER;
+        if (value < 0 || value > 1) return LBH_INVALID_PARAMETER;
         ctx->gemm_shape = value;
         return LBH_OK;
     default: return LBH_INVALID_PARAMETER;
@@ -319,7 +318,6 @@ lbh_status lbh_matrix_destroy(lbh_matrix *m) {
     DeviceGuard g(m->device);
     (void)hipFree(m->planes);  // hipFree waits for work that may still read the planes
     if (m->gemm_a) (void)hipFree(m->gemm_a);
-    if (m->gemm_dm) (void)hipFree(m->gemm_dm);
     delete m;
     return LBH_OK;
 }
@@ -482,7 +480,7 @@ struct lbh_moe {
     int32_t *plan_host;       // pinned
     int tc, rt_gu_r, rt_gu_s, rt_d_r, rt_d_s;
     uint8_t *shared_gemm_mem; // MFMA-ready copies of a K-quant shared expert (batched calls)
-    size_t gemm_off[6];       // (A, d/dmin) offsets of gate, up, down in shared_gemm_mem
+    size_t gemm_off[3];       // A offsets of gate, up, down in shared_gemm_mem
 };
 
 namespace {
@@ -766,7 +764,6 @@ namespace {
 MatGemm gemm_view(const lbh_matrix *m, float *y, int ldy) {
     MatGemm g;
     g.a = m->gemm_a;
-    g.dm = m->gemm_dm;
     g.y = y;
     g.rows = (int32_t)m->rows;
     g.ldy = ldy;
@@ -777,14 +774,11 @@ hipError_t prepare_gemm(lbh_matrix *m, hipStream_t s) {
     if (m->gemm_a) return hipSuccess;
     const int rows = (int)m->rows, nb = (int)m->nb;
     hipError_t e = hipMalloc(&m->gemm_a, gemm_a_bytes(rows, nb));
-    if (e == hipSuccess) e = hipMalloc(&m->gemm_dm, gemm_dm_bytes(rows, nb));
-    if (e == hipSuccess) e = launch_prep_a(view_of(m), m->gemm_a, m->gemm_dm, s);
+    if (e == hipSuccess) e = launch_prep_a(view_of(m), m->gemm_a, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         if (m->gemm_a) (void)hipFree(m->gemm_a);
-        if (m->gemm_dm) (void)hipFree(m->gemm_dm);
         m->gemm_a = nullptr;
-        m->gemm_dm = nullptr;
     }
     return e;
 }
@@ -818,15 +812,13 @@ lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, s
     DeviceGuard g(ctx->device);
     GemmArgs a{};
     uint8_t *bt = static_cast<uint8_t *>(workspace);
-    const size_t tiles = (n_tokens + 31) / 32;
     a.b = bt;
-    a.d8 = reinterpret_cast<const float *>(bt + tiles * nb * 9216);
     a.nb = nb;
     a.n_tokens = (int32_t)n_tokens;
     a.n_mat = 1;
     a.shape = ctx->gemm_shape;
     a.mat[0] = gemm_view(m, y, (int)m->rows);
-    if (launch_prep_b(q8, (int)n_tokens, nb, bt, const_cast<float *>(a.d8), ctx->stream) != hipSuccess)
+    if (launch_prep_b(q8, (int)n_tokens, nb, bt, ctx->stream) != hipSuccess)
         return LBH_HIP_ERROR;
     return launch_kq_gemm(a, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
@@ -949,23 +941,17 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
         a.g_s = reinterpret_cast<float *>(b + o_gs);
         a.u_s = reinterpret_cast<float *>(b + o_us);
         a.bx = b + o_bx;
-        a.d8x = reinterpret_cast<float *>(b + o_bx + (T + 31) / 32 * nbh * 9216);
         a.bh = b + o_bh;
-        a.d8h = reinterpret_cast<float *>(b + o_bh + (T + 31) / 32 * nbs * 9216);
         if (!m->shared_gemm_mem) {
             // MFMA-ready copies of the shared gate, up and down (built once).
             const MatView v[3] = {m->shared.gate, m->shared.up, m->shared.down};
-            size_t so = 0, oa[3], od[3];
+            size_t so = 0, oa[3];
             for (int i = 0; i < 3; ++i) {
                 oa[i] = so;
                 so += (gemm_a_bytes(v[i].rows, v[i].nb) + 255) & ~(size_t)255;
-                od[i] = so;
-                so += (gemm_dm_bytes(v[i].rows, v[i].nb) + 255) & ~(size_t)255;
             }
             e = hipMalloc(&m->shared_gemm_mem, so);
-            for (int i = 0; i < 3 && e == hipSuccess; ++i)
-                e = launch_prep_a(v[i], m->shared_gemm_mem + oa[i], reinterpret_cast<float2 *>(m->shared_gemm_mem + od[i]),
-                                  nullptr);
+            for (int i = 0; i < 3 && e == hipSuccess; ++i) e = launch_prep_a(v[i], m->shared_gemm_mem + oa[i], nullptr);
             if (e == hipSuccess) e = hipDeviceSynchronize();
             if (e != hipSuccess) {
                 if (m->shared_gemm_mem) (void)hipFree(m->shared_gemm_mem);
@@ -975,14 +961,13 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
                 m->cap_tokens = m->cap_k = 0;
                 return hip_fail(err, e);
             }
-            m->gemm_off[0] = oa[0], m->gemm_off[1] = od[0], m->gemm_off[2] = oa[1];
-            m->gemm_off[3] = od[1], m->gemm_off[4] = oa[2], m->gemm_off[5] = od[2];
+            m->gemm_off[0] = oa[0], m->gemm_off[1] = oa[1], m->gemm_off[2] = oa[2];
         }
         uint8_t *g = m->shared_gemm_mem;
         const int ffs = (int)ffn_s, hid = (int)m->hidden;
-        a.sg = MatGemm{g + m->gemm_off[0], reinterpret_cast<const float2 *>(g + m->gemm_off[1]), a.g_s, ffs, ffs};
-        a.su = MatGemm{g + m->gemm_off[2], reinterpret_cast<const float2 *>(g + m->gemm_off[3]), a.u_s, ffs, ffs};
-        a.sd = MatGemm{g + m->gemm_off[4], reinterpret_cast<const float2 *>(g + m->gemm_off[5]), a.d_s, hid, hid};
+        a.sg = MatGemm{g + m->gemm_off[0], a.g_s, ffs, ffs};
+        a.su = MatGemm{g + m->gemm_off[1], a.u_s, ffs, ffs};
+        a.sd = MatGemm{g + m->gemm_off[2], a.d_s, hid, hid};
     }
     m->cap_tokens = max_tokens;
     m->cap_k = top_k;

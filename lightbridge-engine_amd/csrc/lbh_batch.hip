@@ -785,14 +785,13 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
         // shared gate/up on the matrix cores, beside nothing: they only need Q8_K(x)
         GemmArgs gm{};
         gm.b = a.bx;
-        gm.d8 = a.d8x;
         gm.nb = nbh;
         gm.n_tokens = a.n_tokens;
         gm.shape = a.gemm_shape;
         gm.n_mat = 2;
         gm.mat[0] = a.sg;
         gm.mat[1] = a.su;
-        if ((e = launch_prep_b(a.q8x, a.n_tokens, nbh, a.bx, a.d8x, s)) != hipSuccess) return e;
+        if ((e = launch_prep_b(a.q8x, a.n_tokens, nbh, a.bx, s)) != hipSuccess) return e;
         if ((e = launch_kq_gemm(gm, s)) != hipSuccess) return e;
     } else if (a.has_shared && (e = gate_up_any<true>(tsg, a, lds[2], s)) != hipSuccess) {
         return e;
@@ -810,13 +809,12 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
         const int nbs = a.ffn_s / 256;
         GemmArgs gm{};
         gm.b = a.bh;
-        gm.d8 = a.d8h;
         gm.nb = nbs;
         gm.n_tokens = a.n_tokens;
         gm.shape = a.gemm_shape;
         gm.n_mat = 1;
         gm.mat[0] = a.sd;
-        if ((e = launch_prep_b(a.q8h_s, a.n_tokens, nbs, a.bh, a.d8h, s)) != hipSuccess) return e;
+        if ((e = launch_prep_b(a.q8h_s, a.n_tokens, nbs, a.bh, s)) != hipSuccess) return e;
         if ((e = launch_kq_gemm(gm, s)) != hipSuccess) return e;
     } else if (a.has_shared && (e = down_any<true>(tsd, a, lds[4], s)) != hipSuccess) {
         return e;

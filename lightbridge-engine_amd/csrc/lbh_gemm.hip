@@ -1,5 +1,5 @@
-// lbh_gemm.hip — Q4_K / Q5_K x Q8_K for a batch of tokens on the i8 matrix
-// cores (v_mfma_i32_32x32x32_i8), bit-identical to the reference's per-row
+// lbh_gemm.hip — Q4_K / Q5_K x Q8_K for a batch of tokens on the f16 matrix
+// cores (v_mfma_f32_32x32x16_f16), bit-identical to the reference's per-row
 // dot (dot_q4_or_q5_k, crates/bridge-quant-layout/src/q8_k.rs:247-327) for
 // every (row, token):
 //
@@ -8,32 +8,45 @@
 //   per block:  sums[l] += (d * d8) * lane_sums[l];  sum -= (dmin * d8) * minimum_sum
 //   result = sum + sums[0] + ... + sums[7]
 //
-// The integer stage runs on MFMA; the f32 chains run on the VALU in the
-// reference's block order.  Exactness: every lane sum has its own MFMA
-// (K = the 32 elements of residue l), the sub-block scale is folded into the
-// weight (w = sc * q <= 63 * 31, split w = 64 * hi + lo into two int8 rows of
-// the A operand, interleaved so one lane holds both), and the minimum sum is a
-// ninth MFMA on the 6-bit mins and the pair sums of bsums split as
-// 128 * bh + bl.  All integer sums are exact in int32.
+// The integer stage runs on the matrix cores, the f32 chains on the VALU in
+// the reference's block order.  Exactness: the A operand holds the weight
+// pre-scaled by its sub-block scale, w = sc * q <= 63 * 31 = 1953, and the B
+// operand the Q8_K byte, both integers an f16 holds exactly; every product
+// and every partial sum of one lane sum is an integer below 2^24
+// (32 * 1953 * 128 < 2^23), so the f32 accumulation inside the instruction
+// is exact in any order and the result equals lane_sums[l] converted to f32
+// (which the reference's `as f32` also does exactly).  Each lane sum (the 32
+// elements of residue l) is two K = 16 instructions, the second accumulating
+// onto the first.  The minimum sum is a 17th instruction on the 6-bit mins
+// against the pair sums of bsums split as 128 * bh + bl: A holds
+// (128 mn_j, mn_j), B holds (bh_j, bl_j), |partial sums| < 8 * 63 * 8128.
 //
 // Layouts (built once per matrix by k_prep_a, per call by k_prep_b):
-//   A tile (16 rows, block b): 9 MFMA operands x 64 lanes x 16 B; lane j
-//     feeds A row m = j % 32 (real row m / 2, hi when m is even, lo when odd)
-//     with the 16 K-bytes of half j / 32: sub-blocks 4 (j / 32) + q / 4,
-//     k = q % 4 (q = byte).  Operand 8 is the minimum MFMA.
-//   B tile (32 tokens, block b): the same shape; lane j feeds token j % 32.
-//   A and B use the same byte <-> k convention, so the contraction pairs
-//   identical elements whatever the instruction's internal k order.
+//   A tile (32 rows, block b): 17 operands x 64 lanes x 16 B, then the 32
+//     rows' (d, dmin) as f32 pairs.  Operand 2l + p, lane j: row j % 32, the
+//     8 f16 of sub-blocks 4p + 2 (j / 32) + e / 4, element 8 (e % 4) + l.
+//     Operand 16, lane j: sub-blocks 4 (j / 32) + e / 2, (128 mn, mn).
+//   B tile (32 tokens, block b): the same operands for token j % 32 (Q8_K
+//     bytes; operand 16 = (bh, bl)), then the 32 tokens' d8.
+//   A and B use the same slot <-> element convention, so the contraction
+//   pairs identical elements whatever the instruction's internal k order.
 #include "lbh_internal.h"
 #include "lbh_rows.h"
 
 namespace lbh {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
-constexpr int OPS = 9;                 // MFMA operands per (tile, block): 8 residues + minimum
-constexpr int TILE_BYTES = OPS * 1024; // 64 lanes x 16 B per operand
+constexpr int OPS = 17;                          // 8 residues x 2 halves + the minimum
+constexpr int OP_BYTES = 1024;                   // 64 lanes x 8 f16
+constexpr int A_TILE = OPS * OP_BYTES + 32 * 8;  // + (d, dmin) of the tile's rows
+constexpr int B_TILE = OPS * OP_BYTES + 32 * 4;  // + d8 of the tile's tokens
+constexpr int PIECES = OPS + 1;                  // 1 KiB staging units per tile (the last one partial)
+
+__device__ __forceinline__ uint32_t pack_f16(_Float16 lo, _Float16 hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
 
 // ------------------------------------------------------------ A preparation
 //
@@ -41,24 +54,21 @@ constexpr int TILE_BYTES = OPS * 1024; // 64 lanes x 16 B per operand
 // device layout (lbh_layout.h): Q4_K chunk 0 header, chunks 1-8 residue-major
 // qs; Q5_K chunk 0 header, 1-2 residue-major qh, 3-10 residue-major qs.
 template <int TY>
-__global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out, float2 *dm_out) {
+__global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out) {
     const int lane = threadIdx.x;
     const int nb = m.nb;
     const int tile = blockIdx.x / nb, b = blockIdx.x - tile * nb;
-    const int mrow = lane & 31, hl = mrow & 1, h = lane >> 5;
-    const int row = tile * 16 + (mrow >> 1);
+    const int h = lane >> 5;
+    const int row = tile * 32 + (lane & 31);
     const bool valid = row < m.rows;
     const long long U = m.units, u = (long long)row * nb + b;
     constexpr int QS0 = TY == T_Q5_K ? 3 : 1;
-    uint8_t blk[176];
-    if (valid) {
-        const int nch = TY == T_Q5_K ? 11 : 9;
-        for (int c = 0; c < nch; ++c) {
-            const uint4 v = *reinterpret_cast<const uint4 *>(m.planes + ((long long)c * U + u) * 16);
-            *reinterpret_cast<uint4 *>(blk + 16 * c) = v;
-        }
-    } else {
-        for (int i = 0; i < 176; ++i) blk[i] = 0;
+    constexpr int NCH = TY == T_Q5_K ? 11 : 9;
+    uint8_t blk[NCH * 16];
+    for (int c = 0; c < NCH; ++c) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (valid) v = *reinterpret_cast<const uint4 *>(m.planes + ((long long)c * U + u) * 16);
+        *reinterpret_cast<uint4 *>(blk + 16 * c) = v;
     }
     int sc[8], mn[8];
     {
@@ -67,308 +77,416 @@ __global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out, float2
         const uint32_t s2 = *reinterpret_cast<const uint32_t *>(blk + 12);
         for (int j = 0; j < 8; ++j) scale_min_of(s0, s1, s2, j, sc[j], mn[j]);
     }
-    uint8_t *dst = a_out + ((long long)tile * nb + b) * TILE_BYTES + lane * 16;
+    uint8_t *tile_base = a_out + ((long long)tile * nb + b) * A_TILE;
+    uint8_t *dst = tile_base + lane * 16;
     for (int l = 0; l < 8; ++l) {
-        uint8_t o[16];
-        for (int q = 0; q < 16; ++q) {
-            const int jj = 4 * h + q / 4, kk = q % 4;
-            const int g = jj >> 1;
-            // residue-major: dword l of group g holds elements l + 8k of the group's 32 bytes
-            const int pos = 4 * l + kk;
-            const uint8_t qb = blk[16 * (QS0 + 2 * g) + pos];
-            int v = (jj & 1) ? (qb >> 4) : (qb & 15);
-            if (TY == T_Q5_K) {
-                const uint8_t hb = blk[16 + pos];
-                v += ((hb >> jj) & 1) * 16;
+        for (int p = 0; p < 2; ++p) {
+            uint32_t o[4];
+            for (int e = 0; e < 8; e += 2) {
+                int w[2];
+                for (int f = 0; f < 2; ++f) {
+                    const int jj = 4 * p + 2 * h + ((e + f) >> 2), k = (e + f) & 3;
+                    // residue-major: dword l of qs group jj / 2 holds elements l + 8k
+                    const int pos = 4 * l + k;
+                    const uint8_t qb = blk[16 * (QS0 + 2 * (jj >> 1)) + pos];
+                    int v = (jj & 1) ? (qb >> 4) : (qb & 15);
+                    if (TY == T_Q5_K) v += ((blk[16 + pos] >> jj) & 1) << 4;
+                    w[f] = sc[jj] * v;
+                }
+                o[e >> 1] = pack_f16((_Float16)w[0], (_Float16)w[1]);
             }
-            const int w = sc[jj] * v;
-            o[q] = (uint8_t)(hl ? (w & 63) : (w >> 6));
+            *reinterpret_cast<uint4 *>(dst + (2 * l + p) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        for (int q = 0; q < 16; ++q) dst[l * 1024 + q] = o[q];
     }
     {
-        uint8_t o[16];
-        for (int q = 0; q < 16; ++q) {
-            int v = 0;
-            if (h == 0) v = q < 8 ? (hl == 0 ? mn[q] : 0) : (hl == 1 ? mn[q - 8] : 0);
-            o[q] = (uint8_t)v;
+        uint32_t o[4];
+        for (int e = 0; e < 8; e += 2) {
+            const int jj = 4 * h + (e >> 1);
+            o[e >> 1] = pack_f16((_Float16)(128 * mn[jj]), (_Float16)mn[jj]);
         }
-        for (int q = 0; q < 16; ++q) dst[8 * 1024 + q] = o[q];
+        *reinterpret_cast<uint4 *>(dst + 16 * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    if (lane < 16) {
-        const int r = tile * 16 + lane;
+    if (lane < 32) {
         float2 v = make_float2(0.0f, 0.0f);
-        if (r < m.rows) {
-            const uint32_t hdr = *reinterpret_cast<const uint32_t *>(m.planes + ((long long)r * nb + b) * 16);
+        if (valid) {
+            const uint32_t hdr = *reinterpret_cast<const uint32_t *>(blk);
             v = make_float2(f16_to_f32(hdr & 0xffffu), f16_to_f32(hdr >> 16));
         }
-        dm_out[(long long)r * nb + b] = v;
+        reinterpret_cast<float2 *>(tile_base + OPS * OP_BYTES)[lane] = v;
     }
 }
 
 // ------------------------------------------------------------ B preparation
 //
 // One wave per (token tile, block) from GGML Q8_K bytes (d @0, qs @4,
-// bsums @260; block (t, b) at q8 + (t * nb + b) * 292).
-__global__ void __launch_bounds__(64) k_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b_out, float *d8_out) {
+// bsums @260; block (t, b) at q8 + (t * nb + b) * 292).  Lane j needs the
+// four sub-blocks 2 (j / 32) + {0, 1, 4, 5} of token j % 32.
+__global__ void __launch_bounds__(64) k_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b_out) {
     const int lane = threadIdx.x;
     const int tile = blockIdx.x / nb, b = blockIdx.x - tile * nb;
-    const int n = lane & 31, h = lane >> 5;
-    const int t = tile * 32 + n;
+    const int h = lane >> 5;
+    const int t = tile * 32 + (lane & 31);
     const bool valid = t < n_tokens;
     const uint8_t *blk = q8 + ((long long)(valid ? t : 0) * nb + b) * 292;
-    uint8_t *dst = b_out + ((long long)tile * nb + b) * TILE_BYTES + lane * 16;
-    for (int l = 0; l < 8; ++l) {
-        uint32_t w[4];
+    uint8_t *tile_base = b_out + ((long long)tile * nb + b) * B_TILE;
+    uint8_t *dst = tile_base + lane * 16;
+    // qs of sub-blocks 2h, 2h + 1 (p = 0) and 4 + 2h, 5 + 2h (p = 1): 64 bytes each
+    uint32_t q[2][16];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
         for (int i = 0; i < 4; ++i) {
-            uint32_t v = 0;
-            for (int kk = 0; kk < 4; ++kk) {
-                const int jj = 4 * h + i;
-                const uint32_t byte = valid ? blk[4 + 32 * jj + 8 * kk + l] : 0u;
-                v |= byte << (8 * kk);
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (valid) v = *reinterpret_cast<const uint4 *>(blk + 4 + 32 * (4 * p + 2 * h) + 16 * i);
+            q[p][4 * i] = v.x, q[p][4 * i + 1] = v.y, q[p][4 * i + 2] = v.z, q[p][4 * i + 3] = v.w;
+        }
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                _Float16 x[2];
+#pragma unroll
+                for (int f = 0; f < 2; ++f) {
+                    // element 8k + l of sub-block 4p + 2h + (e + f) / 4: byte 32 * ((e + f) / 4) + 8k + l
+                    const int k = (e + f) & 3, byte = 32 * ((e + f) >> 2) + 8 * k + l;
+                    x[f] = (_Float16)(int)(int8_t)(q[p][byte >> 2] >> (8 * (byte & 3)));
+                }
+                o[e >> 1] = pack_f16(x[0], x[1]);
             }
-            w[i] = v;
+            *reinterpret_cast<uint4 *>(dst + (2 * l + p) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        *reinterpret_cast<uint4 *>(dst + l * 1024) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    uint8_t o[16];
-    for (int q = 0; q < 16; ++q) {
-        int v = 0;
-        if (valid && h == 0) {
-            const int j = q & 7;
-            const int bsp = (int)*reinterpret_cast<const int16_t *>(blk + 260 + 4 * j) +
-                            (int)*reinterpret_cast<const int16_t *>(blk + 262 + 4 * j);
-            v = q < 8 ? (bsp >> 7) : (bsp & 127);
+    {
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const int jj = 4 * h + (e >> 1);
+            int bsp = 0;
+            if (valid)
+                bsp = (int)*reinterpret_cast<const int16_t *>(blk + 260 + 4 * jj) +
+                      (int)*reinterpret_cast<const int16_t *>(blk + 262 + 4 * jj);
+            o[e >> 1] = pack_f16((_Float16)(bsp >> 7), (_Float16)(bsp & 127));
         }
-        o[q] = (uint8_t)(int8_t)v;
+        *reinterpret_cast<uint4 *>(dst + 16 * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
     }
-    for (int q = 0; q < 16; ++q) dst[8 * 1024 + q] = o[q];
-    if (lane < 32) d8_out[((long long)tile * nb + b) * 32 + lane] = valid ? *reinterpret_cast<const float *>(blk) : 0.0f;
+    if (lane < 32)
+        reinterpret_cast<float *>(tile_base + OPS * OP_BYTES)[lane] = valid ? *reinterpret_cast<const float *>(blk) : 0.0f;
 }
 
 // ------------------------------------------------------------------ GEMM
 //
-// Workgroup: RG x TG waves; wave (rg, tg) owns 16 rows x 32 tokens and keeps
-// the nine f32 chains of its 8 (row, token) pairs per lane in registers.
-// Per block the workgroup stages its A tiles (RG x 9 KiB), B tiles
-// (TG x 9 KiB), d/dmin and d8 in LDS (double-buffered: the next block's
-// global loads are in flight while the current block is computed).
-template <int RG, int TG>
+// Workgroup: 2 x 2 tiles of 32 rows x 32 tokens, two waves per tile: wave
+// half 0 runs residues 0-3 and the minimum, half 1 residues 4-7 (the eight
+// lane-sum chains are independent until the final sum), so a wave keeps 16
+// (row, token) pairs x 4 or 5 f32 chains in registers and two waves share
+// each SIMD.  Per block the workgroup stages its two A tiles and two B tiles
+// (70 KiB) in LDS, double-buffered.  Two ways to fill the buffers (`mode`):
+//   0  global -> registers -> LDS, two blocks ahead: block b + 2 is loaded
+//      into one register set while block b is computed, and the set loaded
+//      during block b - 1 is written to LDS after it (140 KiB in flight per
+//      CU; the loads are latency-bound, so depth is what buys bandwidth);
+//   1  direct buffer-to-LDS loads one block ahead (no staging registers).
+constexpr int RG = 2, TG = 2;                 // row tiles, token tiles per workgroup
+constexpr int NW = 2 * RG * TG;               // waves
+constexpr int UNITS = (RG + TG) * PIECES;     // 1 KiB staging units per block
+constexpr int UPW = UNITS / NW;               // units per wave (9)
+static_assert(UNITS % NW == 0, "every wave stages the same number of units");
+
+// LDS tiles are PIECES whole KiB: the partial last piece is staged with all
+// 64 lanes (no divergent loads or stores, so the compiler's wait counts stay
+// exact); the bytes past the tile's data are never read.
+constexpr int LDS_TILE = PIECES * OP_BYTES;
 struct GemmLDS {
-    uint8_t a[2][RG][TILE_BYTES];
-    uint8_t b[2][TG][TILE_BYTES];
-    float2 dm[2][RG * 16];
-    float d8[2][TG * 32];
+    uint8_t a[2][RG][LDS_TILE];
+    uint8_t b[2][TG][LDS_TILE];
 };
 
-template <int RG, int TG>
-__global__ void __launch_bounds__(64 * RG * TG) k_kq_gemm(GemmArgs g) {
-    constexpr int NT = 64 * RG * TG;
-    extern __shared__ __align__(16) uint8_t smem[];
-    GemmLDS<RG, TG> &S = *reinterpret_cast<GemmLDS<RG, TG> *>(smem);
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int rg = wid % RG, tg = wid / RG;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Where staging unit k of wave `wid` lives: unit u = wid + NW k is piece
+// u % PIECES of tile u / PIECES (A tiles first).  Tiles past the matrix or
+// the batch are clamped to the last one (their results are not stored).
+struct Unit {
+    bool is_a;
+    int tile, piece;
+};
+__device__ __forceinline__ Unit unit_of(int wid, int k) {
+    const int u = wid + NW * k;
+    Unit x;
+    x.tile = u / PIECES;
+    x.piece = u - x.tile * PIECES;
+    x.is_a = x.tile < RG;
+    if (!x.is_a) x.tile -= RG;
+    return x;
+}
+
+struct StageSrc {
+    __amdgpu_buffer_rsrc_t ra, rb;   // this workgroup's A tiles / B tiles (all blocks)
+    int last_a, last_b;              // last valid tile, relative to the workgroup's first
+};
+
+// Byte offset of unit x of block b in its descriptor (all operands uniform,
+// so the offset is a scalar operand of the load).
+__device__ __forceinline__ uint32_t unit_offset(const StageSrc &src, const Unit &x, int nb, int b) {
+    if (x.is_a) {
+        const int t = x.tile < src.last_a ? x.tile : src.last_a;
+        return (uint32_t)((t * nb + b) * A_TILE + x.piece * OP_BYTES);
+    }
+    const int t = x.tile < src.last_b ? x.tile : src.last_b;
+    return (uint32_t)((t * nb + b) * B_TILE + x.piece * OP_BYTES);
+}
+__device__ __forceinline__ uint8_t *unit_dst(GemmLDS &S, const Unit &x, int buf) {
+    return (x.is_a ? S.a[buf][x.tile] : S.b[buf][x.tile]) + x.piece * OP_BYTES;
+}
+
+__device__ __forceinline__ void stage_regs(const StageSrc &src, uint4 (&R)[UPW], int nb, int b, int wid, int lane) {
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+        const Unit x = unit_of(wid, k);
+        R[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(x.is_a ? src.ra : src.rb, lane * 16,
+                                                                               unit_offset(src, x, nb, b), 0));
+    }
+}
+__device__ __forceinline__ void store_regs(GemmLDS &S, const uint4 (&R)[UPW], int buf, int wid, int lane) {
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+        const Unit x = unit_of(wid, k);
+        reinterpret_cast<uint4 *>(unit_dst(S, x, buf))[lane] = R[k];
+    }
+}
+__device__ __forceinline__ void stage_dma(const StageSrc &src, GemmLDS &S, int nb, int b, int buf, int wid, int lane) {
+#pragma unroll
+    for (int k = 0; k < UPW; ++k) {
+        const Unit x = unit_of(wid, k);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(x.is_a ? src.ra : src.rb, (lds_void *)unit_dst(S, x, buf), 16,
+                                                 lane * 16, unit_offset(src, x, nb, b), 0, 0);
+    }
+}
+__device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Both MFMAs of residue l (operands 2l, 2l + 1), or the minimum (l = 8).
+__device__ __forceinline__ v16f residue_mfma(const v8h *Av, const v8h *Bv, int l) {
+    const v16f zero = {};
+    if (l == 8) {
+        v8h a = Av[16 * 64], b = Bv[16 * 64];
+        asm volatile("" : "+v"(a), "+v"(b));
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, zero, 0, 0, 0);
+    }
+    v8h a0 = Av[2 * l * 64], b0 = Bv[2 * l * 64], a1 = Av[(2 * l + 1) * 64], b1 = Bv[(2 * l + 1) * 64];
+    asm volatile("" : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1));
+    const v16f c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, c, 0, 0, 0);
+}
+
+// The f32 chains of one wave.  The lane's pair i (0..15) is row
+// 8 (i / 4) + 4 (lane / 32) + i % 4 of the tile, token lane % 32.
+template <int HV>
+struct Chains {
+    float c[16][4];   // residues 4 HV + r
+    float msum[16];   // the minimum chain (HV 0)
+};
+
+// One block of one wave: HV 0 folds residues 0-3 and the minimum, HV 1
+// residues 4-7, each in the reference's order within its chain.
+template <int HV>
+__device__ __forceinline__ void fold_block(Chains<HV> &ch, const uint8_t *At, const uint8_t *Bt, int lane) {
+    const int h = lane >> 5;
+    const v8h *Av = reinterpret_cast<const v8h *>(At) + lane;
+    const v8h *Bv = reinterpret_cast<const v8h *>(Bt) + lane;
+    const float d8 = reinterpret_cast<const float *>(Bt + OPS * OP_BYTES)[lane & 31];
+    const float4 *dmv = reinterpret_cast<const float4 *>(At + OPS * OP_BYTES);
+    float sc[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 p0 = dmv[4 * q + 2 * h], p1 = dmv[4 * q + 2 * h + 1];
+        sc[4 * q] = __fmul_rn(p0.x, d8);
+        sc[4 * q + 1] = __fmul_rn(p0.z, d8);
+        sc[4 * q + 2] = __fmul_rn(p1.x, d8);
+        sc[4 * q + 3] = __fmul_rn(p1.z, d8);
+    }
+    // The MFMAs of step r + 1 go out before step r is folded; the empty asm
+    // statements (no instructions) keep the compiler from hoisting every
+    // step's MFMAs (16 result registers each) above the folds.
+    v16f cn = residue_mfma(Av, Bv, 4 * HV);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const v16f c = cn;
+        if (r < 3) cn = residue_mfma(Av, Bv, 4 * HV + r + 1);
+        else if (HV == 0) cn = residue_mfma(Av, Bv, 8);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ch.c[i][r] = __fadd_rn(ch.c[i][r], __fmul_rn(sc[i], c[i]));
+        asm volatile("" : "+v"(ch.c[0][r]), "+v"(ch.c[1][r]), "+v"(ch.c[2][r]), "+v"(ch.c[3][r]),
+                     "+v"(ch.c[4][r]), "+v"(ch.c[5][r]), "+v"(ch.c[6][r]), "+v"(ch.c[7][r]),
+                     "+v"(ch.c[8][r]), "+v"(ch.c[9][r]), "+v"(ch.c[10][r]), "+v"(ch.c[11][r]),
+                     "+v"(ch.c[12][r]), "+v"(ch.c[13][r]), "+v"(ch.c[14][r]), "+v"(ch.c[15][r]));
+    }
+    if (HV == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 p0 = dmv[4 * q + 2 * h], p1 = dmv[4 * q + 2 * h + 1];
+            const float ms[4] = {__fmul_rn(p0.y, d8), __fmul_rn(p0.w, d8), __fmul_rn(p1.y, d8), __fmul_rn(p1.w, d8)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ch.msum[4 * q + e] = __fsub_rn(ch.msum[4 * q + e], __fmul_rn(ms[e], cn[4 * q + e]));
+        }
+    }
+}
+
+template <int MODE, int HV>
+__device__ __forceinline__ void gemm_tile(const GemmArgs &g, const MatGemm &M, GemmLDS &S, const StageSrc &src,
+                                          int rg, int tg, int tw, int wid, int lane, int rt0, int tt0) {
     const int nb = g.nb;
-    const int m_sel = blockIdx.y;   // which matrix of the launch
-    const MatGemm &M = g.mat[m_sel];
-    const int row_tiles_wg = (M.rows + 16 * RG - 1) / (16 * RG);
-    const int tok_tiles_wg = (g.n_tokens + 32 * TG - 1) / (32 * TG);
+    Chains<HV> ch;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        ch.msum[i] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ch.c[i][r] = 0.0f;
+    }
+    if (MODE == 0) {
+        // Block j: loaded into R[j % 2] during block j - 2, written to LDS
+        // buffer j % 2 after block j - 1, computed as block j.  The loads
+        // are unconditional (block index clamped; past the end they re-read
+        // the last block) so the compiler's wait before each LDS store
+        // leaves the younger set's loads in flight.
+        const int last = nb - 1;
+        uint4 R0[UPW], R1[UPW];
+        stage_regs(src, R0, nb, 0, wid, lane);
+        stage_regs(src, R1, nb, 1 < last ? 1 : last, wid, lane);
+        store_regs(S, R0, 0, wid, lane);
+        __syncthreads();
+        for (int b = 0; b < nb; b += 2) {
+            stage_regs(src, R0, nb, b + 2 < last ? b + 2 : last, wid, lane);
+            fold_block<HV>(ch, S.a[0][rg], S.b[0][tg], lane);
+            if (b + 1 < nb) store_regs(S, R1, 1, wid, lane);
+            __syncthreads();
+            if (b + 1 >= nb) break;
+            stage_regs(src, R1, nb, b + 3 < last ? b + 3 : last, wid, lane);
+            fold_block<HV>(ch, S.a[1][rg], S.b[1][tg], lane);
+            if (b + 2 < nb) store_regs(S, R0, 0, wid, lane);
+            __syncthreads();
+        }
+    } else {
+        stage_dma(src, S, nb, 0, 0, wid, lane);
+        wait_dma();
+        __syncthreads();
+        for (int b = 0; b < nb; ++b) {
+            const int buf = b & 1;
+            if (b + 1 < nb) stage_dma(src, S, nb, b + 1, buf ^ 1, wid, lane);
+            fold_block<HV>(ch, S.a[buf][rg], S.b[buf][tg], lane);
+            wait_dma();
+            __syncthreads();
+        }
+    }
+
+    // result = minimum chain + sums[0] + ... + sums[7]: half 0 adds its four
+    // chains onto the minimum chain and hands the partial to half 1 through
+    // LDS (the staging buffers are free after the last barrier).
+    const int h = lane >> 5;
+    float *xch = reinterpret_cast<float *>(&S) + tw * 16 * 64;
+    if (HV == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float v = ch.msum[i];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v = __fadd_rn(v, ch.c[i][r]);
+            xch[i * 64 + lane] = v;
+        }
+    }
+    __syncthreads();
+    if (HV == 1) {
+        const int t = (tt0 + tg) * 32 + (lane & 31);
+        if (t >= g.n_tokens) return;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int row = (rt0 + rg) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+            float v = xch[i * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v = __fadd_rn(v, ch.c[i][r]);
+            if (row < M.rows) M.y[(long long)t * M.ldy + row] = v;
+        }
+    }
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(64 * NW) k_kq_gemm(GemmArgs g) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    GemmLDS &S = *reinterpret_cast<GemmLDS *>(smem);
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // waves w and w + RG * TG (the two halves of one tile) land on the same SIMD
+    const int tw = wid % (RG * TG), hv = wid / (RG * TG);
+    const int rg = tw % RG, tg = tw / RG;
+    const MatGemm &M = g.mat[blockIdx.y];   // which matrix of the launch
+    const int n_rt = (M.rows + 31) / 32, n_tt = (g.n_tokens + 31) / 32;
+    const int row_wgs = (n_rt + RG - 1) / RG, tok_wgs = (n_tt + TG - 1) / TG;
     // XCD-aware order: workgroups are dealt to the eight XCDs round robin;
     // consecutive workgroups of one XCD share a row tile, so each A tile is
     // fetched into that XCD's L2 once for all of its token tiles.
-    const int nwg = row_tiles_wg * tok_tiles_wg;
+    const int nwg = row_wgs * tok_wgs;
     const int id = (int)blockIdx.x;
     if (id >= nwg) return;
     const int nfull = nwg & ~7;
     const int lin = id < nfull ? (id % 8) * (nfull / 8) + id / 8 : id;   // a bijection of [0, nwg)
-    const int wrt = lin / tok_tiles_wg, wtt = lin - wrt * tok_tiles_wg;
-    const int rtile0 = wrt * RG, ttile0 = wtt * TG;
+    const int wrt = lin / tok_wgs, wtt = lin - wrt * tok_wgs;
+    const int rt0 = wrt * RG, tt0 = wtt * TG;
 
-    // staging: per block, RG A tiles + TG B tiles as 16-byte units, then dm/d8
-    constexpr int UNITS = (RG + TG) * TILE_BYTES / 16;
-    constexpr int PER = (UNITS + NT - 1) / NT;
-    uint4 st[PER];
-    float2 st_dm;
-    float st_d8;
-    const int n_rtiles = (M.rows + 15) / 16;
-    const int n_ttiles = (g.n_tokens + 31) / 32;
-    auto load_stage = [&](int b) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int uidx = tid + i * NT;
-            st[i] = make_uint4(0, 0, 0, 0);
-            if (uidx < UNITS) {
-                const int which = uidx / (TILE_BYTES / 16), off = uidx - which * (TILE_BYTES / 16);
-                if (which < RG) {
-                    const int rt = rtile0 + which;
-                    if (rt < n_rtiles)
-                        st[i] = reinterpret_cast<const uint4 *>(M.a + ((long long)rt * nb + b) * TILE_BYTES)[off];
-                } else {
-                    const int tt = ttile0 + which - RG;
-                    if (tt < n_ttiles)
-                        st[i] = reinterpret_cast<const uint4 *>(g.b + ((long long)tt * nb + b) * TILE_BYTES)[off];
-                }
-            }
-        }
-        st_dm = make_float2(0.0f, 0.0f);
-        if (tid < RG * 16) {
-            const int r = rtile0 * 16 + tid;
-            if (r < M.rows) st_dm = M.dm[(long long)r * nb + b];
-        }
-        st_d8 = 0.0f;
-        if (tid < TG * 32) {
-            const int tt = ttile0 + tid / 32;
-            if (tt < n_ttiles) st_d8 = g.d8[((long long)tt * nb + b) * 32 + (tid & 31)];
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int uidx = tid + i * NT;
-            if (uidx < UNITS) {
-                const int which = uidx / (TILE_BYTES / 16), off = uidx - which * (TILE_BYTES / 16);
-                uint4 *dst = which < RG ? reinterpret_cast<uint4 *>(S.a[buf][which])
-                                        : reinterpret_cast<uint4 *>(S.b[buf][which - RG]);
-                dst[off] = st[i];
-            }
-        }
-        if (tid < RG * 16) S.dm[buf][tid] = st_dm;
-        if (tid < TG * 32) S.d8[buf][tid] = st_d8;
-    };
+    StageSrc src;
+    src.ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(M.a + (long long)rt0 * g.nb * A_TILE), (short)0,
+                                               RG * g.nb * A_TILE, 0x00020000);
+    src.rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(g.b + (long long)tt0 * g.nb * B_TILE), (short)0,
+                                               TG * g.nb * B_TILE, 0x00020000);
+    src.last_a = n_rt - 1 - rt0;
+    src.last_b = n_tt - 1 - tt0;
 
-    // The lane's rows: register pair (r, r + 1), r = 4 (s / 2) + 2 (s % 2),
-    // holds (hi, lo) of real row 4 (s / 2) + 2 (lane / 32) + s % 2 of the tile.
-    const int hsel = lane >> 5;
-    float chain[8][8];
-    float msum[8];
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        msum[s] = 0.0f;
-#pragma unroll
-        for (int l = 0; l < 8; ++l) chain[s][l] = 0.0f;
-    }
-
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-    for (int b = 0; b < nb; ++b) {
-        const int buf = b & 1;
-        if (b + 1 < nb) load_stage(b + 1);
-        const uint8_t *A = S.a[buf][rg];
-        const uint8_t *B = S.b[buf][tg];
-        const float d8 = S.d8[buf][tg * 32 + (lane & 31)];
-        float sc[8], ms[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-            const float2 dm = S.dm[buf][rg * 16 + 4 * (s >> 1) + 2 * hsel + (s & 1)];
-            sc[s] = __fmul_rn(dm.x, d8);
-            ms[s] = __fmul_rn(dm.y, d8);
-        }
-        // Two accumulators in flight: the MFMA of operand l + 1 is issued
-        // before operand l is folded.  The empty asm statements (no
-        // instructions) order "operands of l + 1 ready" after "fold of l - 1
-        // done", so the compiler cannot hoist every MFMA of the block (nine
-        // 16-register results) ahead of the folds.
-        const v4i *Av = reinterpret_cast<const v4i *>(A) + lane;
-        const v4i *Bv = reinterpret_cast<const v4i *>(B) + lane;
-        const v16i zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-        v4i a0 = Av[0], b0 = Bv[0];
-        asm volatile("" : "+v"(a0), "+v"(b0));
-        v16i cn = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, zero, 0, 0, 0);
-#pragma unroll
-        for (int l = 0; l < OPS; ++l) {
-            const v16i c = cn;
-            if (l + 1 < OPS) {
-                v4i an = Av[(l + 1) * 64], bn = Bv[(l + 1) * 64];
-                asm volatile("" : "+v"(an), "+v"(bn));
-                cn = __builtin_amdgcn_mfma_i32_32x32x32_i8(an, bn, zero, 0, 0, 0);
-            }
-            if (l < 8) {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const int r = 4 * (s >> 1) + 2 * (s & 1);
-                    const int v = (c[r] << 6) + c[r + 1];
-                    chain[s][l] = __fadd_rn(chain[s][l], __fmul_rn(sc[s], (float)v));
-                }
-                asm volatile("" : "+v"(chain[0][l]), "+v"(chain[1][l]), "+v"(chain[2][l]), "+v"(chain[3][l]),
-                             "+v"(chain[4][l]), "+v"(chain[5][l]), "+v"(chain[6][l]), "+v"(chain[7][l]));
-            } else {
-#pragma unroll
-                for (int s = 0; s < 8; ++s) {
-                    const int r = 4 * (s >> 1) + 2 * (s & 1);
-                    const int v = (c[r] << 7) + c[r + 1];
-                    msum[s] = __fsub_rn(msum[s], __fmul_rn(ms[s], (float)v));
-                }
-                asm volatile("" : "+v"(msum[0]), "+v"(msum[1]), "+v"(msum[2]), "+v"(msum[3]), "+v"(msum[4]),
-                             "+v"(msum[5]), "+v"(msum[6]), "+v"(msum[7]));
-            }
-        }
-        if (b + 1 < nb) store_stage(buf ^ 1);
-        __syncthreads();
-    }
-
-    const int t = (ttile0 + tg) * 32 + (lane & 31);
-    if (t >= g.n_tokens) return;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const int r = (rtile0 + rg) * 16 + 4 * (s >> 1) + 2 * hsel + (s & 1);
-        if (r >= M.rows) continue;
-        float v = msum[s];
-#pragma unroll
-        for (int l = 0; l < 8; ++l) v = __fadd_rn(v, chain[s][l]);
-        M.y[(long long)t * M.ldy + r] = v;
-    }
+    if (hv == 0)
+        gemm_tile<MODE, 0>(g, M, S, src, rg, tg, tw, wid, lane, rt0, tt0);
+    else
+        gemm_tile<MODE, 1>(g, M, S, src, rg, tg, tw, wid, lane, rt0, tt0);
 }
 
 // ---------------------------------------------------------------- launchers
 
 static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
-size_t gemm_a_bytes(int rows, int nb) { return (size_t)cdiv(rows, 16) * nb * TILE_BYTES; }
-size_t gemm_dm_bytes(int rows, int nb) { return (size_t)cdiv(rows, 16) * 16 * nb * sizeof(float2); }
-size_t gemm_b_bytes(int n_tokens, int nb) {
-    return (size_t)cdiv(n_tokens, 32) * nb * (TILE_BYTES + 32 * sizeof(float));
-}
+size_t gemm_a_bytes(int rows, int nb) { return (size_t)cdiv(rows, 32) * nb * A_TILE; }
+size_t gemm_b_bytes(int n_tokens, int nb) { return (size_t)cdiv(n_tokens, 32) * nb * B_TILE; }
 
-hipError_t launch_prep_a(const MatView &m, uint8_t *a, float2 *dm, hipStream_t s) {
-    const int grid = cdiv(m.rows, 16) * m.nb;
+hipError_t launch_prep_a(const MatView &m, uint8_t *a, hipStream_t s) {
+    const int grid = cdiv(m.rows, 32) * m.nb;
     if (m.type == T_Q4_K)
-        hipLaunchKernelGGL(k_prep_a<T_Q4_K>, dim3(grid), dim3(64), 0, s, m, a, dm);
+        hipLaunchKernelGGL(k_prep_a<T_Q4_K>, dim3(grid), dim3(64), 0, s, m, a);
     else if (m.type == T_Q5_K)
-        hipLaunchKernelGGL(k_prep_a<T_Q5_K>, dim3(grid), dim3(64), 0, s, m, a, dm);
+        hipLaunchKernelGGL(k_prep_a<T_Q5_K>, dim3(grid), dim3(64), 0, s, m, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
-hipError_t launch_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b, float *d8, hipStream_t s) {
-    hipLaunchKernelGGL(k_prep_b, dim3(cdiv(n_tokens, 32) * nb), dim3(64), 0, s, q8, n_tokens, nb, b, d8);
+hipError_t launch_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b, hipStream_t s) {
+    hipLaunchKernelGGL(k_prep_b, dim3(cdiv(n_tokens, 32) * nb), dim3(64), 0, s, q8, n_tokens, nb, b);
     return hipGetLastError();
 }
 
-template <int RG, int TG>
-static hipError_t gemm_shape(const GemmArgs &g, hipStream_t s) {
-    const int lds = (int)sizeof(GemmLDS<RG, TG>);
-    if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_kq_gemm<RG, TG>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e != hipSuccess) return e;
-    }
+template <int MODE>
+static hipError_t gemm_mode(const GemmArgs &g, hipStream_t s) {
+    const int lds = (int)sizeof(GemmLDS);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(k_kq_gemm<MODE>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (e != hipSuccess) return e;
     int rows = 0;
     for (int i = 0; i < g.n_mat; ++i) rows = g.mat[i].rows > rows ? g.mat[i].rows : rows;
-    const int grid = cdiv(rows, 16 * RG) * cdiv(g.n_tokens, 32 * TG);
-    hipLaunchKernelGGL((k_kq_gemm<RG, TG>), dim3(grid, g.n_mat), dim3(64 * RG * TG), lds, s, g);
+    const int grid = cdiv(cdiv(rows, 32), RG) * cdiv(cdiv(g.n_tokens, 32), TG);
+    hipLaunchKernelGGL((k_kq_gemm<MODE>), dim3(grid, g.n_mat), dim3(64 * NW), lds, s, g);
     return hipGetLastError();
 }
 
 hipError_t launch_kq_gemm(const GemmArgs &g, hipStream_t s) {
-    if (g.n_mat < 1 || g.n_mat > GEMM_MAX_MATS || g.n_tokens < 1 || g.nb < 1) return hipErrorInvalidValue;
-    switch (g.shape) {
-    case 0: return gemm_shape<2, 4>(g, s);
-    case 1: return gemm_shape<2, 2>(g, s);
-    case 2: return gemm_shape<4, 2>(g, s);
-    default: return gemm_shape<1, 4>(g, s);
-    }
+    if (g.n_mat < 1 || g.n_mat > GEMM_MAX_MATS || g.n_tokens < 1 || g.nb < 1 || g.nb > 64) return hipErrorInvalidValue;
+    return g.shape == 1 ? gemm_mode<1>(g, s) : gemm_mode<0>(g, s);
 }
 
 }  // namespace lbh

@@ -113,14 +113,13 @@ struct MoeArgs {
     RouterArgs router;
 };
 
-// ------------------------------------------------ K-quant GEMM on i8 MFMA
+// ------------------------------------------------ K-quant GEMM on f16 MFMA
 
 constexpr int GEMM_MAX_MATS = 3;
 
-// One matrix of a GEMM launch: its MFMA-ready copy (A tiles, d/dmin) and output.
+// One matrix of a GEMM launch: its MFMA-ready copy and output.
 struct MatGemm {
-    const uint8_t *a;      // [ceil(rows / 16)][nb] tiles of 9 KiB
-    const float2 *dm;      // [ceil(rows / 16) * 16][nb] (d, dmin)
+    const uint8_t *a;      // [ceil(rows / 32)][nb] A tiles (operands, then (d, dmin) per row)
     float *y;              // y[t * ldy + r]
     int32_t rows;
     int32_t ldy;
@@ -128,8 +127,7 @@ struct MatGemm {
 
 struct GemmArgs {
     MatGemm mat[GEMM_MAX_MATS];   // matrices sharing K and the activations
-    const uint8_t *b;             // [ceil(n_tokens / 32)][nb] tiles of 9 KiB
-    const float *d8;              // [ceil(n_tokens / 32)][nb][32]
+    const uint8_t *b;             // [ceil(n_tokens / 32)][nb] B tiles (operands, then d8 per token)
     int32_t n_mat, nb, n_tokens, shape;
 };
 
@@ -169,13 +167,12 @@ struct BatchArgs {
     int32_t rt_gu_r, rt_gu_s;   // gate/up rows per workgroup (routed, shared)
     int32_t rt_d_r, rt_d_s;     // down rows per workgroup (routed, shared)
     int32_t type_gate_r, type_down_r;
-    // K-quant shared expert on the i8 matrix cores: gate/up -> g_s/u_s, SwiGLU
+    // K-quant shared expert on the matrix cores: gate/up -> g_s/u_s, SwiGLU
     // fused into the h quantization, down -> d_s.
     int32_t shared_gemm, gemm_shape;
     MatGemm sg, su, sd;         // MFMA-ready copies of the shared gate / up / down
     float *g_s, *u_s;           // [n_tokens][ffn_s]
     uint8_t *bx, *bh;           // GEMM activation tiles of x and of h_s
-    float *d8x, *d8h;
 };
 
 // Batch selection: top-k of each token's finished logits (select_route).
@@ -190,10 +187,9 @@ struct RouteBatchArgs {
 };
 
 size_t gemm_a_bytes(int rows, int nb);
-size_t gemm_dm_bytes(int rows, int nb);
 size_t gemm_b_bytes(int n_tokens, int nb);
-hipError_t launch_prep_a(const MatView &m, uint8_t *a, float2 *dm, hipStream_t s);
-hipError_t launch_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b, float *d8, hipStream_t s);
+hipError_t launch_prep_a(const MatView &m, uint8_t *a, hipStream_t s);
+hipError_t launch_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b, hipStream_t s);
 hipError_t launch_kq_gemm(const GemmArgs &g, hipStream_t s);
 
 hipError_t launch_route_batch(const RouteBatchArgs &a, hipStream_t s);

@@ -236,7 +236,7 @@ class HipBackend:
             raise KernelError(LbhError(status=st))
 
     def gemm_q8_k(self, m: "DeviceMatrix", q8, n_tokens: int, y, workspace) -> None:
-        """y[t, r] = vec_dot_q8_k(row r, token t) for a batch of Q8_K rows on the i8
+        """y[t, r] = vec_dot_q8_k(row r, token t) for a batch of Q8_K rows on the
         matrix cores (the matrix must be prepared with DeviceMatrix.prepare_gemm)."""
         st = lib().lbh_gemm_q8_k(self.ctx, m.handle, _dev_ptr(q8), n_tokens, _dev_ptr(y), _dev_ptr(workspace),
                                  workspace.numel() * workspace.element_size())

@@ -1,10 +1,10 @@
-"""GPU parity of the i8-MFMA K-quant GEMM (lbh_gemm_q8_k) against the CPU oracle.
+"""GPU parity of the matrix-core K-quant GEMM (lbh_gemm_q8_k) against the CPU oracle.
 
 Every output y[t, r] must equal the reference's per-row dot
 (dot_q4_or_q5_k, crates/bridge-quant-layout/src/q8_k.rs:247-327) of row r with
 token t's Q8_K row, bit for bit: random blocks, negative d/dmin, the integer
 extremes (scale 63, mins 63, 5-bit quants 31, activations at +-127), ragged row
-and token counts, every workgroup shape, and the BASELINE configs[4] shape
+and token counts, both tile staging modes, and the BASELINE configs[4] shape
 (Q5_K 12288 x 4096, 512 tokens) in full.
 """
 import numpy as np
@@ -85,8 +85,8 @@ def test_gemm_integer_extremes(be, oracle, ty):
     assert _same(run_gemm(be, ty, w, rows, k, q8), oracle_gemm(oracle, ty, w, rows, k, q8))
 
 
-@pytest.mark.parametrize("shape", [0, 1, 2, 3])
-def test_gemm_workgroup_shapes_give_the_same_bits(be, oracle, shape):
+@pytest.mark.parametrize("shape", [0, 1])
+def test_gemm_staging_modes_give_the_same_bits(be, oracle, shape):
     rows, k, n = 200, 1024, 100
     w = synth.random_matrix(Q5_K, rows, k, seed=9)
     q8 = q8_rows(oracle, np.random.default_rng(10).standard_normal((n, k)).astype(np.float32))
