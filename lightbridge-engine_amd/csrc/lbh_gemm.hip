@@ -242,12 +242,17 @@ __device__ __forceinline__ uint8_t *unit_dst(GemmLDS &S, const Unit &x, int buf)
     return (x.is_a ? S.a[buf][x.tile] : S.b[buf][x.tile]) + x.piece * OP_BYTES;
 }
 
+// Loads block b's units of this wave into R; for b >= nb the lane offset is
+// pushed past the descriptors' ranges (< 2^31 bytes), so the loads return
+// zeros and read no memory.
 __device__ __forceinline__ void stage_regs(const StageSrc &src, uint4 (&R)[UPW], int nb, int b, int wid, int lane) {
+    const uint32_t vo = (uint32_t)lane * 16 + (b < nb ? 0u : 0x80000000u);
+    const int bc = b < nb ? b : nb - 1;
 #pragma unroll
     for (int k = 0; k < UPW; ++k) {
         const Unit x = unit_of(wid, k);
-        R[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(x.is_a ? src.ra : src.rb, lane * 16,
-                                                                               unit_offset(src, x, nb, b), 0));
+        R[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(x.is_a ? src.ra : src.rb, vo,
+                                                                               unit_offset(src, x, nb, bc), 0));
     }
 }
 __device__ __forceinline__ void store_regs(GemmLDS &S, const uint4 (&R)[UPW], int buf, int wid, int lane) {
@@ -348,23 +353,23 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs &g, const MatGemm &M, G
     }
     if (MODE == 0) {
         // Block j: loaded into R[j % 2] during block j - 2, written to LDS
-        // buffer j % 2 after block j - 1, computed as block j.  The loads
-        // are unconditional (block index clamped; past the end they re-read
-        // the last block) so the compiler's wait before each LDS store
-        // leaves the younger set's loads in flight.
-        const int last = nb - 1;
+        // buffer j % 2 after block j - 1, computed as block j.  Every load
+        // is unconditional, so the compiler's wait before each LDS store
+        // leaves the younger set's loads in flight; loads past the last
+        // block are sent out of the descriptor's range (they return zeros
+        // without touching memory).
         uint4 R0[UPW], R1[UPW];
         stage_regs(src, R0, nb, 0, wid, lane);
-        stage_regs(src, R1, nb, 1 < last ? 1 : last, wid, lane);
+        stage_regs(src, R1, nb, 1, wid, lane);
         store_regs(S, R0, 0, wid, lane);
         __syncthreads();
         for (int b = 0; b < nb; b += 2) {
-            stage_regs(src, R0, nb, b + 2 < last ? b + 2 : last, wid, lane);
+            stage_regs(src, R0, nb, b + 2, wid, lane);
             fold_block<HV>(ch, S.a[0][rg], S.b[0][tg], lane);
             if (b + 1 < nb) store_regs(S, R1, 1, wid, lane);
             __syncthreads();
             if (b + 1 >= nb) break;
-            stage_regs(src, R1, nb, b + 3 < last ? b + 3 : last, wid, lane);
+            stage_regs(src, R1, nb, b + 3, wid, lane);
             fold_block<HV>(ch, S.a[1][rg], S.b[1][tg], lane);
             if (b + 2 < nb) store_regs(S, R0, 0, wid, lane);
             __syncthreads();
