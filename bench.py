@@ -55,7 +55,7 @@ BATCH_TOKENS = 64
 # HBM bytes per launch (read + write) measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain copy of
 # known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2355397 + 6144, "down": 2965999 + 19648, "prefill": 220835137 + 25170528}
+MEASURED_TRAFFIC = {"gate": 2384059 + 6144, "down": 2981354 + 19648, "prefill": 324295660 + 25175088}
 
 
 def parse():

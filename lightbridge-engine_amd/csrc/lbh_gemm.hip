@@ -23,7 +23,7 @@
 //
 // Layouts (built once per matrix by k_prep_a, per call by k_prep_b):
 //   A tile (32 rows, block b): 17 operands x 64 lanes x 16 B, then the 32
-//     rows' (d, dmin) as f32 pairs.  Operand 2l + p, lane j: row j % 32, the
+//     rows' d, then their dmin, as f32.  Operand 2l + p, lane j: row j % 32, the
 //     8 f16 of sub-blocks 4p + 2 (j / 32) + e / 4, element 8 (e % 4) + l.
 //     Operand 16, lane j: sub-blocks 4 (j / 32) + e / 2, (128 mn, mn).
 //   B tile (32 tokens, block b): the same operands for token j % 32 (Q8_K
@@ -40,7 +40,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int OPS = 17;                          // 8 residues x 2 halves + the minimum
 constexpr int OP_BYTES = 1024;                   // 64 lanes x 8 f16
-constexpr int A_TILE = OPS * OP_BYTES + 32 * 8;  // + (d, dmin) of the tile's rows
+constexpr int A_TILE = OPS * OP_BYTES + 32 * 8;  // + d[32], dmin[32] of the tile's rows
 constexpr int B_TILE = OPS * OP_BYTES + 32 * 4;  // + d8 of the tile's tokens
 constexpr int PIECES = OPS + 1;                  // 1 KiB staging units per tile (the last one partial)
 
@@ -112,7 +112,9 @@ __global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out) {
             const uint32_t hdr = *reinterpret_cast<const uint32_t *>(blk);
             v = make_float2(f16_to_f32(hdr & 0xffffu), f16_to_f32(hdr >> 16));
         }
-        reinterpret_cast<float2 *>(tile_base + OPS * OP_BYTES)[lane] = v;
+        float *dm = reinterpret_cast<float *>(tile_base + OPS * OP_BYTES);
+        dm[lane] = v.x;
+        dm[32 + lane] = v.y;
     }
 }
 
@@ -302,15 +304,16 @@ __device__ __forceinline__ void fold_block(Chains<HV> &ch, const uint8_t *At, co
     const v8h *Av = reinterpret_cast<const v8h *>(At) + lane;
     const v8h *Bv = reinterpret_cast<const v8h *>(Bt) + lane;
     const float d8 = reinterpret_cast<const float *>(Bt + OPS * OP_BYTES)[lane & 31];
-    const float4 *dmv = reinterpret_cast<const float4 *>(At + OPS * OP_BYTES);
+    // d of rows 8q + 4h + 0..3 (the lane's pairs 4q..4q + 3): one 16-byte read per q
+    const float4 *dv = reinterpret_cast<const float4 *>(At + OPS * OP_BYTES);
     float sc[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float4 p0 = dmv[4 * q + 2 * h], p1 = dmv[4 * q + 2 * h + 1];
-        sc[4 * q] = __fmul_rn(p0.x, d8);
-        sc[4 * q + 1] = __fmul_rn(p0.z, d8);
-        sc[4 * q + 2] = __fmul_rn(p1.x, d8);
-        sc[4 * q + 3] = __fmul_rn(p1.z, d8);
+        const float4 d = dv[2 * q + h];
+        sc[4 * q] = __fmul_rn(d.x, d8);
+        sc[4 * q + 1] = __fmul_rn(d.y, d8);
+        sc[4 * q + 2] = __fmul_rn(d.z, d8);
+        sc[4 * q + 3] = __fmul_rn(d.w, d8);
     }
     // The MFMAs of step r + 1 go out before step r is folded; the empty asm
     // statements (no instructions) keep the compiler from hoisting every
@@ -331,8 +334,8 @@ __device__ __forceinline__ void fold_block(Chains<HV> &ch, const uint8_t *At, co
     if (HV == 0) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 p0 = dmv[4 * q + 2 * h], p1 = dmv[4 * q + 2 * h + 1];
-            const float ms[4] = {__fmul_rn(p0.y, d8), __fmul_rn(p0.w, d8), __fmul_rn(p1.y, d8), __fmul_rn(p1.w, d8)};
+            const float4 m = dv[8 + 2 * q + h];   // dmin
+            const float ms[4] = {__fmul_rn(m.x, d8), __fmul_rn(m.y, d8), __fmul_rn(m.z, d8), __fmul_rn(m.w, d8)};
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 ch.msum[4 * q + e] = __fsub_rn(ch.msum[4 * q + e], __fmul_rn(ms[e], cn[4 * q + e]));
