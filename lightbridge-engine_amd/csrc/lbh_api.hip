@@ -464,6 +464,7 @@ struct lbh_moe {
     size_t n_experts, hidden, ffn_r, ffn_s;
     int type_gate_r, type_down_r;
     ExpertDev *experts_dev;
+    ExpertDev *experts_host;  // the same table on the host (host-given routing passes planes as arguments)
     ExpertDev shared;
     int has_shared;
     float *h;
@@ -489,6 +490,7 @@ void free_moe(lbh_moe *m) {
     if (!m) return;
     DeviceGuard g(m->device);
     if (m->experts_dev) (void)hipFree(m->experts_dev);
+    delete[] m->experts_host;
     if (m->batch_mem) (void)hipFree(m->batch_mem);
     if (m->shared_gemm_mem) (void)hipFree(m->shared_gemm_mem);
     if (m->plan_host) (void)hipHostFree(m->plan_host);
@@ -523,7 +525,19 @@ MoeArgs moe_args(const lbh_moe *m, const float *x, float *y) {
     a.stop_step = 0x7fffffff;
     a.type_gate_r = m->type_gate_r;
     a.type_down_r = m->type_down_r;
+    a.routed_shape = m->experts_host[0];
     return a;
+}
+
+// Host-given routing: the routed experts' planes go into the arguments.
+void set_routed_planes(MoeArgs &a, const lbh_moe *m, const uint32_t *ids, size_t n) {
+    a.routed_given = 1;
+    for (size_t i = 0; i < n; ++i) {
+        const ExpertDev &e = m->experts_host[ids[i]];
+        a.routed_planes[i][0] = e.gate.planes;
+        a.routed_planes[i][1] = e.up.planes;
+        a.routed_planes[i][2] = e.down.planes;
+    }
 }
 
 }  // namespace
@@ -578,17 +592,18 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
         m->shared.up = view_of(shared_up);
         m->shared.down = view_of(shared_down);
     }
-    // Gate/up workgroups: three per CU, split in proportion to the decode
-    // work of the top-8 routed experts and of the shared expert (per byte an
-    // IQ stream issues about three times the VALU work of a K-quant one).
+    // Gate/up workgroups (measured on the configs[2] shapes): two per CU for
+    // the routed stream, and for the shared stream its byte share of two per
+    // CU (the top-8 routed gate/up against the shared gate/up).  More routed
+    // workgroups slow the device-router path, where every routed workgroup
+    // selects the route from the logits in its prologue.
     {
-        auto cost = [](int ty) { return ty == LBH_IQ2_S || ty == LBH_IQ3_S ? 3.0 : 1.0; };
-        const double br = 8.0 * 2.0 * (double)gate[0]->bytes * cost(tg);
-        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes * cost(shared_gate->type) : 0.0;
-        const int total = 3 * ctx->cu_count;
+        const double br = 8.0 * 2.0 * (double)gate[0]->bytes;
+        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes : 0.0;
+        const int total = 2 * ctx->cu_count;
         m->wg_s = has_shared ? (int)(total * bs / (br + bs) + 0.5) : 0;
         if (has_shared && m->wg_s < 1) m->wg_s = 1;
-        m->wg_r = total - m->wg_s > 1 ? total - m->wg_s : 1;
+        m->wg_r = total;
     }
     m->tile_d = 16;
     m->tc = 8;
@@ -609,9 +624,9 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
         table[e].up = view_of(up[e]);
         table[e].down = view_of(down[e]);
     }
+    m->experts_host = table;
     hipError_t e = hipMalloc(&m->experts_dev, n_experts * sizeof(ExpertDev));
     if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
-    delete[] table;
     if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&m->status, sizeof(MoeStatus));
     if (e == hipSuccess) e = hipHostMalloc(&m->status_host, sizeof(MoeStatus), hipHostMallocDefault);
@@ -652,6 +667,7 @@ lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const 
         a.route.coefs[i] = coefs[i];
     }
     a.n_launch = (int32_t)n_routed;
+    set_routed_planes(a, m, ids, n_routed);
     DeviceGuard g(ctx->device);
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
@@ -701,6 +717,7 @@ lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *i
         a.route.ids[i] = ids[i];
         a.route.coefs[i] = coefs[i];
     }
+    set_routed_planes(a, m, ids, i_host);
     a.status = m->status;
     a.check = 1;
     a.n_launch = (int32_t)i_host;

@@ -111,6 +111,12 @@ struct MoeArgs {
     int32_t select_in_kernel;
     int32_t skip_shared_gate_up;
     RouterArgs router;
+    // Host-given routing: the routed experts' plane pointers per routing slot
+    // travel in the arguments (no dependent load of the expert table before
+    // the first weight loads); every routed expert has routed_shape's views.
+    int32_t routed_given;
+    ExpertDev routed_shape;
+    const uint8_t *routed_planes[MOE_MAX_ROUTED][3];   // gate, up, down
 };
 
 // ------------------------------------------------ K-quant GEMM on f16 MFMA

@@ -33,6 +33,16 @@ __device__ __forceinline__ int route_n(const MoeArgs &a) { return a.route_dev ? 
 __device__ __forceinline__ uint32_t route_id(const MoeArgs &a, int s) {
     return a.route_dev ? a.route_dev->ids[s] : a.route.ids[s];
 }
+// Views of the routed expert in routing slot s (expert id e): from the
+// arguments when the host gave the routing, else from the device table.
+__device__ __forceinline__ ExpertDev routed_view(const MoeArgs &a, int s, uint32_t e) {
+    if (!a.routed_given) return a.experts[e];
+    ExpertDev v = a.routed_shape;
+    v.gate.planes = a.routed_planes[s][0];
+    v.up.planes = a.routed_planes[s][1];
+    v.down.planes = a.routed_planes[s][2];
+    return v;
+}
 __device__ __forceinline__ float route_coef(const MoeArgs &a, int s) {
     return a.route_dev ? a.route_dev->coefs[s] : a.route.coefs[s];
 }
@@ -177,7 +187,7 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
         s_ids[threadIdx.x] = route_id(a, threadIdx.x < route_n(a) ? threadIdx.x : 0);
     }
     __syncthreads();
-    if (threadIdx.x < a.n_launch) s_views[threadIdx.x] = a.experts[s_ids[threadIdx.x]];
+    if (threadIdx.x < a.n_launch) s_views[threadIdx.x] = routed_view(a, threadIdx.x, s_ids[threadIdx.x]);
     __syncthreads();
     const int wg_r = gridDim.x - wg_s;
     gate_up_stream<TYR, LPUR>(a, RoutedSlots{s_views}, a.n_launch, a.ffn_r, (blockIdx.x - wg_s) * MOE_WAVES,
@@ -290,7 +300,7 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     const int tasks = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
     for (int t = wid; t < tasks; t += nw) {
         if (t < n) {
-            down_wave<TYR, LPUR>(a.experts[route_id(a, t)].down, s_q8 + t * nbr * 292, nbr, r0, r1, 0, 1,
+            down_wave<TYR, LPUR>(routed_view(a, t, route_id(a, t)).down, s_q8 + t * nbr * 292, nbr, r0, r1, 0, 1,
                                  s_grid_r,
                                  *reinterpret_cast<FoldLDS<TYR> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>()),
                                  s_y + t * ystride);
