@@ -33,14 +33,40 @@ __device__ __forceinline__ int route_n(const MoeArgs &a) { return a.route_dev ? 
 __device__ __forceinline__ uint32_t route_id(const MoeArgs &a, int s) {
     return a.route_dev ? a.route_dev->ids[s] : a.route.ids[s];
 }
-// Views of the routed expert in routing slot s (expert id e): from the
-// arguments when the host gave the routing, else from the device table.
-__device__ __forceinline__ ExpertDev routed_view(const MoeArgs &a, int s, uint32_t e) {
-    if (!a.routed_given) return a.experts[e];
+// A matrix view the compiler may treat as divergent (read from LDS or
+// indexed by a wave-dependent slot) but that is the same in every lane of
+// the wave: take lane 0's copy, so the buffer descriptor built from it lives
+// in SGPRs (a divergent descriptor turns every load into a readfirstlane
+// loop).
+// (readfirstlane returns a signed int: each half goes through uint32_t so
+// the low half does not sign-extend into the high one.)
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t v) {
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    return ((uint64_t)hi << 32) | (uint64_t)lo;
+}
+__device__ __forceinline__ MatView uniform_view(const MatView &v) {
+    MatView u;
+    u.planes = reinterpret_cast<const uint8_t *>(uniform_u64(reinterpret_cast<uint64_t>(v.planes)));
+    u.type = __builtin_amdgcn_readfirstlane(v.type);
+    u.nb = __builtin_amdgcn_readfirstlane(v.nb);
+    u.rows = __builtin_amdgcn_readfirstlane(v.rows);
+    u.pad = 0;
+    u.units = (long long)uniform_u64((uint64_t)v.units);
+    u.bytes = (long long)uniform_u64((uint64_t)v.bytes);
+    return u;
+}
+
+// Views of the routed expert in routing slot s (wave-uniform): from the
+// arguments when the host gave the routing (scalar loads of the argument
+// segment), else from the device table.
+__device__ __forceinline__ ExpertDev routed_view(const MoeArgs &a, int s) {
+    const int su = __builtin_amdgcn_readfirstlane(s);
+    if (!a.routed_given) return a.experts[__builtin_amdgcn_readfirstlane((int)route_id(a, su))];
     ExpertDev v = a.routed_shape;
-    v.gate.planes = a.routed_planes[s][0];
-    v.up.planes = a.routed_planes[s][1];
-    v.down.planes = a.routed_planes[s][2];
+    v.gate.planes = a.routed_planes[su][0];
+    v.up.planes = a.routed_planes[su][1];
+    v.down.planes = a.routed_planes[su][2];
     return v;
 }
 __device__ __forceinline__ float route_coef(const MoeArgs &a, int s) {
@@ -77,9 +103,9 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
         const int m = it / per, j = it - m * per;
         const int r = j * L.rpw + L.slot;
         if (!(L.lane_on && r < rows)) return;
-        const ExpertDev &E = slot_of(m);
-        const Planes PG = make_planes(E.gate.planes, E.gate.units, E.gate.bytes);
-        const Planes PU = make_planes(E.up.planes, E.up.units, E.up.bytes);
+        const MatView VG = uniform_view(slot_of(m).gate), VU = uniform_view(slot_of(m).up);
+        const Planes PG = make_planes(VG.planes, VG.units, VG.bytes);
+        const Planes PU = make_planes(VU.planes, VU.units, VU.bytes);
         const uint32_t po = part_offset<TY, LPU>(PG, L.part);
         const uint32_t u = (uint32_t)(r * NB + L.b);
         load_slice(PG, u, po, L.part, wg);
@@ -99,9 +125,9 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
         const int m = itc / per, j = itc - m * per;
         int r = j * L.rpw + (L.lane_on ? L.slot : L.rpw - 1);
         r = r < rows ? r : rows - 1;
-        const ExpertDev &E = slot_of(m);
-        const Planes PG = make_planes(E.gate.planes, E.gate.units, E.gate.bytes);
-        const Planes PU = make_planes(E.up.planes, E.up.units, E.up.bytes);
+        const MatView VG = uniform_view(slot_of(m).gate), VU = uniform_view(slot_of(m).up);
+        const Planes PG = make_planes(VG.planes, VG.units, VG.bytes);
+        const Planes PU = make_planes(VU.planes, VU.units, VU.bytes);
         const uint32_t po = part_offset<TY, LPU>(PG, L.part);
         const uint32_t u = (uint32_t)(r * NB + L.b);
         load_slice(PG, u, po, L.part, ga);
@@ -149,6 +175,14 @@ struct RoutedSlots {
     __device__ int slot(int m) const { return m; }
     __device__ int order(int m) const { return m; }
 };
+// Host-given routing: the views come from the arguments per item (slot m is
+// wave-uniform), with no staging of ids or views in the prologue.
+struct GivenSlots {
+    const MoeArgs &a;
+    __device__ ExpertDev operator()(int m) const { return routed_view(a, m); }
+    __device__ int slot(int m) const { return m; }
+    __device__ int order(int m) const { return m; }
+};
 struct SharedSlot {
     const MoeArgs &a;
     int n;
@@ -170,6 +204,12 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
         gate_up_stream<TYS, LPUS>(a, SharedSlot{a, n}, 1, a.ffn_s, blockIdx.x * MOE_WAVES, wg_s * MOE_WAVES, smem);
         return;
     }
+    const int wg_r = gridDim.x - wg_s;
+    if (a.routed_given) {
+        gate_up_stream<TYR, LPUR>(a, GivenSlots{a}, a.n_launch, a.ffn_r, (blockIdx.x - wg_s) * MOE_WAVES,
+                                  wg_r * MOE_WAVES, smem);
+        return;
+    }
     if (a.select_in_kernel) {
         // Every workgroup selects the same route from the finished logits;
         // workgroup wg_s publishes it for the down kernel.
@@ -187,9 +227,8 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
         s_ids[threadIdx.x] = route_id(a, threadIdx.x < route_n(a) ? threadIdx.x : 0);
     }
     __syncthreads();
-    if (threadIdx.x < a.n_launch) s_views[threadIdx.x] = routed_view(a, threadIdx.x, s_ids[threadIdx.x]);
+    if (threadIdx.x < a.n_launch) s_views[threadIdx.x] = a.experts[s_ids[threadIdx.x]];
     __syncthreads();
-    const int wg_r = gridDim.x - wg_s;
     gate_up_stream<TYR, LPUR>(a, RoutedSlots{s_views}, a.n_launch, a.ffn_r, (blockIdx.x - wg_s) * MOE_WAVES,
                               wg_r * MOE_WAVES, smem);
 }
@@ -215,10 +254,11 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_router_shared(MoeArgs a) {
 // lane per row accumulates them in the reference order
 //     y = ((0 + c_0 d_0) + c_1 d_1) + ... + 1.0 * d_shared   (moe.rs:141-146).
 template <int TY, int LPU>
-__device__ __forceinline__ void down_wave(const MatView &V, const uint8_t *q8, int nb, int r0, int r1, int first,
+__device__ __forceinline__ void down_wave(const MatView &Vd, const uint8_t *q8, int nb, int r0, int r1, int first,
                                           int stride, const void *s_grid, FoldLDS<TY> &fold, float *s_y) {
     const int lane = threadIdx.x & 63;
     const LaneMap<LPU> L(lane, nb);
+    const MatView V = uniform_view(Vd);
     const Planes P = make_planes(V.planes, V.units, V.bytes);
     const uint32_t po = part_offset<TY, LPU>(P, L.part);
     const int items = (r1 - r0 + L.rpw - 1) / L.rpw;
@@ -300,7 +340,7 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     const int tasks = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
     for (int t = wid; t < tasks; t += nw) {
         if (t < n) {
-            down_wave<TYR, LPUR>(routed_view(a, t, route_id(a, t)).down, s_q8 + t * nbr * 292, nbr, r0, r1, 0, 1,
+            down_wave<TYR, LPUR>(routed_view(a, t).down, s_q8 + t * nbr * 292, nbr, r0, r1, 0, 1,
                                  s_grid_r,
                                  *reinterpret_cast<FoldLDS<TYR> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>()),
                                  s_y + t * ystride);
