@@ -100,6 +100,31 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
     }
 }
 
+// Maximum of a 32-bit value over the wave, returned in every lane (uniform):
+// DPP steps (quad butterflies, half-row and row mirrors, then the row 15 and
+// row 31 broadcasts) leave the maximum in lane 63, read back as a scalar.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_max_step(uint32_t v) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xf, false);
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = dpp_max_step<0xB1, 0xf>(v);    // quad_perm [1, 0, 3, 2]
+    v = dpp_max_step<0x4E, 0xf>(v);    // quad_perm [2, 3, 0, 1]
+    v = dpp_max_step<0x141, 0xf>(v);   // row_half_mirror
+    v = dpp_max_step<0x140, 0xf>(v);   // row_mirror
+    v = dpp_max_step<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v = dpp_max_step<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+// The 64-bit key maximum as two 32-bit passes: the high words, then the low
+// words of the lanes that hold that high word.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+    const uint32_t hi = wave_max_u32((uint32_t)(v >> 32));
+    const uint32_t lo = wave_max_u32((uint32_t)(v >> 32) == hi ? (uint32_t)v : 0u);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 // Called by all 64 lanes of one wave; every lane returns the same route.
 // bad: ~0 when valid, else (first invalid expert << 2) | field
 // (0 logit, 1 bias, 2 selection score: the checks of routing.rs:72-77).
@@ -107,18 +132,27 @@ __device__ __forceinline__ void select_route(const RouterArgs &a, MoeRoute &out,
     const int lane = threadIdx.x & 63;
     constexpr int SLOTS = 4;   // up to 256 experts
     unsigned long long key[SLOTS];
-    float weight[SLOTS];
+    float weight[SLOTS], logit[SLOTS], bias[SLOTS];
     bad = ~0ull;
+    // Every load first (row clamped into the table), so they share one round
+    // trip instead of one per slot behind the slot's branches.
+#pragma unroll
+    for (int k = 0; k < SLOTS; ++k) {
+        const int e = lane + 64 * k;
+        const int ec = e < a.n_experts ? e : a.n_experts - 1;
+        logit[k] = a.logits[ec];
+        bias[k] = a.mode == 1 ? a.bias[ec] : 0.0f;
+    }
 #pragma unroll
     for (int k = 0; k < SLOTS; ++k) {
         const int e = lane + 64 * k;
         key[k] = 0;
         weight[k] = 0.0f;
         if (e < a.n_experts) {
-            const float l = a.logits[e];
+            const float l = logit[k];
             float score = l;
             if (a.mode == 1) {
-                const float b = a.bias[e];
+                const float b = bias[k];
                 const float w = sigmoid_ref(l);
                 score = __fadd_rn(w, b);
                 weight[k] = w;
@@ -143,22 +177,21 @@ __device__ __forceinline__ void select_route(const RouterArgs &a, MoeRoute &out,
         win_id[r] = 0, win_score[r] = 0.0f, win_w[r] = 0.0f;
         if (r >= a.top_k) continue;
         unsigned long long best = key[0];
-        int bk = 0;
 #pragma unroll
         for (int k = 1; k < SLOTS; ++k)
-            if (key[k] > best) best = key[k], bk = k;
-        unsigned long long m = best;
-        for (int off = 32; off >= 1; off >>= 1) {
-            const unsigned long long o = __shfl_xor(m, off, 64);
-            m = o > m ? o : m;
-        }
+            if (key[k] > best) best = key[k];
+        const unsigned long long m = wave_max_u64(best);   // uniform
         const uint32_t id = 0xffffffffu - (uint32_t)(m & 0xffffffffull);
         const int owner = (int)(id & 63);
         const int slot = (int)(id >> 6);
-        const float wv = __shfl(weight[bk], owner, 64);
+        // the winner's weight and logit, read from its owner lane
+        float wsel = weight[0], lsel = logit[0];
+#pragma unroll
+        for (int k = 1; k < SLOTS; ++k)
+            if (k == slot) wsel = weight[k], lsel = logit[k];
         win_id[r] = id;
-        win_w[r] = wv;
-        win_score[r] = a.mode == 1 ? 0.0f : a.logits[id];
+        win_w[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsel), owner));
+        win_score[r] = a.mode == 1 ? 0.0f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lsel), owner));
         if (lane == owner) {
 #pragma unroll
             for (int k = 0; k < SLOTS; ++k)
@@ -176,34 +209,50 @@ __device__ __forceinline__ void select_route(const RouterArgs &a, MoeRoute &out,
 #pragma unroll
         for (int r = 0; r < MOE_MAX_ROUTED; ++r) coef[r] = __fmul_rn(__fdiv_rn(win_w[r], wsum), a.weight_scale);
     } else {
+        // Lane r evaluates the exponential of winner r (the values are uniform,
+        // so one call per lane in parallel instead of sixteen dependent table
+        // reads in one lane), then the sum runs in rank order as before.
         const float mx = win_score[0];
+        float in = 0.0f;
+#pragma unroll
+        for (int r = 0; r < MOE_MAX_ROUTED; ++r)
+            if (lane == r) in = __fsub_rn(win_score[r], mx);
+        const float ev_lane = expf_libm(in);
         float ev[MOE_MAX_ROUTED];
         float s = 0.0f;
 #pragma unroll
         for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
-            ev[r] = expf_libm(__fsub_rn(win_score[r], mx));
+            ev[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ev_lane), r));
             if (r < a.top_k) s = __fadd_rn(s, ev[r]);
         }
+        const float coef_lane = __fdiv_rn(ev_lane, s);
 #pragma unroll
-        for (int r = 0; r < MOE_MAX_ROUTED; ++r) coef[r] = __fdiv_rn(ev[r], s);
+        for (int r = 0; r < MOE_MAX_ROUTED; ++r)
+            coef[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(coef_lane), r));
     }
-    // Output ascending by id (routing.rs:105): position = winners with a smaller id.
+    // Output ascending by id (routing.rs:105): position = winners with a
+    // smaller id.  Lane r holds winner r and counts its position; position q
+    // is then read from the lane that holds it.
     out.n = a.top_k;
     out.pad = 0;
+    uint32_t my_id = 0;
+    float my_coef = 0.0f;
 #pragma unroll
-    for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
-        out.ids[r] = 0;
-        out.coefs[r] = 0.0f;
-    }
+    for (int r = 0; r < MOE_MAX_ROUTED; ++r)
+        if (lane == r) my_id = win_id[r], my_coef = coef[r];
+    int pos = 0;
 #pragma unroll
-    for (int r = 0; r < MOE_MAX_ROUTED; ++r) {
-        if (r >= a.top_k) continue;
-        int pos = 0;
+    for (int q = 0; q < MOE_MAX_ROUTED; ++q) pos += (q < a.top_k && win_id[q] < my_id) ? 1 : 0;
+    const bool holds = lane < a.top_k;
 #pragma unroll
-        for (int q = 0; q < MOE_MAX_ROUTED; ++q) pos += (q < a.top_k && win_id[q] < win_id[r]) ? 1 : 0;
-#pragma unroll
-        for (int q = 0; q < MOE_MAX_ROUTED; ++q)
-            if (q == pos) out.ids[q] = win_id[r], out.coefs[q] = coef[r];
+    for (int q = 0; q < MOE_MAX_ROUTED; ++q) {
+        out.ids[q] = 0;
+        out.coefs[q] = 0.0f;
+        if (q >= a.top_k) continue;
+        const unsigned long long m = __ballot(holds && pos == q);
+        const int src = (int)__builtin_ctzll(m);
+        out.ids[q] = (uint32_t)__builtin_amdgcn_readlane((int)my_id, src);
+        out.coefs[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_coef), src));
     }
 }
 
