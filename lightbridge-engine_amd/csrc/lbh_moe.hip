@@ -314,22 +314,52 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     float *s_y = reinterpret_cast<float *>(s_foldp + nw * down_fold_bytes<TYR, TYS>());
     uint8_t *s_q8 = reinterpret_cast<uint8_t *>(s_y + (MOE_MAX_ROUTED + 1) * a.tile_d);   // [n * nbr + nbs] blocks
 
-    fill_grid<TYR>(s_grid_r);
-    if (TYS != TYR) fill_grid<TYS>(s_grid_s);
     // Q8_K of every expert's h into LDS (quantize_row_q8_k_into of the down
     // projection's input, gemv.rs:161-163): chunks of up to four blocks of one
-    // slot per wave step.
+    // slot.  Each wave loads the h of two chunks (and the codebook loads go
+    // out first) before quantizing either, so the prologue waits for one
+    // round trip instead of one per chunk; the second chunk's index is
+    // clamped (an in-range reload) so the loads are unconditional.
     {
+        const GridIn<TYR> gin_r = grid_load<TYR>();
+        const GridIn<TYS> gin_s = grid_load<TYS>();
         const int cr = (nbr + 3) / 4, cs = (nbs + 3) / 4;
         const int chunks = n * cr + (a.has_shared ? cs : 0);
-        for (int c = wid; c < chunks; c += nw) {
+        auto chunk = [&](int c, const float *&x, uint8_t *&out, int &b0, int &nbl) {
             if (c < n * cr) {
-                const int m = c / cr, b0 = 4 * (c - m * cr);
-                quantize_blocks_wave(a.h + (long long)m * a.h_stride, s_q8 + m * nbr * 292, b0, nbr);
+                const int m = c / cr;
+                b0 = 4 * (c - m * cr);
+                x = a.h + (long long)m * a.h_stride;
+                out = s_q8 + m * nbr * 292;
+                nbl = nbr;
             } else {
-                const int b0 = 4 * (c - n * cr);
-                quantize_blocks_wave(a.h + (long long)MOE_SHARED_SLOT * a.h_stride, s_q8 + n * nbr * 292, b0, nbs);
+                b0 = 4 * (c - n * cr);
+                x = a.h + (long long)MOE_SHARED_SLOT * a.h_stride;
+                out = s_q8 + n * nbr * 292;
+                nbl = nbs;
             }
+        };
+        bool first = true;
+        for (int c = wid; c < chunks; c += 2 * nw) {
+            const float *x0, *x1;
+            uint8_t *o0, *o1;
+            int b0, b1, n0, n1;
+            const int c1 = c + nw;
+            chunk(c, x0, o0, b0, n0);
+            chunk(c1 < chunks ? c1 : c, x1, o1, b1, n1);
+            const QuantIn q0 = quantize_load(x0, b0, n0);
+            const QuantIn q1 = quantize_load(x1, b1, n1);
+            if (first) {
+                grid_store<TYR>(gin_r, s_grid_r);
+                if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
+                first = false;
+            }
+            quantize_store(q0, o0);
+            if (c1 < chunks) quantize_store(q1, o1);
+        }
+        if (first) {   // a wave without chunks still stores its share of the codebooks
+            grid_store<TYR>(gin_r, s_grid_r);
+            if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
         }
     }
     __syncthreads();
