@@ -9,6 +9,8 @@ divided by the step time, in GB/s.
 
 Secondary workloads in the same JSON line:
   configs[0]  Q4_K x Q8_K matvec 4096x4096 (the reference's CPU-runnable case);
+  model_matvecs  the same fused matvec at the Hy3 model's attention, dense-FFN and
+              output-head shapes (up to the 340 MB Q5_K output head);
   configs[2]  the full MoE FFN block of one token: 192 routed experts (IQ2_S
               gate/up 1536x4096, IQ3_S down 4096x1536), top-8 of an F32 4096x192
               router with softmax weights, a Q4_K/Q5_K shared expert with ffn
@@ -243,6 +245,39 @@ def bench_q4k(args, be, timer, torch, np, synth):
     return w, {"workload": "configs[0]: Q4_K x Q8_K matvec 4096x4096, batch 1 (fused Q8_K + matvec kernel)",
                "us_per_matvec": round(us, 3), "GB/s": round(Q4K_BYTES / us / 1e3, 2),
                "roofline_frac": round(Q4K_BYTES / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies}
+
+
+# Decode matvecs of the Hy3 model's own tensors (crates/bridge-model-hy3/src/schema.rs:96-201,
+# sizes from profile.rs:17-44): (name, type, rows, K).
+MODEL_SHAPES = [("attn_q IQ2_S 8192x4096", 22, 8192, 4096), ("attn_k IQ2_S 1024x4096", 22, 1024, 4096),
+                ("attn_v Q4_K 1024x4096", 12, 1024, 4096), ("attn_output IQ3_S 4096x8192", 21, 4096, 8192),
+                ("dense_gate IQ2_S 13312x4096", 22, 13312, 4096), ("dense_down IQ3_S 4096x13312", 21, 4096, 13312),
+                ("output Q5_K 120832x4096", 13, 120832, 4096)]
+
+
+def bench_model_shapes(args, be, timer, torch, np, synth):
+    """One fused Q8_K + matvec launch per shape, > 600 MB of weight copies in rotation."""
+    out = {}
+    for name, ty, rows, k in MODEL_SHAPES:
+        w = synth.random_matrix(ty, rows, k, seed=rows + k)
+        copies = max(2, math.ceil(600e6 / w.nbytes))
+        wd = torch.from_numpy(w.reshape(-1)).cuda()
+        ms = [be.upload(ty, rows, k, wd) for _ in range(copies)]
+        del wd
+        xs = torch.randn(copies, k, device="cuda")
+        ys = torch.zeros(copies, rows, device="cuda")
+        g = timer.graph(lambda: [be.gemv_f32(ms[c], xs[c], ys[c]) for c in range(copies)])
+        reps = max(3, min(400, int(0.25 / (copies * w.nbytes / 5e12))))
+        timer.time(g, 2)
+        us = timer.time(g, reps) / (reps * copies) * 1e6
+        alg = w.nbytes + Q8(k) + 4 * rows
+        out[name] = {"us": round(us, 3), "algorithmic_bytes": alg, "GB/s": round(alg / us / 1e3, 1),
+                     "roofline_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies}
+        for m in ms:
+            m.close()
+        del ms, xs, ys, g
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_moe(args, be, timer, torch, np, synth, lbhip):
@@ -556,6 +591,7 @@ def main():
 
     mv = bench_matvec_step(args, be, timer, torch, np, synth)
     w_q4k, q4k = bench_q4k(args, be, timer, torch, np, synth)
+    model_mv = bench_model_shapes(args, be, timer, torch, np, synth)
     moe = state = batch = batch_check = None
     prefill, pf_check = bench_prefill(args, be, timer, torch, np, synth)
     if not args.no_moe:
@@ -592,6 +628,8 @@ def main():
                      "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2]},
         "kernels_us": {"iq2s_gate": round(mv["gate_us"], 3), "iq3s_down": round(mv["down_us"], 3)},
         "q4k_matvec": q4k,
+        "model_matvecs": {"workload": "decode matvecs (fused Q8_K + matvec, batch 1) at the Hy3 model's tensor shapes "
+                                      "and types (schema.rs:96-201)", "shapes": model_mv},
         "prefill_gemm": prefill,
     }
     if moe is not None:

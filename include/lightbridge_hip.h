@@ -103,7 +103,7 @@ lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream);
  * its thread count, CpuBackendConfig, lib.rs:7-17).  value 0 restores the default. */
 enum lbh_tuning_key {
     LBH_TUNE_GEMV_LPU = 1,         /* lanes per (row, block) unit: 1, 2 or 4 */
-    LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop */
+    LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop (0: resident x CUs) */
     LBH_TUNE_GEMM_SHAPE = 3,       /* K-quant GEMM tile staging: 0 = through registers, two blocks ahead;
                                       1 = direct buffer-to-LDS loads, one block ahead */
     LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 2, 3 or 4 */

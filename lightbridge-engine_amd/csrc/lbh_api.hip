@@ -152,7 +152,8 @@ lbh_status lbh_ctx_create(int32_t device, void *stream, lbh_ctx **out, lbh_error
     c->device = device;
     c->cu_count = prop.multiProcessorCount;
     c->tuning.lpu = 0;
-    c->tuning.max_blocks = 8 * prop.multiProcessorCount;
+    c->tuning.max_blocks = 0;
+    c->tuning.cu_count = prop.multiProcessorCount;
     c->stream = static_cast<hipStream_t>(stream);
     hipError_t e = hipMalloc(&c->status, sizeof(DevStatus));
     if (e == hipSuccess) e = hipHostMalloc(&c->status_host, sizeof(DevStatus), hipHostMallocDefault);
@@ -192,7 +193,7 @@ lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
         return LBH_OK;
     case LBH_TUNE_GEMV_MAX_BLOCKS:
         if (value < 0) return LBH_INVALID_PARAMETER;
-        ctx->tuning.max_blocks = value ? value : 8 * ctx->cu_count;
+        ctx->tuning.max_blocks = value;
         return LBH_OK;
     case LBH_TUNE_GEMV_DEPTH:
         if (value < 0 || value == 1 || value > 4) return LBH_INVALID_PARAMETER;

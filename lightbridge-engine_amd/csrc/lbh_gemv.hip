@@ -11,6 +11,8 @@
 // LDS.  With FUSEQ the kernel also performs the Q8_K quantization of the f32
 // input itself (each workgroup quantizes into LDS; workgroup 0 publishes the
 // bytes), which removes a launch from every gemv_into.
+#include <atomic>
+
 #include "lbh_internal.h"
 #include "lbh_rows.h"
 
@@ -114,61 +116,84 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
 
 static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
-template <int TY, int LPU, int D>
-static hipError_t launch_depth(const GemvArgs &a, int grid, hipStream_t s) {
-    if (a.x)
-        hipLaunchKernelGGL((k_gemv<TY, LPU, true, D>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
-    else
-        hipLaunchKernelGGL((k_gemv<TY, LPU, false, D>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
-    return hipGetLastError();
+// Workgroups of one kernel instance that fit on a CU at once (register and LDS
+// limited), queried once per instance.
+template <int TY, int LPU, bool FUSEQ, int D>
+static int resident_per_cu() {
+    static std::atomic<int> cached{0};
+    int n = cached.load(std::memory_order_relaxed);
+    if (n == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv<TY, LPU, FUSEQ, D>, GEMV_THREADS, 0) != hipSuccess ||
+            n < 1)
+            n = 1;
+        cached.store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
-template <int TY, int LPU>
-static hipError_t launch_typed(const GemvArgs &a, int max_blocks, int depth, hipStream_t s) {
+// Grid: one workgroup per GEMV_WAVES wave steps, capped at `max_blocks`, or,
+// when that is 0, at the workgroups resident on the device at once: a
+// persistent grid pays the prologue (codebook and activation staging) once per
+// resident workgroup instead of once per later wave of workgroups.
+template <int TY, int LPU, bool FUSEQ, int D>
+static hipError_t launch_inst(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
     const int rpw = (64 / LPU) / a.m.nb;
     const int items = cdiv(a.m.rows, rpw);
     int grid = cdiv(items, GEMV_WAVES);
-    if (max_blocks > 0 && grid > max_blocks) grid = max_blocks;
+    const int cap = t.max_blocks > 0 ? t.max_blocks : resident_per_cu<TY, LPU, FUSEQ, D>() * t.cu_count;
+    if (cap > 0 && grid > cap) grid = cap;
+    hipLaunchKernelGGL((k_gemv<TY, LPU, FUSEQ, D>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int TY, int LPU, int D>
+static hipError_t launch_depth(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
+    return a.x ? launch_inst<TY, LPU, true, D>(a, t, s) : launch_inst<TY, LPU, false, D>(a, t, s);
+}
+
+template <int TY, int LPU>
+static hipError_t launch_typed(const GemvArgs &a, const GemvTuning &t, int depth, hipStream_t s) {
     switch (depth) {
-    case 4: return launch_depth<TY, LPU, 4>(a, grid, s);
-    case 3: return launch_depth<TY, LPU, 3>(a, grid, s);
-    default: return launch_depth<TY, LPU, 2>(a, grid, s);
+    case 4: return launch_depth<TY, LPU, 4>(a, t, s);
+    case 3: return launch_depth<TY, LPU, 3>(a, t, s);
+    default: return launch_depth<TY, LPU, 2>(a, t, s);
     }
 }
 
 template <int TY>
-static hipError_t launch_lpu(const GemvArgs &a, int lpu, int max_blocks, int depth, hipStream_t s) {
+static hipError_t launch_lpu(const GemvArgs &a, const GemvTuning &t, int lpu, int depth, hipStream_t s) {
     // A wave step must hold at least one whole row: NB * LPU <= 64.
     while (lpu > 1 && a.m.nb * lpu > 64) lpu >>= 1;
     switch (lpu) {
-    case 4: return launch_typed<TY, 4>(a, max_blocks, depth, s);
-    case 2: return launch_typed<TY, 2>(a, max_blocks, depth, s);
-    default: return launch_typed<TY, 1>(a, max_blocks, depth, s);
+    case 4: return launch_typed<TY, 4>(a, t, depth, s);
+    case 2: return launch_typed<TY, 2>(a, t, depth, s);
+    default: return launch_typed<TY, 1>(a, t, depth, s);
     }
 }
 
-// Built-in lanes-per-unit choice per type.
-static int default_lpu(int ty) {
-    switch (ty) {
-    case T_IQ2_S: return 2;
-    case T_IQ3_S: return 2;
-    case T_Q4_K: return 2;
-    case T_Q5_K: return 2;
-    default: return 1;
-    }
+// Built-in lanes-per-unit choice.  One lane per (row, block) unit reads each
+// block once with the fewest instructions, but holds a whole block of
+// activations in registers (two or three waves per SIMD); it is the faster
+// choice once the matrix gives every CU at least four such waves.  Smaller
+// matrices are latency-bound and gain from the shorter per-lane work of two
+// lanes per unit (measured on MI355X: Q4_K 4096x4096 6.0 vs 6.9 us at one and
+// two lanes; IQ2_S 1536x4096 5.4 vs 5.8 us at two and one).
+static int default_lpu(const GemvArgs &a, int cu_count) {
+    const long long units = (long long)a.m.rows * a.m.nb;
+    return units >= 64LL * 4 * (cu_count > 0 ? cu_count : 256) ? 1 : 2;
 }
 
 hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
     const int nb = a.m.nb;
     if (nb < 1 || nb > MAX_NB || a.m.rows < 1) return hipErrorInvalidValue;
     if (!a.q8 && !a.x) return hipErrorInvalidValue;
-    const int lpu = t.lpu > 0 ? t.lpu : default_lpu(a.m.type);
+    const int lpu = t.lpu > 0 ? t.lpu : default_lpu(a, t.cu_count);
     const int depth = t.depth > 0 ? t.depth : 2;
     switch (a.m.type) {
-    case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, lpu, t.max_blocks, depth, s);
-    case T_IQ3_S: return launch_lpu<T_IQ3_S>(a, lpu, t.max_blocks, depth, s);
-    case T_Q4_K: return launch_lpu<T_Q4_K>(a, lpu, t.max_blocks, depth, s);
-    case T_Q5_K: return launch_lpu<T_Q5_K>(a, lpu, t.max_blocks, depth, s);
+    case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, t, lpu, depth, s);
+    case T_IQ3_S: return launch_lpu<T_IQ3_S>(a, t, lpu, depth, s);
+    case T_Q4_K: return launch_lpu<T_Q4_K>(a, t, lpu, depth, s);
+    case T_Q5_K: return launch_lpu<T_Q5_K>(a, t, lpu, depth, s);
     default: return hipErrorInvalidValue;
     }
 }

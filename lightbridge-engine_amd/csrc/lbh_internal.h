@@ -43,8 +43,9 @@ struct GemvArgs {
 // Launch-shape knobs of the matvec kernels (0 = built-in default).
 struct GemvTuning {
     int lpu;          // lanes per (row, block) unit: 1, 2 or 4
-    int max_blocks;   // cap on workgroups of the persistent row loop
+    int max_blocks;   // cap on workgroups of the persistent row loop (0: resident occupancy x CUs)
     int depth;        // row steps in flight per wave (2..4)
+    int cu_count;     // compute units of the device (sizes the default grid)
 };
 
 // ---------------------------------------------------------------- MoE block
