@@ -305,6 +305,103 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *router, const float *
 lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev, size_t top_k,
                                  int32_t mode, float weight_scale, float *y_dev);
 
+/* ---- HBM expert cache ---------------------------------------------------------
+ * Counterpart of CompressedCache<ExpertKey> (crates/bridge-cache/src/lib.rs:32-595)
+ * as the runtime uses it for routed experts (crates/bridge-runtime/src/hy3_scalar.rs:
+ * 456-459, 575-604): a fixed byte ceiling, pins held by leases, LRU eviction of
+ * unpinned entries, admission after `admit_after_requests` misses of a key
+ * (below it an entry is ephemeral: dropped when its last lease is released),
+ * concurrent misses of one key deduplicated.  Entries live in HBM in the device
+ * layout, one fixed-size slot per expert.  A miss calls the caller's loader,
+ * which writes the expert's tight record (gate | up | down GGML bytes: the
+ * record of an expert-major sidecar, crates/bridge-format/src/lib.rs:63-100, read
+ * by Sidecar::read_expert :309-329) straight into pinned staging; the record is
+ * DMA'd and repacked on the cache's copy stream.  Thread-safe. */
+typedef struct lbh_expert_cache lbh_expert_cache;
+
+/* CacheConfig (lib.rs:13-30). */
+typedef struct lbh_expert_cache_config {
+    uint64_t capacity_bytes;
+    uint64_t admit_after_requests;
+} lbh_expert_cache_config;
+
+/* CacheStats (lib.rs:480-494), plus the slot geometry and bytes DMA'd. */
+typedef struct lbh_cache_stats {
+    uint64_t capacity_bytes, used_bytes, reserved_bytes;
+    uint64_t resident_entries, pinned_entries, loading_entries, heat_entries;
+    uint64_t hits, misses, loads, waits, evictions;
+    uint64_t entry_bytes, slots, bytes_uploaded;
+} lbh_cache_stats;
+
+/* A pinned entry (CacheLease, lib.rs:396-443): release it exactly once. */
+typedef struct lbh_expert_lease {
+    uint32_t layer, expert;
+    int32_t slot;
+    int32_t reserved;
+} lbh_expert_lease;
+
+/* Loader of one tight record (the closure given to get_or_try_insert, lib.rs:129-265):
+ * writes the record into dst (capacity `bytes`), sets *written to the length
+ * written, returns 0 on success or a loader-specific non-zero code. */
+typedef int32_t (*lbh_expert_loader)(void *user, uint32_t layer, uint32_t expert, uint8_t *dst, size_t bytes,
+                                     size_t *written);
+
+/* CacheError status codes (lib.rs:496-516) and LoadError::Loader (lib.rs:518-524). */
+#define LBH_CACHE_ZERO_CAPACITY 30            /* ZeroCapacity */
+#define LBH_CACHE_ZERO_ADMISSION_THRESHOLD 31 /* ZeroAdmissionThreshold */
+#define LBH_CACHE_ENTRY_TOO_LARGE 32          /* EntryTooLarge { requested = expected, capacity = actual } */
+#define LBH_CACHE_CAPACITY_PINNED 33          /* CapacityPinned { requested = expected } */
+#define LBH_CACHE_LOADED_SIZE_MISMATCH 34     /* LoadedSizeMismatch { expected, actual } */
+#define LBH_CACHE_LOADER_FAILED 35            /* LoadError::Loader: the loader's code in `actual` */
+
+/* CompressedCache::new (lib.rs:75-99) for the routed experts of one shape:
+ * gate/up [ffn x hidden] of gate_up_type, down [hidden x ffn] of down_type.
+ * Allocates capacity_bytes / entry_bytes slots in HBM (entry_bytes = the tight
+ * record length) and two pinned staging buffers. */
+lbh_status lbh_expert_cache_create(lbh_ctx *ctx, const lbh_expert_cache_config *config, uint32_t hidden, uint32_t ffn,
+                                   int32_t gate_up_type, int32_t down_type, lbh_expert_cache **out, lbh_error *err);
+lbh_status lbh_expert_cache_destroy(lbh_expert_cache *cache);
+/* Tight record length of one expert: the `expected_bytes` of every load. */
+uint64_t lbh_expert_cache_entry_bytes(const lbh_expert_cache *cache);
+
+/* get_or_try_insert (lib.rs:129-265): a hit pins the entry; a miss reserves a slot
+ * (evicting least recently used unpinned entries; LBH_CACHE_CAPACITY_PINNED when
+ * pins block it, before the loader runs), calls the loader, checks the length and
+ * every f16 d / dmin (LBH_NON_FINITE_SCALE with the block, field, bits and row,
+ * `expected` = 0 gate / 1 up / 2 down), then uploads on the copy stream.  A
+ * concurrent miss of the same key waits for the first one.  On any error the
+ * reservation is released and nothing is inserted.  Work that reads the entry is
+ * ordered after its upload by lbh_moe_forward_leased. */
+lbh_status lbh_expert_cache_get_or_load(lbh_expert_cache *cache, uint32_t layer, uint32_t expert,
+                                        lbh_expert_loader loader, void *user, lbh_expert_lease *out,
+                                        lbh_error *err);
+/* get (lib.rs:101-127): pins a ready entry (*found = 1) or counts a miss (*found = 0). */
+lbh_status lbh_expert_cache_get(lbh_expert_cache *cache, uint32_t layer, uint32_t expert, lbh_expert_lease *out,
+                                int32_t *found);
+/* Drop of CacheLease (lib.rs:419-443): unpins; an ephemeral entry whose last pin
+ * goes is removed.  The slot is not reused before the work the context's stream
+ * holds at this call has finished. */
+lbh_status lbh_expert_cache_release(lbh_expert_cache *cache, lbh_expert_lease *lease);
+/* stats (lib.rs:267-299) and clear_unpinned (lib.rs:301-322). */
+lbh_status lbh_expert_cache_stats(lbh_expert_cache *cache, lbh_cache_stats *out);
+lbh_status lbh_expert_cache_clear_unpinned(lbh_expert_cache *cache, uint64_t *removed);
+/* [sync] The leased entry's tight record read back from HBM (inverse of the repack):
+ * byte-identical to what the loader wrote. */
+lbh_status lbh_expert_cache_read_record(lbh_expert_cache *cache, const lbh_expert_lease *lease, void *host_out,
+                                        size_t bytes, lbh_error *err);
+
+/* A MoE layer whose routed experts come from `cache` (same hidden / ffn / types)
+ * and whose shared expert (optional) is resident: the runtime's streaming MoE
+ * (hy3_scalar.rs:561-626).  Only lbh_moe_forward_leased computes with it. */
+lbh_status lbh_moe_create_cached(lbh_ctx *ctx, lbh_expert_cache *cache, const lbh_matrix *shared_gate,
+                                 const lbh_matrix *shared_up, const lbh_matrix *shared_down, lbh_moe **out,
+                                 lbh_error *err);
+/* [async] lbh_moe_forward over leased experts: leases[i] is routed expert i (ascending
+ * expert ids, distinct, n_routed <= 16) with coefficient coefs[i]; the computation
+ * waits on the copy stream for each entry's upload. */
+lbh_status lbh_moe_forward_leased(lbh_ctx *ctx, lbh_moe *moe, const lbh_expert_lease *leases, const float *coefs,
+                                  size_t n_routed, const float *x_dev, float *y_dev);
+
 /* ---- diagnostics ------------------------------------------------------------- */
 
 /* [sync] The device expf used by SwiGLU and the routers (swiglu == 0), or the

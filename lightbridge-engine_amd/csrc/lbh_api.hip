@@ -12,79 +12,14 @@
 #include <new>
 
 #include "../../include/lightbridge_hip.h"
+#include "lbh_cache.h"
+#include "lbh_host.h"
 #include "lbh_internal.h"
 #include "lbh_math.h"
 
 using namespace lbh;
 
-struct lbh_ctx {
-    int device;
-    int cu_count;
-    hipStream_t stream;
-    DevStatus *status;        // device
-    DevStatus *status_host;   // pinned mirror
-    GemvTuning tuning;
-    int gemm_shape;           // K-quant GEMM staging (0: registers, two blocks ahead; 1: direct to LDS)
-};
-
-struct lbh_matrix {
-    int device;
-    int32_t type;
-    size_t rows, k, nb;
-    uint8_t *planes;
-    size_t bytes;
-    uint8_t *gemm_a;     // MFMA-ready copy for token batches (lbh_matrix_prepare_gemm), or NULL
-};
-
 namespace {
-
-lbh_status fail(lbh_error *err, lbh_status st, int ty = 0, uint64_t index = 0, uint64_t expected = 0,
-                uint64_t actual = 0, uint32_t bits = 0, uint32_t field = 0, uint64_t row = 0) {
-    if (err) {
-        std::memset(err, 0, sizeof(*err));
-        err->status = st;
-        err->ty = ty;
-        err->index = index;
-        err->expected = expected;
-        err->actual = actual;
-        err->bits = bits;
-        err->field = field;
-        err->row = row;
-    }
-    return st;
-}
-
-lbh_status hip_fail(lbh_error *err, hipError_t e) {
-    lbh_status st = fail(err, LBH_HIP_ERROR);
-    if (err) err->hip_error = (int32_t)e;
-    return st;
-}
-
-#define HIP_TRY(expr)                              \
-    do {                                           \
-        hipError_t e_ = (expr);                    \
-        if (e_ != hipSuccess) return hip_fail(err, e_); \
-    } while (0)
-
-lbh_status ok(lbh_error *err) {
-    if (err) {
-        std::memset(err, 0, sizeof(*err));
-        err->status = LBH_OK;
-    }
-    return LBH_OK;
-}
-
-struct DeviceGuard {
-    int prev = -1;
-    explicit DeviceGuard(int dev) {
-        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-        if (prev != dev) (void)hipSetDevice(dev);
-    }
-    ~DeviceGuard() {
-        int cur;
-        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
-    }
-};
 
 size_t block_bytes(int ty) { return (size_t)layout_of(ty).block_bytes; }
 
@@ -462,7 +397,8 @@ lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in, float *out, si
 
 struct lbh_moe {
     int device;
-    size_t n_experts, hidden, ffn_r, ffn_s;
+    size_t n_experts, hidden, ffn_r, ffn_s;   // n_experts = 0: routed experts come from `cache`
+    lbh_expert_cache *cache;
     int type_gate_r, type_down_r;
     ExpertDev *experts_dev;
     ExpertDev *experts_host;  // the same table on the host (host-given routing passes planes as arguments)
@@ -541,6 +477,90 @@ void set_routed_planes(MoeArgs &a, const lbh_moe *m, const uint32_t *ids, size_t
     }
 }
 
+// The layer object from validated routed views: `table` (owned) holds the
+// n_experts resident experts, or, when n_experts == 0, one entry with the
+// routed shape of `cache` (null planes).
+lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_expert_cache *cache, size_t hidden,
+                     size_t ffn_r, int tg, int td, size_t gate_bytes, const lbh_matrix *shared_gate,
+                     const lbh_matrix *shared_up, const lbh_matrix *shared_down, lbh_moe **out, lbh_error *err) {
+    const bool has_shared = shared_gate != nullptr;
+    size_t ffn_s = 0;
+    if (has_shared) {
+        ffn_s = shared_gate->rows;
+        if (shared_gate->k != hidden || shared_up->k != hidden || shared_up->rows != ffn_s ||
+            shared_up->type != shared_gate->type || shared_down->rows != hidden || shared_down->k != ffn_s) {
+            delete[] table;
+            return fail(err, LBH_DIMENSION_MISMATCH, shared_gate->type, n_experts, hidden, shared_gate->k);
+        }
+    }
+    if (!moe_types_supported(tg, has_shared ? shared_gate->type : tg, td, has_shared ? shared_down->type : td)) {
+        delete[] table;
+        return fail(err, LBH_UNSUPPORTED_TYPE, tg);
+    }
+    if (hidden / 256 > 64 || ffn_r / 256 > 64 || ffn_s / 256 > 64) {
+        delete[] table;
+        return fail(err, LBH_UNSUPPORTED_SHAPE);
+    }
+    DeviceGuard guard(ctx->device);
+    lbh_moe *m = new (std::nothrow) lbh_moe();
+    if (!m) {
+        delete[] table;
+        return fail(err, LBH_HIP_ERROR);
+    }
+    m->experts_host = table;
+    m->cache = cache;
+    m->device = ctx->device;
+    m->n_experts = n_experts;
+    m->hidden = hidden;
+    m->ffn_r = ffn_r;
+    m->ffn_s = ffn_s;
+    m->type_gate_r = tg;
+    m->type_down_r = td;
+    m->has_shared = has_shared;
+    if (has_shared) {
+        m->shared.gate = view_of(shared_gate);
+        m->shared.up = view_of(shared_up);
+        m->shared.down = view_of(shared_down);
+    }
+    // Gate/up workgroups (measured on the configs[2] shapes): two per CU for
+    // the routed stream, and for the shared stream its byte share of two per
+    // CU (the top-8 routed gate/up against the shared gate/up).  More routed
+    // workgroups slow the device-router path, where every routed workgroup
+    // selects the route from the logits in its prologue.
+    {
+        const double br = 8.0 * 2.0 * (double)gate_bytes;
+        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes : 0.0;
+        const int total = 2 * ctx->cu_count;
+        m->wg_s = has_shared ? (int)(total * bs / (br + bs) + 0.5) : 0;
+        if (has_shared && m->wg_s < 1) m->wg_s = 1;
+        m->wg_r = total;
+    }
+    m->tile_d = 16;
+    m->tc = 8;
+    m->rt_gu_r = 64;
+    m->rt_gu_s = 64;
+    m->rt_d_r = 160;
+    m->rt_d_s = 64;
+    const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
+    m->h_stride = (int)max_ffn;
+    const size_t slots = MOE_MAX_ROUTED + 1;
+    hipError_t e = hipSuccess;
+    if (n_experts > 0) {
+        e = hipMalloc(&m->experts_dev, n_experts * sizeof(ExpertDev));
+        if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
+    }
+    if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&m->status, sizeof(MoeStatus));
+    if (e == hipSuccess) e = hipHostMalloc(&m->status_host, sizeof(MoeStatus), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        free_moe(m);
+        return hip_fail(err, e);
+    }
+    *out = m;
+    return ok(err);
+}
+
 }  // namespace
 
 extern "C" {
@@ -567,77 +587,15 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
         if (g->device != ctx->device || u->device != ctx->device || d->device != ctx->device)
             return fail(err, LBH_INVALID_PARAMETER, 0, e);
     }
-    size_t ffn_s = 0;
-    if (has_shared) {
-        ffn_s = shared_gate->rows;
-        if (shared_gate->k != hidden || shared_up->k != hidden || shared_up->rows != ffn_s ||
-            shared_up->type != shared_gate->type || shared_down->rows != hidden || shared_down->k != ffn_s)
-            return fail(err, LBH_DIMENSION_MISMATCH, shared_gate->type, n_experts, hidden, shared_gate->k);
-    }
-    if (!moe_types_supported(tg, has_shared ? shared_gate->type : tg, td, has_shared ? shared_down->type : td))
-        return fail(err, LBH_UNSUPPORTED_TYPE, tg);
-    if (hidden / 256 > 64 || ffn_r / 256 > 64 || ffn_s / 256 > 64) return fail(err, LBH_UNSUPPORTED_SHAPE);
-    DeviceGuard guard(ctx->device);
-    lbh_moe *m = new (std::nothrow) lbh_moe();
-    if (!m) return fail(err, LBH_HIP_ERROR);
-    m->device = ctx->device;
-    m->n_experts = n_experts;
-    m->hidden = hidden;
-    m->ffn_r = ffn_r;
-    m->ffn_s = ffn_s;
-    m->type_gate_r = tg;
-    m->type_down_r = td;
-    m->has_shared = has_shared;
-    if (has_shared) {
-        m->shared.gate = view_of(shared_gate);
-        m->shared.up = view_of(shared_up);
-        m->shared.down = view_of(shared_down);
-    }
-    // Gate/up workgroups (measured on the configs[2] shapes): two per CU for
-    // the routed stream, and for the shared stream its byte share of two per
-    // CU (the top-8 routed gate/up against the shared gate/up).  More routed
-    // workgroups slow the device-router path, where every routed workgroup
-    // selects the route from the logits in its prologue.
-    {
-        const double br = 8.0 * 2.0 * (double)gate[0]->bytes;
-        const double bs = has_shared ? 2.0 * (double)shared_gate->bytes : 0.0;
-        const int total = 2 * ctx->cu_count;
-        m->wg_s = has_shared ? (int)(total * bs / (br + bs) + 0.5) : 0;
-        if (has_shared && m->wg_s < 1) m->wg_s = 1;
-        m->wg_r = total;
-    }
-    m->tile_d = 16;
-    m->tc = 8;
-    m->rt_gu_r = 64;
-    m->rt_gu_s = 64;
-    m->rt_d_r = 160;
-    m->rt_d_s = 64;
-    const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
-    m->h_stride = (int)max_ffn;
-    const size_t slots = MOE_MAX_ROUTED + 1;
     ExpertDev *table = new (std::nothrow) ExpertDev[n_experts];
-    if (!table) {
-        free_moe(m);
-        return fail(err, LBH_HIP_ERROR);
-    }
+    if (!table) return fail(err, LBH_HIP_ERROR);
     for (size_t e = 0; e < n_experts; ++e) {
         table[e].gate = view_of(gate[e]);
         table[e].up = view_of(up[e]);
         table[e].down = view_of(down[e]);
     }
-    m->experts_host = table;
-    hipError_t e = hipMalloc(&m->experts_dev, n_experts * sizeof(ExpertDev));
-    if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc(&m->status, sizeof(MoeStatus));
-    if (e == hipSuccess) e = hipHostMalloc(&m->status_host, sizeof(MoeStatus), hipHostMallocDefault);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-        free_moe(m);
-        return hip_fail(err, e);
-    }
-    *out = m;
-    return ok(err);
+    return build_moe(ctx, n_experts, table, nullptr, hidden, ffn_r, tg, td, gate[0]->bytes, shared_gate, shared_up,
+                     shared_down, out, err);
 }
 
 lbh_status lbh_moe_destroy(lbh_moe *m) {
@@ -670,6 +628,51 @@ lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const 
     a.n_launch = (int32_t)n_routed;
     set_routed_planes(a, m, ids, n_routed);
     DeviceGuard g(ctx->device);
+    if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_create_cached(lbh_ctx *ctx, lbh_expert_cache *cache, const lbh_matrix *shared_gate,
+                                 const lbh_matrix *shared_up, const lbh_matrix *shared_down, lbh_moe **out,
+                                 lbh_error *err) {
+    if (!ctx || !cache || !out) return fail(err, LBH_NULL_ARGUMENT);
+    *out = nullptr;
+    const bool has_shared = shared_gate || shared_up || shared_down;
+    if (has_shared && !(shared_gate && shared_up && shared_down)) return fail(err, LBH_NULL_ARGUMENT);
+    CacheShape sh;
+    cache_shape(cache, &sh);
+    if (sh.device != ctx->device) return fail(err, LBH_INVALID_PARAMETER);
+    ExpertDev *table = new (std::nothrow) ExpertDev[1];
+    if (!table) return fail(err, LBH_HIP_ERROR);
+    table[0] = sh.views;
+    return build_moe(ctx, 0, table, cache, sh.hidden, sh.ffn, sh.type_gate_up, sh.type_down,
+                     (size_t)sh.views.gate.bytes, shared_gate, shared_up, shared_down, out, err);
+}
+
+// The streaming MoE step of the runtime (hy3_scalar.rs:575-626): the routed
+// experts are the leased cache entries, in the caller's (ascending id) order.
+lbh_status lbh_moe_forward_leased(lbh_ctx *ctx, lbh_moe *m, const lbh_expert_lease *leases, const float *coefs,
+                                  size_t n_routed, const float *x, float *y) {
+    if (!ctx || !m || !leases || !coefs || !x || !y) return LBH_NULL_ARGUMENT;
+    if (!m->cache) return LBH_INVALID_PARAMETER;
+    if (n_routed == 0 || n_routed > MOE_MAX_ROUTED) return LBH_UNSUPPORTED_SHAPE;
+    MoeArgs a = moe_args(m, x, y);
+    a.route.n = (int32_t)n_routed;
+    a.routed_given = 1;
+    DeviceGuard g(ctx->device);
+    for (size_t i = 0; i < n_routed; ++i) {
+        if (i > 0 && leases[i].expert == leases[i - 1].expert) return LBH_DUPLICATE_ROUTED_EXPERT;   // moe.rs:94-105
+        if (i > 0 && leases[i].expert < leases[i - 1].expert) return LBH_ROUTED_EXPERT_ORDER;
+        const uint8_t *planes[3];
+        hipEvent_t ready;
+        if (!cache_lease_planes(m->cache, &leases[i], planes, &ready)) return LBH_INVALID_PARAMETER;
+        if (hipStreamWaitEvent(ctx->stream, ready, 0) != hipSuccess) return LBH_HIP_ERROR;
+        a.route.ids[i] = leases[i].expert;
+        a.route.coefs[i] = coefs[i];
+        for (int k = 0; k < 3; ++k) a.routed_planes[i][k] = planes[k];
+    }
+    a.n_launch = (int32_t)n_routed;
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;

@@ -119,6 +119,17 @@ def lib() -> C.CDLL:
             "lbh_moe_forward_batch": ([p, p, p, p, sz, sz, p, p], i32),
             "lbh_moe_routed_by_id_batch_into": ([p, p, p, p, sz, sz, p, sz, p, sz, E], i32),
             "lbh_route_experts_batch": ([p, p, sz, sz, sz, i32, C.c_float, p, p, p], i32),
+            "lbh_expert_cache_create": ([p, p, u32, u32, i32, i32, C.POINTER(p), E], i32),
+            "lbh_expert_cache_destroy": ([p], i32),
+            "lbh_expert_cache_entry_bytes": ([p], C.c_uint64),
+            "lbh_expert_cache_get_or_load": ([p, u32, u32, p, p, p, E], i32),
+            "lbh_expert_cache_get": ([p, u32, u32, p, p], i32),
+            "lbh_expert_cache_release": ([p, p], i32),
+            "lbh_expert_cache_stats": ([p, p], i32),
+            "lbh_expert_cache_clear_unpinned": ([p, p], i32),
+            "lbh_expert_cache_read_record": ([p, p, p, sz, E], i32),
+            "lbh_moe_create_cached": ([p, p, p, p, p, C.POINTER(p), E], i32),
+            "lbh_moe_forward_leased": ([p, p, p, p, sz, p, p], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
