@@ -71,6 +71,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on each CPU baseline sample")
     ap.add_argument("--lpu", type=int, default=0, help="matvec lanes per (row, block) unit (0 = library default)")
     ap.add_argument("--batch-reps", type=int, default=8, help="timed replays of the 8-step configs[3] graph")
+    ap.add_argument("--stream-tokens", type=int, default=48,
+                    help="tokens of the expert-streaming leg (sidecar -> HBM cache); 0 skips it")
     ap.add_argument("--pmc-workloads", action="store_true",
                     help="run a few dispatches of each workload for rocprofv3 --pmc passes and exit")
     return ap.parse_args()
@@ -369,6 +371,69 @@ def bench_batch(args, be, timer, torch, np, synth, state):
     return res, check
 
 
+def bench_streaming(args, be, torch, np, synth, lbhip, state):
+    """configs[2] decode with the routed experts streamed through the HBM expert
+    cache from an expert-major sidecar file (the reference runtime's streaming
+    MoE, crates/bridge-runtime/src/hy3_scalar.rs:561-626): per token, lease the
+    8 routed experts (a miss reads the record from the sidecar into pinned
+    staging, DMAs and repacks it on the copy stream), queue the leased forward,
+    release.  Wall clock over the tokens, host work and PCIe included."""
+    import shutil
+    import tempfile
+
+    from lbhip import sidecar as sc
+    from lbhip.cache import CachedMoeLayer, ExpertCache
+
+    tmp = Path(tempfile.mkdtemp(prefix="lbh_sidecar_"))
+    try:
+        names = ("IQ2_S", "IQ2_S", "IQ3_S")
+        sc.write_sidecar(tmp / "experts.sidecar", tmp / "experts.json",
+                         [(sc.ExpertKey(1, e), tuple(m.reshape(-1) for m in state["experts_np"][e]), names)
+                          for e in range(N_EXPERTS)], sc.FUSED_GATE_UP, 4096)
+        side = sc.Sidecar(tmp / "experts.sidecar", tmp / "experts.json")
+        logits = synth.zipf_routes(args.stream_tokens, N_EXPERTS, TOP_K, 1.1, seed=909)
+        routes = [np.sort(np.argsort(-logits[t], kind="stable")[:TOP_K]).astype(np.uint32)
+                  for t in range(args.stream_tokens)]
+        coefs = np.full(TOP_K, 1.0 / TOP_K, np.float32)
+        xs = torch.from_numpy(np.stack([synth.random_activations(HIDDEN, seed=950 + t)
+                                        for t in range(args.stream_tokens)])).cuda()
+        ys = torch.zeros(args.stream_tokens, HIDDEN, device="cuda")
+        out = {"workload": "configs[2] MoE block decode with the 192 routed experts streamed from an expert-major "
+                           "sidecar file through the HBM expert cache (Zipf(s=1.1) top-8 routes)",
+               "sidecar_bytes": side.manifest.sidecar["length"]}
+        for name, entries, admit, warm in (("cold_8_entries", 8, 1, False), ("zipf_32_entries", 32, 2, False),
+                                           ("warm_all_resident", N_EXPERTS, 1, True)):
+            cache = ExpertCache(be, entries * EXPERT_BYTES, admit, HIDDEN, FFN, synth.IQ2_S, synth.IQ3_S)
+            layer = CachedMoeLayer(be, cache, state["shared"])
+            load = lambda e: (lambda dst: side.read_into(sc.ExpertKey(1, e), dst))  # noqa: E731
+            if warm:
+                for e in range(N_EXPERTS):
+                    cache.get_or_try_insert(sc.ExpertKey(1, e), load(e), into=True).release()
+            torch.cuda.synchronize()
+            s0 = cache.stats()
+            t0 = time.perf_counter()
+            for t, ids in enumerate(routes):
+                leases = [cache.get_or_try_insert(sc.ExpertKey(1, int(e)), load(int(e)), into=True) for e in ids]
+                layer.forward_leased(leases, coefs, xs[t], ys[t])
+                for lease in leases:
+                    lease.release()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            s1 = cache.stats()
+            hits, misses = s1["hits"] - s0["hits"], s1["misses"] - s0["misses"]
+            up = s1["bytes_uploaded"] - s0["bytes_uploaded"]
+            out[name] = {"cache_entries": entries, "admit_after_requests": admit, "tokens": len(routes),
+                         "ms_per_token": round(dt / len(routes) * 1e3, 3), "tokens_per_s": round(len(routes) / dt, 1),
+                         "hit_rate": round(hits / max(1, hits + misses), 3), "bytes_uploaded": up,
+                         "upload_GB/s": round(up / dt / 1e9, 2)}
+            layer.close()
+            cache.close()
+        side.close()
+        return out
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def cpu_batch(experts_np, shared_np, check, seconds):
     """Oracle per token (the reference's token-serial loop) over the configs[3]
     batch's tokens and routes: moe_routed_by_id_into single pass."""
@@ -592,11 +657,13 @@ def main():
     mv = bench_matvec_step(args, be, timer, torch, np, synth)
     w_q4k, q4k = bench_q4k(args, be, timer, torch, np, synth)
     model_mv = bench_model_shapes(args, be, timer, torch, np, synth)
-    moe = state = batch = batch_check = None
+    moe = state = batch = batch_check = streaming = None
     prefill, pf_check = bench_prefill(args, be, timer, torch, np, synth)
     if not args.no_moe:
         moe, state = bench_moe(args, be, timer, torch, np, synth, lbhip)
         batch, batch_check = bench_batch(args, be, timer, torch, np, synth, state)
+        if args.stream_tokens > 0:
+            streaming = bench_streaming(args, be, torch, np, synth, lbhip, state)
 
     value = STEP_BYTES / (mv["ms_per_step"] * 1e-3) / 1e9
     if mv["down_us"] >= mv["gate_us"]:
@@ -635,6 +702,8 @@ def main():
     if moe is not None:
         line["moe_block"] = moe
         line["moe_batch"] = batch
+    if streaming is not None:
+        line["expert_streaming"] = streaming
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds)
         cq = cpu_q4k(w_q4k, args.cpu_seconds / 2)
