@@ -434,6 +434,42 @@ def bench_streaming(args, be, torch, np, synth, lbhip, state):
         shutil.rmtree(tmp, ignore_errors=True)
 
 
+def bench_ingest(args, be, torch, np, synth, lbhip):
+    """GGUF payload ingestion straight to HBM (SURVEY 8(f) row 4's path): the
+    Hy3 output head (Q5_K 120832x4096, 340 MB) in a GGUF file (page cache),
+    located by the directory reader and streamed through pinned 32 MiB chunks
+    with lbh_matrix_create_streamed, against lbh_matrix_create from host memory."""
+    import shutil
+    import tempfile
+
+    from lbhip import gguf as gg
+    rows, k = 120832, HIDDEN
+    w = synth.random_matrix(synth.Q5_K, rows, k, seed=77)
+    tmp = Path(tempfile.mkdtemp(prefix="lbh_gguf_"))
+    try:
+        path = tmp / "head.gguf"
+        gg.write_gguf(path, [("general.architecture", gg.STRING, "hy3")],
+                      [("output.weight", (k, rows), synth.Q5_K, w.tobytes())], alignment=4096)
+        gg.ingest(be, path)["output.weight"].close()   # warm the page cache and the code paths
+        t0 = time.perf_counter()
+        m = gg.ingest(be, path)["output.weight"]
+        t_stream = time.perf_counter() - t0
+        exact = bool(np.array_equal(m.read_ggml(), w.reshape(-1)))
+        m.close()
+        t0 = time.perf_counter()
+        m2 = be.upload(synth.Q5_K, rows, k, w)
+        t_host = time.perf_counter() - t0
+        m2.close()
+        return {"workload": "GGUF ingestion: Q5_K output head 120832x4096 (340 MB) from a GGUF file in the page "
+                            "cache to HBM (directory parse, positioned reads into pinned chunks, DMA, repack)",
+                "bytes": int(w.nbytes), "streamed_s": round(t_stream, 4),
+                "streamed_GB/s": round(w.nbytes / t_stream / 1e9, 2),
+                "from_host_memory_s": round(t_host, 4), "from_host_memory_GB/s": round(w.nbytes / t_host / 1e9, 2),
+                "read_back_bit_exact": exact}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+
 def cpu_batch(experts_np, shared_np, check, seconds):
     """Oracle per token (the reference's token-serial loop) over the configs[3]
     batch's tokens and routes: moe_routed_by_id_into single pass."""
@@ -657,6 +693,7 @@ def main():
     mv = bench_matvec_step(args, be, timer, torch, np, synth)
     w_q4k, q4k = bench_q4k(args, be, timer, torch, np, synth)
     model_mv = bench_model_shapes(args, be, timer, torch, np, synth)
+    ingest = bench_ingest(args, be, torch, np, synth, lbhip)
     moe = state = batch = batch_check = streaming = None
     prefill, pf_check = bench_prefill(args, be, timer, torch, np, synth)
     if not args.no_moe:
@@ -697,6 +734,7 @@ def main():
         "q4k_matvec": q4k,
         "model_matvecs": {"workload": "decode matvecs (fused Q8_K + matvec, batch 1) at the Hy3 model's tensor shapes "
                                       "and types (schema.rs:96-201)", "shapes": model_mv},
+        "gguf_ingest": ingest,
         "prefill_gemm": prefill,
     }
     if moe is not None:

@@ -138,6 +138,19 @@ lbh_status lbh_quantize_q8_k_rows(lbh_ctx *ctx, const float *input_dev, size_t r
 /* [sync] `bytes` is host memory when bytes_on_device == 0, device memory otherwise. */
 lbh_status lbh_matrix_create(lbh_ctx *ctx, int32_t ggml_type, size_t rows, size_t k, const void *bytes,
                              size_t byte_len, int32_t bytes_on_device, lbh_matrix **out, lbh_error *err);
+/* Reader of a tensor's GGML payload: writes `bytes` bytes starting at `offset`
+ * (relative to the tensor's first byte) into dst; returns 0 or a reader-specific
+ * non-zero code (reported as LBH_SOURCE_READ_FAILED with the code in `actual`). */
+typedef int32_t (*lbh_byte_reader)(void *user, uint64_t offset, uint8_t *dst, size_t bytes);
+#define LBH_SOURCE_READ_FAILED 36
+/* [sync] lbh_matrix_create for a tensor streamed from its source (a GGUF file's
+ * payload, crates/bridge-gguf/src/reader.rs:194-341 locates it) straight to HBM:
+ * the reader fills 32 MiB pinned chunks, each checked on the host (the
+ * validation of lbh_matrix_create, same error payload) and DMA'd and repacked
+ * while the next one is read; no host copy of the whole tensor and no device
+ * staging of it.  On error nothing is created. */
+lbh_status lbh_matrix_create_streamed(lbh_ctx *ctx, int32_t ggml_type, size_t rows, size_t k, lbh_byte_reader reader,
+                                      void *user, lbh_matrix **out, lbh_error *err);
 lbh_status lbh_matrix_destroy(lbh_matrix *m);
 /* [sync] Inverse of the device layout: writes the original GGML bytes to host memory. */
 lbh_status lbh_matrix_read_ggml(lbh_ctx *ctx, const lbh_matrix *m, void *host_bytes, size_t byte_len,

@@ -249,6 +249,102 @@ lbh_status lbh_matrix_create(lbh_ctx *ctx, int32_t ty, size_t rows, size_t k, co
     return ok(err);
 }
 
+// Tensor bytes pulled through the caller's reader in chunks of this size
+// (a multiple of the block size), double-buffered in pinned host memory.
+constexpr size_t STREAM_CHUNK_BYTES = 32u << 20;
+
+lbh_status lbh_matrix_create_streamed(lbh_ctx *ctx, int32_t ty, size_t rows, size_t k, lbh_byte_reader reader,
+                                      void *user, lbh_matrix **out, lbh_error *err) {
+    if (!ctx || !out || !reader) return fail(err, LBH_NULL_ARGUMENT);
+    *out = nullptr;
+    if (!is_dot_type(ty)) return fail(err, LBH_UNSUPPORTED_TYPE, ty);
+    lbh_status st = check_elements(ty, k, err);
+    if (st) return st;
+    if (rows == 0) return fail(err, LBH_DIMENSION_MISMATCH, ty, 0, 1, 0);
+    const size_t nb = k / 256, bb = block_bytes(ty), want = rows * nb * bb;
+    if (nb > 64 || rows > 0x7fffffffull) return fail(err, LBH_UNSUPPORTED_SHAPE, ty, 0, 64, nb);
+    if (want >= (1ull << 32)) return fail(err, LBH_UNSUPPORTED_SHAPE, ty, 0, (1ull << 32) - 1, want);
+    const long long U = (long long)(rows * nb);
+    long long per = (long long)(STREAM_CHUNK_BYTES / bb);
+    if (per > U) per = U;
+    const size_t cb = (size_t)per * bb;
+    const bool kq = ty == LBH_Q4_K || ty == LBH_Q5_K;
+    DeviceGuard g(ctx->device);
+    uint8_t *planes = nullptr, *host[2] = {nullptr, nullptr}, *dev[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool pending[2] = {false, false};
+    hipError_t e = hipMalloc(&planes, want);
+    for (int b = 0; b < 2 && e == hipSuccess; ++b) {
+        e = hipHostMalloc(&host[b], cb, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipMalloc(&dev[b], cb);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&done[b], hipEventDisableTiming);
+    }
+    st = e == hipSuccess ? LBH_OK : hip_fail(err, e);
+    // Chunk i: wait until its host buffer's previous DMA is done, read, check
+    // the scales on the host (validate_scales, k_quants.rs:178-208: first
+    // offending block in order, d before dmin), then DMA and repack the units
+    // on the stream while the host reads chunk i + 1 into the other buffer.
+    for (long long u0 = 0, i = 0; st == LBH_OK && u0 < U; u0 += per, ++i) {
+        const int b = (int)(i & 1);
+        const long long n = U - u0 < per ? U - u0 : per;
+        if (pending[b]) {
+            e = hipEventSynchronize(done[b]);
+            if (e != hipSuccess) {
+                st = hip_fail(err, e);
+                break;
+            }
+        }
+        const int32_t code = reader(user, (uint64_t)u0 * bb, host[b], (size_t)n * bb);
+        if (code != 0) {
+            st = fail(err, (lbh_status)LBH_SOURCE_READ_FAILED, ty, (uint64_t)u0 * bb, 0, (uint64_t)(int64_t)code);
+            break;
+        }
+        for (long long j = 0; j < n && st == LBH_OK; ++j) {
+            const uint8_t *blk = host[b] + (size_t)j * bb;
+            for (int f = 0; f < (kq ? 2 : 1); ++f) {
+                const uint32_t h = blk[2 * f] | ((uint32_t)blk[2 * f + 1] << 8);
+                if ((h & 0x7c00u) == 0x7c00u) {
+                    const long long u = u0 + j;
+                    st = fail(err, LBH_NON_FINITE_SCALE, ty, (uint64_t)(u % (long long)nb), 0, 0, h, (uint32_t)f,
+                              (uint64_t)(u / (long long)nb));
+                    break;
+                }
+            }
+        }
+        if (st != LBH_OK) break;
+        e = hipMemcpyAsync(dev[b], host[b], (size_t)n * bb, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = launch_repack_range(ty, dev[b], planes, U, u0, n, ctx->stream);
+        if (e == hipSuccess) e = hipEventRecord(done[b], ctx->stream);
+        if (e != hipSuccess) st = hip_fail(err, e);
+        pending[b] = true;
+    }
+    e = hipStreamSynchronize(ctx->stream);
+    if (st == LBH_OK && e != hipSuccess) st = hip_fail(err, e);
+    for (int b = 0; b < 2; ++b) {
+        if (host[b]) (void)hipHostFree(host[b]);
+        if (dev[b]) (void)hipFree(dev[b]);
+        if (done[b]) (void)hipEventDestroy(done[b]);
+    }
+    if (st != LBH_OK) {
+        if (planes) (void)hipFree(planes);
+        return st;
+    }
+    lbh_matrix *m = new (std::nothrow) lbh_matrix();
+    if (!m) {
+        (void)hipFree(planes);
+        return fail(err, LBH_HIP_ERROR);
+    }
+    m->device = ctx->device;
+    m->type = ty;
+    m->rows = rows;
+    m->k = k;
+    m->nb = nb;
+    m->planes = planes;
+    m->bytes = want;
+    *out = m;
+    return ok(err);
+}
+
 lbh_status lbh_matrix_destroy(lbh_matrix *m) {
     if (!m) return LBH_NULL_ARGUMENT;
     DeviceGuard g(m->device);

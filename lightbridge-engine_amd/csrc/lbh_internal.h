@@ -219,6 +219,8 @@ hipError_t launch_reset_status(DevStatus *st, hipStream_t s);
 hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s);
 hipError_t launch_repack(int ty, const uint8_t *ggml, uint8_t *planes, long long units, int to_device,
                          hipStream_t s);
+hipError_t launch_repack_range(int ty, const uint8_t *src, uint8_t *dst, long long U, long long u0, long long n,
+                               hipStream_t s);
 hipError_t launch_validate_scales(int ty, const uint8_t *ggml, long long units,
                                   unsigned long long *first, hipStream_t s);
 hipError_t launch_f16_to_f32(const uint16_t *in, float *out, long long n, hipStream_t s);

@@ -80,6 +80,16 @@ __global__ void k_repack(const uint8_t *__restrict__ src, uint8_t *__restrict__ 
     }
 }
 
+// Units [u0, u0 + n) of a matrix of U units, GGML bytes of those units
+// contiguous at `src`, into their places in the device layout.
+template <int TY>
+__global__ void k_repack_range(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, long long U, long long u0,
+                               long long n) {
+    constexpr int BB = layout_of(TY).block_bytes;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        for (int p = 0; p < BB; ++p) dst[dev_offset(TY, U, u0 + i, p)] = src[i * BB + p];
+}
+
 // First non-finite f16 d / dmin in unit order (validate_scales, k_quants.rs:178-208).
 template <int TY>
 __global__ void k_validate_scales(const uint8_t *__restrict__ ggml, long long U, unsigned long long *first) {
@@ -132,6 +142,21 @@ hipError_t launch_repack(int ty, const uint8_t *src, uint8_t *dst, long long U, 
     case T_IQ3_S: hipLaunchKernelGGL(k_repack<T_IQ3_S>, dim3(grid), dim3(256), 0, s, src, dst, U, to_device); break;
     case T_Q4_K: hipLaunchKernelGGL(k_repack<T_Q4_K>, dim3(grid), dim3(256), 0, s, src, dst, U, to_device); break;
     case T_Q5_K: hipLaunchKernelGGL(k_repack<T_Q5_K>, dim3(grid), dim3(256), 0, s, src, dst, U, to_device); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_range(int ty, const uint8_t *src, uint8_t *dst, long long U, long long u0, long long n,
+                               hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    int grid = cdiv(n, 256);
+    grid = grid > 8192 ? 8192 : grid;
+    switch (ty) {
+    case T_IQ2_S: hipLaunchKernelGGL(k_repack_range<T_IQ2_S>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
+    case T_IQ3_S: hipLaunchKernelGGL(k_repack_range<T_IQ3_S>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
+    case T_Q4_K: hipLaunchKernelGGL(k_repack_range<T_Q4_K>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
+    case T_Q5_K: hipLaunchKernelGGL(k_repack_range<T_Q5_K>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

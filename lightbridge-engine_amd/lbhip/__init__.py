@@ -29,6 +29,7 @@ STATUS = {
     8: "NonFiniteScale", 9: "NonFiniteActivation", 10: "NonFiniteQ8Scale",
     20: "DimensionMismatch", 21: "ScratchTooSmall", 22: "NonFiniteValue",
     23: "RoutedExpertOrder", 24: "DuplicateRoutedExpert", 25: "InvalidParameter",
+    36: "SourceReadFailed",
     100: "HipError", 101: "NullArgument", 102: "UnsupportedShape",
 }
 QUANT_ERRORS = {1, 2, 3, 4, 6, 7, 8, 9, 10}
@@ -130,6 +131,7 @@ def lib() -> C.CDLL:
             "lbh_expert_cache_read_record": ([p, p, p, sz, E], i32),
             "lbh_moe_create_cached": ([p, p, p, p, p, C.POINTER(p), E], i32),
             "lbh_moe_forward_leased": ([p, p, p, p, sz, p, p], i32),
+            "lbh_matrix_create_streamed": ([p, i32, sz, sz, p, p, C.POINTER(p), E], i32),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -438,6 +440,19 @@ class DeviceMatrix:
                   C.byref(h))
         self.handle = h
         self.nbytes = lib().lbh_matrix_bytes(h)
+
+    @classmethod
+    def streamed(cls, be: HipBackend, ty: int, rows: int, k: int, reader) -> "DeviceMatrix":
+        """A matrix whose GGML bytes come from `reader` (a ctypes lbh_byte_reader
+        callback), streamed through pinned chunks straight to HBM."""
+        self = cls.__new__(cls)
+        self.be, self.ty, self.rows, self.k = be, ty, rows, k
+        h = C.c_void_p()
+        self.handle = None
+        _call(lib().lbh_matrix_create_streamed, be.ctx, ty, rows, k, C.cast(reader, C.c_void_p), None, C.byref(h))
+        self.handle = h
+        self.nbytes = lib().lbh_matrix_bytes(h)
+        return self
 
     def prepare_gemm(self) -> None:
         """Build the MFMA-ready copy used by gemm_q8_k (Q4_K / Q5_K)."""
