@@ -254,39 +254,55 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_router_shared(MoeArgs a) {
 // lane per row accumulates them in the reference order
 //     y = ((0 + c_0 d_0) + c_1 d_1) + ... + 1.0 * d_shared   (moe.rs:141-146).
 template <int TY, int LPU>
+struct DownStream {
+    using W = WOf<TY, LPU>;
+    Planes P;
+    int nb, r0, r1, it, stride;
+    W wa, wb;
+
+    __device__ __forceinline__ void issue(const LaneMap<LPU> &L, uint32_t po, int items, int i, W &w) const {
+        const int r = r0 + i * L.rpw + L.slot;
+        if (i < items && L.lane_on && r < r1) load_slice(P, (uint32_t)(r * nb + L.b), po, L.part, w);
+    }
+    // The stream's views and its first step's weight loads: callable before
+    // the workgroup's prologue, so that HBM round trip overlaps it.
+    __device__ __forceinline__ void start(const MatView &Vd, int nb_, int r0_, int r1_, int first, int stride_) {
+        nb = nb_, r0 = r0_, r1 = r1_, it = first, stride = stride_;
+        const MatView V = uniform_view(Vd);
+        P = make_planes(V.planes, V.units, V.bytes);
+        const LaneMap<LPU> L(threadIdx.x & 63, nb);
+        issue(L, part_offset<TY, LPU>(P, L.part), (r1 - r0 + L.rpw - 1) / L.rpw, it, wa);
+    }
+    __device__ __forceinline__ void run(const uint8_t *q8, const void *s_grid, FoldLDS<TY> &fold, float *s_y) {
+        const LaneMap<LPU> L(threadIdx.x & 63, nb);
+        const uint32_t po = part_offset<TY, LPU>(P, L.part);
+        const int items = (r1 - r0 + L.rpw - 1) / L.rpw;
+        ActOf<TY, LPU> act;
+        load_act(q8 + L.b * 292, L.part, act);
+        auto process = [&](int i, const W &w) {
+            const int r = r0 + i * L.rpw + L.slot;
+            const bool on = L.lane_on && r < r1;
+            const float v = row_dot<TY, LPU>(w, act, on, L, s_grid, fold, nullptr, 0);
+            if (on && L.leader()) s_y[r - r0] = v;
+        };
+        while (it < items) {
+            issue(L, po, items, it + stride, wb);
+            process(it, wa);
+            it += stride;
+            if (it >= items) break;
+            issue(L, po, items, it + stride, wa);
+            process(it, wb);
+            it += stride;
+        }
+    }
+};
+
+template <int TY, int LPU>
 __device__ __forceinline__ void down_wave(const MatView &Vd, const uint8_t *q8, int nb, int r0, int r1, int first,
                                           int stride, const void *s_grid, FoldLDS<TY> &fold, float *s_y) {
-    const int lane = threadIdx.x & 63;
-    const LaneMap<LPU> L(lane, nb);
-    const MatView V = uniform_view(Vd);
-    const Planes P = make_planes(V.planes, V.units, V.bytes);
-    const uint32_t po = part_offset<TY, LPU>(P, L.part);
-    const int items = (r1 - r0 + L.rpw - 1) / L.rpw;
-    using W = WOf<TY, LPU>;
-    auto issue = [&](int it, W &w) {
-        const int r = r0 + it * L.rpw + L.slot;
-        if (it < items && L.lane_on && r < r1) load_slice(P, (uint32_t)(r * nb + L.b), po, L.part, w);
-    };
-    int it = first;
-    W wa, wb;
-    issue(it, wa);
-    ActOf<TY, LPU> act;
-    load_act(q8 + L.b * 292, L.part, act);
-    auto process = [&](int it, const W &w) {
-        const int r = r0 + it * L.rpw + L.slot;
-        const bool on = L.lane_on && r < r1;
-        const float v = row_dot<TY, LPU>(w, act, on, L, s_grid, fold, nullptr, 0);
-        if (on && L.leader()) s_y[r - r0] = v;
-    };
-    while (it < items) {
-        issue(it + stride, wb);
-        process(it, wa);
-        it += stride;
-        if (it >= items) break;
-        issue(it + stride, wa);
-        process(it, wb);
-        it += stride;
-    }
+    DownStream<TY, LPU> d;
+    d.start(Vd, nb, r0, r1, first, stride);
+    d.run(q8, s_grid, fold, s_y);
 }
 
 template <int TYR, int TYS>
@@ -302,8 +318,10 @@ template <int TYR, int LPUR, int TYS, int LPUS>
 __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     if (a.status && (a.status->first_bad_input != ~0ull || a.status->first_bad_swiglu != ~0ull)) return;
-    const int wid = threadIdx.x >> 6;
-    const int n = route_n(a);
+    // Wave index and route count through readfirstlane: the task choice below
+    // (and every descriptor derived from it) is wave-uniform.
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = __builtin_amdgcn_readfirstlane(route_n(a));
     const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
     const int r0 = blockIdx.x * a.tile_d;
     const int r1 = r0 + a.tile_d < a.hidden ? r0 + a.tile_d : a.hidden;
@@ -313,6 +331,18 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     const int nw = blockDim.x >> 6;
     float *s_y = reinterpret_cast<float *>(s_foldp + nw * down_fold_bytes<TYR, TYS>());
     uint8_t *s_q8 = reinterpret_cast<uint8_t *>(s_y + (MOE_MAX_ROUTED + 1) * a.tile_d);   // [n * nbr + nbs] blocks
+
+    // Each wave's first task (routed expert `wid`, or its part of the shared
+    // expert) issues its first weight loads now: their HBM latency overlaps
+    // the h quantization below.
+    const int tasks = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
+    const bool first_routed = wid < n, first_shared = !first_routed && wid < tasks;
+    DownStream<TYR, LPUR> d_r;
+    DownStream<TYS, LPUS> d_s;
+    if (first_routed)
+        d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
+    else if (first_shared)
+        d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
 
     // Q8_K of every expert's h into LDS (quantize_row_q8_k_into of the down
     // projection's input, gemv.rs:161-163): chunks of up to four blocks of one
@@ -365,10 +395,16 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     __syncthreads();
 
     // Tasks: routed experts 0..n-1, then DOWN_SHARED_WAVES interleaved parts of
-    // the shared expert; wave w takes tasks w, w + nw, ...
+    // the shared expert; wave w takes tasks w, w + nw, ... (the first one
+    // started before the prologue).
     const int ystride = a.tile_d;
-    const int tasks = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
-    for (int t = wid; t < tasks; t += nw) {
+    FoldLDS<TYR> &fold_r = *reinterpret_cast<FoldLDS<TYR> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>());
+    FoldLDS<TYS> &fold_s = *reinterpret_cast<FoldLDS<TYS> *>(s_foldp + wid * down_fold_bytes<TYR, TYS>());
+    if (first_routed)
+        d_r.run(s_q8 + wid * nbr * 292, s_grid_r, fold_r, s_y + wid * ystride);
+    else if (first_shared)
+        d_s.run(s_q8 + n * nbr * 292, TYS == TYR ? s_grid_r : s_grid_s, fold_s, s_y + n * ystride);
+    for (int t = wid + nw; t < tasks; t += nw) {
         if (t < n) {
             down_wave<TYR, LPUR>(routed_view(a, t).down, s_q8 + t * nbr * 292, nbr, r0, r1, 0, 1,
                                  s_grid_r,
