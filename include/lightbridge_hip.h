@@ -268,6 +268,17 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *moe, size_t max_tokens, size_t top_k, 
 lbh_status lbh_moe_set_batch_tiles(lbh_moe *moe, int32_t tokens_per_chunk, int32_t rows_gate_up_routed,
                                    int32_t rows_gate_up_shared, int32_t rows_down_routed, int32_t rows_down_shared);
 
+/* Engine of the batched IQ2_S / IQ3_S streams (no counterpart in the reference,
+ * whose batch is a loop over tokens).  Chunks of at least mx_min_tokens tokens
+ * (1..16; default 5) run on the f16 matrix cores, one 16-row x 16-token product
+ * per codebook step, with mx_rows_gate_up / mx_rows_down rows per workgroup
+ * (0: default); smaller chunks run on the VALU integer dots; mx_min_tokens = 0
+ * keeps every chunk on the VALU.  Every choice gives the same bits.  Resets the
+ * tokens per chunk (16 with the matrix cores, 8 without) and the VALU row tiles
+ * to their defaults. */
+lbh_status lbh_moe_set_batch_engine(lbh_moe *moe, int32_t mx_min_tokens, int32_t mx_rows_gate_up,
+                                    int32_t mx_rows_down);
+
 /* [async] Batched form of lbh_moe_forward: ids_dev / coefs_dev are device arrays
  * [n_tokens][top_k] (each token's ids ascending and distinct), x_dev [n_tokens][hidden],
  * y_dev [n_tokens][hidden].  Unchecked; a routing with an id >= n_experts or a token

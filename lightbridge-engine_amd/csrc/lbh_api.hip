@@ -513,11 +513,24 @@ struct lbh_moe {
     float *batch_coefs;
     int32_t *plan_host;       // pinned
     int tc, rt_gu_r, rt_gu_s, rt_d_r, rt_d_s;
+    int mx_min;               // batched IQ chunks of >= mx_min tokens on the matrix cores (0: none)
+    int mx_rt_gu, mx_rt_d;    // their rows per workgroup
     uint8_t *shared_gemm_mem; // MFMA-ready copies of a K-quant shared expert (batched calls)
     size_t gemm_off[3];       // A offsets of gate, up, down in shared_gemm_mem
 };
 
 namespace {
+
+// Batched launch shapes measured on MI355X at the configs[3] shapes (64 tokens,
+// hidden 4096, routed ffn 1536): with the matrix cores on, chunks of 16 tokens
+// (one instruction's width); the VALU streams alone do best with chunks of 8.
+constexpr int MX_MIN_DEFAULT = 5;
+void set_batch_defaults(lbh_moe *m, int mx_min) {
+    m->mx_min = mx_min;
+    m->mx_rt_gu = 64, m->mx_rt_d = 128;
+    m->tc = mx_min > 0 ? 16 : 8;
+    m->rt_gu_r = 64, m->rt_gu_s = 64, m->rt_d_r = 160, m->rt_d_s = 64;
+}
 
 void free_moe(lbh_moe *m) {
     if (!m) return;
@@ -632,11 +645,7 @@ lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_exper
         m->wg_r = total;
     }
     m->tile_d = 16;
-    m->tc = 8;
-    m->rt_gu_r = 64;
-    m->rt_gu_s = 64;
-    m->rt_d_r = 160;
-    m->rt_d_s = 64;
+    set_batch_defaults(m, MX_MIN_DEFAULT);
     const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
     m->h_stride = (int)max_ffn;
     const size_t slots = MOE_MAX_ROUTED + 1;
@@ -974,6 +983,12 @@ BatchArgs batch_args(const lbh_moe *m, const uint32_t *ids, const float *coefs, 
     a.rt_d_s = m->rt_d_s;
     a.type_gate_r = m->type_gate_r;
     a.type_down_r = m->type_down_r;
+    a.mx = m->mx_min > 0 ? 1 : 0;
+    a.mx_min = m->mx_min > 0 ? m->mx_min : BATCH_MAX_TC + 1;
+    a.mx_rt_gu = m->mx_rt_gu;
+    a.mx_rt_d = m->mx_rt_d;
+    a.vc = a.mx ? (a.tc < a.mx_min - 1 ? a.tc : a.mx_min - 1) : a.tc;
+    if (a.vc < 1) a.vc = 1;
     return a;
 }
 
@@ -1014,6 +1029,10 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     const size_t o_q8hr = take(P * nbr * 292), o_q8hs = take(T * nbs * 292);
     const size_t o_dr = take(P * m->hidden * 4), o_ds = take(T * m->hidden * 4);
     const size_t o_ids = take(P * 4), o_coefs = take(P * 4);
+    // operand copies of the Q8_K rows for the matrix-core IQ streams
+    const size_t o_xqm = take(T * nbh * 256), o_xdm = take(T * nbh * 4);
+    const size_t o_hqr = take(P * nbr * 256), o_hdr = take(P * nbr * 4);
+    const size_t o_hqs = take(T * nbs * 256), o_hds = take(T * nbs * 4);
     // A K-quant shared expert runs on the matrix cores: gate/up outputs and the
     // GEMM activation tiles of x and h_s.
     const bool sgemm = m->has_shared && is_kquant(m->shared.gate.type) && is_kquant(m->shared.down.type);
@@ -1051,6 +1070,12 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     a.q8h_s = b + o_q8hs;
     a.d_r = reinterpret_cast<float *>(b + o_dr);
     a.d_s = reinterpret_cast<float *>(b + o_ds);
+    a.xq_mx = b + o_xqm;
+    a.xd_mx = reinterpret_cast<float *>(b + o_xdm);
+    a.hq_mx_r = b + o_hqr;
+    a.hd_mx_r = reinterpret_cast<float *>(b + o_hdr);
+    a.hq_mx_s = b + o_hqs;
+    a.hd_mx_s = reinterpret_cast<float *>(b + o_hds);
     m->batch_ids = reinterpret_cast<uint32_t *>(b + o_ids);
     m->batch_coefs = reinterpret_cast<float *>(b + o_coefs);
     a.shared_gemm = sgemm ? 1 : 0;
@@ -1098,12 +1123,33 @@ lbh_status lbh_moe_set_batch_tiles(lbh_moe *m, int32_t tokens_per_chunk, int32_t
     const int v[4] = {rows_gate_up_routed, rows_gate_up_shared, rows_down_routed, rows_down_shared};
     for (int i = 0; i < 4; ++i)
         if (v[i] < 1 || v[i] > 65536) return LBH_INVALID_PARAMETER;
-    BatchArgs probe = batch_args(m, nullptr, nullptr, 1, 1, nullptr, nullptr);
-    probe.tc = tokens_per_chunk;
+    const int tc_old = m->tc;
+    m->tc = tokens_per_chunk;
+    const BatchArgs probe = batch_args(m, nullptr, nullptr, 1, 1, nullptr, nullptr);
+    m->tc = tc_old;
     for (int st = 0; st < 5; ++st)
         if (batch_lds_bytes(probe, st) > 160 * 1024) return LBH_UNSUPPORTED_SHAPE;
     m->tc = tokens_per_chunk;
     m->rt_gu_r = v[0], m->rt_gu_s = v[1], m->rt_d_r = v[2], m->rt_d_s = v[3];
+    return LBH_OK;
+}
+
+lbh_status lbh_moe_set_batch_engine(lbh_moe *m, int32_t mx_min_tokens, int32_t mx_rows_gate_up,
+                                    int32_t mx_rows_down) {
+    if (!m) return LBH_NULL_ARGUMENT;
+    if (mx_min_tokens < 0 || mx_min_tokens > BATCH_MAX_TC || mx_rows_gate_up < 0 || mx_rows_gate_up > 65536 ||
+        mx_rows_down < 0 || mx_rows_down > 65536)
+        return LBH_INVALID_PARAMETER;
+    const lbh_moe saved = *m;
+    set_batch_defaults(m, mx_min_tokens);
+    if (mx_rows_gate_up) m->mx_rt_gu = mx_rows_gate_up;
+    if (mx_rows_down) m->mx_rt_d = mx_rows_down;
+    const BatchArgs probe = batch_args(m, nullptr, nullptr, 1, 1, nullptr, nullptr);
+    for (int st = 0; st < 5; ++st)
+        if (batch_lds_bytes(probe, st) > 160 * 1024) {
+            *m = saved;
+            return LBH_UNSUPPORTED_SHAPE;
+        }
     return LBH_OK;
 }
 

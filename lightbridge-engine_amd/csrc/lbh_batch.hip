@@ -34,6 +34,14 @@ constexpr int MB_WAVES = MB_THREADS / 64;
 // quants so a lane's slice is a run of 16-byte reads).
 constexpr int Q8L = 304;
 
+// Matrix-core operand copy of Q8_K rows, written beside the GGML bytes by the
+// quantize kernels: block k's 256 quants XOR 0x80 (as unsigned bytes, q + 128)
+// at q + 256 k, its scale at d[k].
+struct MxRows {
+    uint8_t *q;
+    float *d;
+};
+
 __host__ __device__ constexpr int al16(int v) { return (v + 15) & ~15; }
 
 // ------------------------------------------------------------ activations
@@ -325,13 +333,15 @@ __device__ __forceinline__ void batch_rows(const MatView (&mv)[NM], int r0, int 
     const int steps = (r1 - r0 + rpw - 1) / rpw;
     // Lanes past the tile (or past the wave's last whole row) load and decode
     // the tile's last row: every register is defined, and `on` gates the writes.
+    // The loads are unconditional (a step past the end reloads the tile's last
+    // row, never used), so the wait before a step's use leaves the next step's
+    // loads in flight.
     auto issue = [&](int j, W (&w)[NM]) {
-        if (j < steps) {
-            int r = r0 + j * rpw + L.slot;
-            r = L.lane_on && r < r1 ? r : r1 - 1;
+        int r = r0 + j * rpw + L.slot;
+        r = L.lane_on && r < r1 ? r : r1 - 1;
+        r = r < r1 ? r : r1 - 1;
 #pragma unroll
-            for (int m = 0; m < NM; ++m) load_slice(P[m], (uint32_t)(r * nb + L.b), po[m], L.part, w[m]);
-        }
+        for (int m = 0; m < NM; ++m) load_slice(P[m], (uint32_t)(r * nb + L.b), po[m], L.part, w[m]);
     };
     auto process = [&](int j, const W (&w)[NM]) {
         const int r = r0 + j * rpw + L.slot;
@@ -390,14 +400,22 @@ constexpr int mb_lpu() {
 // Sort of the batch's pairs by expert (workgroup 0) and Q8_K of every token
 // (the other workgroups, four blocks per wave).
 __device__ __forceinline__ void quantize_rows_out(const float *x, long long nblocks, long long first, uint8_t *plain,
-                                                  uint8_t *rm, uint8_t *lds_wave) {
+                                                  uint8_t *rm, uint8_t *lds_wave, MxRows mx = MxRows{}) {
     // Blocks [first, first + 4) (x points at block `first`) into the wave's
-    // LDS, then out to global memory: the GGML bytes, and (rm != NULL) the copy
-    // with residue-major qs.
+    // LDS, then out to global memory: the GGML bytes, (rm != NULL) the copy
+    // with residue-major qs, and (mx.q != NULL) the matrix-core operand copy.
     const int lane = threadIdx.x & 63;
     const long long cnt = nblocks - first < 4 ? nblocks - first : 4;
     quantize_blocks_wave(x, lds_wave, 0, cnt);
     wave_sync();
+    if (mx.q) {
+        for (int k = lane; k < (int)cnt * 64; k += 64) {
+            const int blk = k >> 6, w = k & 63;
+            const uint32_t v = *reinterpret_cast<const uint32_t *>(lds_wave + blk * 292 + 4 + 4 * w);
+            reinterpret_cast<uint32_t *>(mx.q)[(first + blk) * 64 + w] = v ^ 0x80808080u;
+        }
+        if (lane < cnt) mx.d[first + lane] = *reinterpret_cast<const float *>(lds_wave + lane * 292);
+    }
     const int dw = (int)cnt * 73;
     for (int k = lane; k < dw; k += 64) {
         const int blk = k / 73, w = k - blk * 73;
@@ -427,7 +445,7 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_prep(BatchArgs a) {
         const bool rm = a.has_shared && !a.shared_gemm && (a.shared.gate.type == T_Q4_K || a.shared.gate.type == T_Q5_K);
         if (first < nblocks)
             quantize_rows_out(a.x + first * 256, nblocks, first, a.q8x, rm ? a.q8x_rm : nullptr,
-                              smem + (tid >> 6) * 4 * 292);
+                              smem + (tid >> 6) * 4 * 292, MxRows{a.mx ? a.xq_mx : nullptr, a.xd_mx});
         return;
     }
     const int NE = a.n_experts, T = a.n_tokens, K = a.top_k, TC = a.tc;
@@ -513,6 +531,18 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_prep(BatchArgs a) {
     }
 }
 
+// A chunk of n tokens of a TY stream belongs to the matrix-core kernels.
+template <int TY>
+__device__ __forceinline__ bool mx_takes(const BatchArgs &a, int n) {
+    return (TY == T_IQ2_S || TY == T_IQ3_S) && a.mx && n >= a.mx_min;
+}
+
+// Tokens a VALU stream of type ty stages at most: the chunks the matrix cores
+// leave to it (IQ types with mx on), else whole chunks.
+__host__ __device__ inline int valu_cap(const BatchArgs &a, int ty) {
+    return a.mx && (ty == T_IQ2_S || ty == T_IQ3_S) ? a.vc : a.tc;
+}
+
 // Gate/up, SwiGLU (activation.rs:170-178) -> h, one launch per stream:
 // SHARED: workgroup (token chunk, row tile) of the shared expert; else
 // workgroup (routed chunk, row tile), idle past the sort's chunk count.
@@ -523,13 +553,14 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
     const int nb = a.hidden / 256;
     constexpr int LPU = mb_lpu<TY>();
     uint8_t *s_act = smem;
-    uint8_t *grid = smem + al16(a.tc * nb * Q8L);
+    uint8_t *grid = smem + al16(valu_cap(a, TY) * nb * Q8L);
     float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
     if constexpr (SHARED) {
         const int tiles = (a.ffn_s + a.rt_gu_s - 1) / a.rt_gu_s;
         const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
         const int t0 = c * a.tc;
         const int n = a.n_tokens - t0 < a.tc ? a.n_tokens - t0 : a.tc;
+        if (mx_takes<TY>(a, n)) return;
         const int r0 = tile * a.rt_gu_s, r1 = r0 + a.rt_gu_s < a.ffn_s ? r0 + a.rt_gu_s : a.ffn_s;
         const uint8_t *src = Traits<TY>::KQ ? a.q8x_rm : a.q8x;
         const MatView mv[2] = {a.shared.gate, a.shared.up};
@@ -548,6 +579,7 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
         const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
         if (c >= a.plan[0]) return;
         const int e = a.chunk_expert[c], p0 = a.chunk_p0[c], n = a.chunk_n[c];
+        if (mx_takes<TY>(a, n)) return;
         const int r0 = tile * a.rt_gu_r, r1 = r0 + a.rt_gu_r < a.ffn_r ? r0 + a.rt_gu_r : a.ffn_r;
         const MatView mv[2] = {a.experts[e].gate, a.experts[e].up};
         batch_rows<TY, LPU, 2>(
@@ -579,7 +611,7 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shar
     const long long chunk = ((long long)blockIdx.x * MB_WAVES + wid) * 4;
     uint8_t *lw = lds + wid * 4 * 292;
     if (chunk < br) {
-        quantize_rows_out(a.h_r + chunk * 256, br, chunk, a.q8h_r, nullptr, lw);
+        quantize_rows_out(a.h_r + chunk * 256, br, chunk, a.q8h_r, nullptr, lw, MxRows{a.mx ? a.hq_mx_r : nullptr, a.hd_mx_r});
     } else if (chunk >= brp && chunk - brp < bs) {
         const long long f = chunk - brp;
         if (shared_mode == 2) {
@@ -596,7 +628,7 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shar
             quantize_rows_out(&hbuf[wid][0], bs, f, a.q8h_s, nullptr, lw);
         } else {
             quantize_rows_out(a.h_s + f * 256, bs, f, shared_mode ? nullptr : a.q8h_s, shared_mode ? a.q8h_s : nullptr,
-                              lw);
+                              lw, MxRows{a.mx && !shared_mode ? a.hq_mx_s : nullptr, a.hd_mx_s});
         }
     }
 }
@@ -614,8 +646,9 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
         const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
         const int t0 = c * a.tc;
         const int n = a.n_tokens - t0 < a.tc ? a.n_tokens - t0 : a.tc;
+        if (mx_takes<TY>(a, n)) return;
         const int r0 = tile * a.rt_d_s, r1 = r0 + a.rt_d_s < a.hidden ? r0 + a.rt_d_s : a.hidden;
-        uint8_t *grid = smem + al16(a.tc * nb * Q8L);
+        uint8_t *grid = smem + al16(valu_cap(a, TY) * nb * Q8L);
         float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
         const MatView mv[1] = {a.shared.down};
         batch_rows<TY, LPU, 1>(
@@ -632,8 +665,9 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
         const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
         if (c >= a.plan[0]) return;
         const int e = a.chunk_expert[c], p0 = a.chunk_p0[c], n = a.chunk_n[c];
+        if (mx_takes<TY>(a, n)) return;
         const int r0 = tile * a.rt_d_r, r1 = r0 + a.rt_d_r < a.hidden ? r0 + a.rt_d_r : a.hidden;
-        uint8_t *grid = smem + al16(a.tc * nb * Q8L);
+        uint8_t *grid = smem + al16(valu_cap(a, TY) * nb * Q8L);
         float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
         const MatView mv[1] = {a.experts[e].down};
         batch_rows<TY, LPU, 1>(
@@ -645,6 +679,326 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
             },
             [&](int i, int r, const float *res) { a.d_r[(long long)(p0 + i) * a.hidden + r] = res[0]; });
     }
+}
+
+// ==================================================== IQ streams on the matrix cores
+//
+// The IQ2_S / IQ3_S gate/up and down streams as f16 matrix-core products
+// (v_mfma_f32_16x16x32_f16), bit-identical to the dot4 streams above: per
+// (row, token, block) the integer block sum is formed exactly and folded in
+// the reference's order.
+//
+// Wave tile: 16 rows x the chunk's tokens (up to 16) per block.  Lane l holds
+// row l % 16 of the A operand and token l % 16 of the B operand, both for the
+// block's elements 64 (l / 16) + 8 m .. + 7 in instruction m (m = 0..7): A and
+// B use the same (lane, slot) -> element map, so each instruction contracts 32
+// elements of the block whatever its internal k order.  The lane's slice of
+// its row is the four-lane part l / 16 of the unit (load_slice<TY, 4>).
+//   A: one codebook entry (IQ2_S: one 8-element grid entry; IQ3_S: two
+//      4-element entries) from LDS tables of f16 magnitudes, the eight sign
+//      bits applied by XOR with an f16 sign-mask table entry, times the
+//      entry's integer scale (IQ2_S 1 + 2 nibble per 16 elements, IQ3_S
+//      2 nibble + 1 per 32): |A| <= 43 * 31 = 1333 (IQ2_S), 15 * 31 = 465
+//      (IQ3_S), integers an f16 holds exactly.
+//   B: the Q8_K quants (|B| <= 128) from the operand copy of q + 128 as
+//      unsigned bytes: 0x6400 | (q + 128) is the f16 1024 + q + 128, and one
+//      packed f16 subtraction of 1152 leaves q exactly.
+// Every product is an integer below 2^18 and every partial sum of a chain of
+// instructions stays below 2^24 (IQ2_S: chains of three instructions, 96
+// elements, 96 * 1333 * 128 < 2^24; IQ3_S: the whole block, 256 * 465 * 128 <
+// 2^24), so the f32 accumulation is exact in any order; each chain converted
+// to int32 and summed gives the reference's integer block sum (q8_k.rs:337-364,
+// :380-428, integer additions, exact in any order).  The fold is the one of
+// lbh_rows.h: term = (d * d8) * (float)bsum, chain += term in block order,
+// IQ2_S result = 0.125 * chain.
+
+typedef _Float16 mx_h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mx_h2 __attribute__((ext_vector_type(2)));
+typedef float mx_f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t mx_u4 __attribute__((ext_vector_type(4)));
+
+constexpr int MX_THREADS = 256;
+constexpr int MX_WAVES = MX_THREADS / 64;
+
+// LDS tables: the f16 magnitudes of every codebook entry (IQ2_S 1024 x 8,
+// IQ3_S 512 x 4), then 256 sign masks of eight f16 (bit 15 of element i is
+// bit i of the sign byte).
+template <int TY>
+struct MxTab {
+    static constexpr int ENTRY = TY == T_IQ2_S ? 16 : 8;
+    static constexpr int GRID = (TY == T_IQ2_S ? 1024 : 512) * ENTRY;
+    static constexpr int BYTES = GRID + 256 * 16;
+};
+
+__device__ __forceinline__ uint32_t mx_bits(mx_h2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ mx_h2 mx_pair(uint32_t v) { return __builtin_bit_cast(mx_h2, v); }
+
+// Bytes i, i + 1 of v as an f16 pair.
+__device__ __forceinline__ uint32_t mx_f16_bytes(uint32_t v, int i) {
+    return mx_bits(mx_h2{(_Float16)(float)byte_of(v, i), (_Float16)(float)byte_of(v, i + 1)});
+}
+
+template <int TY>
+__device__ __forceinline__ void mx_fill(uint8_t *tab) {
+    if constexpr (TY == T_IQ2_S) {
+        for (int i = threadIdx.x; i < 1024; i += MX_THREADS) {
+            const uint64_t v = c_iq2s_grid[i];
+            const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+            reinterpret_cast<uint4 *>(tab)[i] =
+                make_uint4(mx_f16_bytes(lo, 0), mx_f16_bytes(lo, 2), mx_f16_bytes(hi, 0), mx_f16_bytes(hi, 2));
+        }
+    } else {
+        for (int i = threadIdx.x; i < 512; i += MX_THREADS) {
+            const uint32_t v = c_iq3s_grid[i];
+            reinterpret_cast<uint2 *>(tab)[i] = make_uint2(mx_f16_bytes(v, 0), mx_f16_bytes(v, 2));
+        }
+    }
+    for (int s = threadIdx.x; s < 256; s += MX_THREADS) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            w[k] = ((((uint32_t)s >> (2 * k)) & 1u) << 15) | ((((uint32_t)s >> (2 * k + 1)) & 1u) << 31);
+        reinterpret_cast<uint4 *>(tab + MxTab<TY>::GRID)[s] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// Eight f16 magnitudes with their signs applied, times the integer scale ls.
+__device__ __forceinline__ mx_h8 mx_signed_scaled(uint4 mag, uint4 sgn, uint32_t ls) {
+    const _Float16 f = (_Float16)(float)ls;
+    const mx_h2 s = {f, f};
+    const mx_u4 r = {mx_bits(mx_pair(mag.x ^ sgn.x) * s), mx_bits(mx_pair(mag.y ^ sgn.y) * s),
+                     mx_bits(mx_pair(mag.z ^ sgn.z) * s), mx_bits(mx_pair(mag.w ^ sgn.w) * s)};
+    return __builtin_bit_cast(mx_h8, r);
+}
+
+// A operand of instruction m: the lane's slice holds sub-blocks 2p, 2p + 1;
+// m covers entry m % 4 of sub-block m / 4 (q8_k.rs:337-364 index, sign and
+// scale layout, as slice_sum in lbh_dev.h).
+__device__ __forceinline__ mx_h8 mx_a(const WSlice<T_IQ2_S, 4> &w, const uint8_t *tab, int m) {
+    const int g = m >> 2, lg = m & 3;
+    const uint32_t h = byte_of(w.qh, g);
+    const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
+    const uint4 mag = reinterpret_cast<const uint4 *>(tab)[idx];
+    const uint4 sgn = reinterpret_cast<const uint4 *>(tab + MxTab<T_IQ2_S>::GRID)[byte_of(w.sg[g], lg)];
+    const uint32_t ls = 1u + 2u * ((byte_of(w.sc, g) >> (4 * (lg >> 1))) & 15u);
+    return mx_signed_scaled(mag, sgn, ls);
+}
+
+// IQ3_S (q8_k.rs:380-428): instruction m covers the two 4-element entries of
+// eighth m % 4 of sub-block m / 4, the sign byte's low nibble on the first.
+__device__ __forceinline__ mx_h8 mx_a(const WSlice<T_IQ3_S, 4> &w, const uint8_t *tab, int m) {
+    const int g = m >> 2, lg = m & 3;
+    const uint32_t h = byte_of(w.qh, g);
+    const uint32_t qq = w.qs[2 * g + (lg >> 1)];
+    const int sh = 16 * (lg & 1);
+    const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
+    const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
+    const uint2 m1 = reinterpret_cast<const uint2 *>(tab)[i1], m2 = reinterpret_cast<const uint2 *>(tab)[i2];
+    const uint4 sgn = reinterpret_cast<const uint4 *>(tab + MxTab<T_IQ3_S>::GRID)[byte_of(w.sg[g], lg)];
+    const uint32_t ls = 2u * ((w.sc >> (4 * g)) & 15u) + 1u;
+    return mx_signed_scaled(make_uint4(m1.x, m1.y, m2.x, m2.y), sgn, ls);
+}
+
+// B operand: eight biased quants (two dwords) as f16.
+__device__ __forceinline__ mx_h8 mx_b(uint32_t x0, uint32_t x1) {
+    const mx_h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const mx_u4 r = {mx_bits(mx_pair(perm(0x64646464u, x0, 0x04010400u)) + off),
+                     mx_bits(mx_pair(perm(0x64646464u, x0, 0x04030402u)) + off),
+                     mx_bits(mx_pair(perm(0x64646464u, x1, 0x04010400u)) + off),
+                     mx_bits(mx_pair(perm(0x64646464u, x1, 0x04030402u)) + off)};
+    return __builtin_bit_cast(mx_h8, r);
+}
+
+template <int TY>
+constexpr int mx_chain() {
+    return TY == T_IQ2_S ? 3 : 8;   // instructions per exact f32 chain
+}
+
+// One wave step's inputs: the lane's slices of NM matrices and the block of
+// its token from the operand copy.
+template <int TY, int NM>
+struct MxStep {
+    WSlice<TY, 4> w[NM];
+    uint4 bq[4];
+    float d8;
+};
+
+// Rows [r0, r1) of NM matrices (K = 256 nb) against the chunk's tokens: wave w
+// takes the 16-row tiles w, w + MX_WAVES, ...; lane l's token column holds the
+// operand row bq / bd.  The first step's loads are issued before `prologue`
+// (table fill, ended by a workgroup barrier); then each step's loads are in
+// flight while the one before is computed.  out(token column, row, values)
+// is called by every lane for its four (row, token) results of each tile.
+template <int TY, int NM, class Prologue, class Out>
+__device__ __forceinline__ void mx_rows(const MatView (&mv)[NM], int r0, int r1, int nb, const uint8_t *bq,
+                                        const float *bd, const uint8_t *tab, Prologue prologue, Out out) {
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, q = lane >> 4;
+    Planes P[NM];
+    uint32_t po[NM];
+#pragma unroll
+    for (int t = 0; t < NM; ++t) {
+        P[t] = make_planes(mv[t].planes, mv[t].units, mv[t].bytes);
+        po[t] = part_offset<TY, 4>(P[t], q);
+    }
+    const int ntile = (r1 - r0 + 15) >> 4;
+    const int mine = ntile > wid ? (ntile - wid + MX_WAVES - 1) / MX_WAVES : 0;
+    const int steps = mine * nb;
+    // Rows past r1 load the last row (every register defined; not stored).
+    // The loads are unconditional: a step past the wave's last one reloads the
+    // last step (in bounds, never used), so the compiler's wait before a step's
+    // use counts exactly the younger step's loads instead of draining them.
+    auto issue = [&](int s, MxStep<TY, NM> &st) {
+        const int sc = s < steps ? s : (steps > 0 ? steps - 1 : 0);
+        const int k = sc / nb, b = sc - k * nb;
+        int r = r0 + 16 * (wid + MX_WAVES * k) + c;
+        r = r < r1 ? r : r1 - 1;
+#pragma unroll
+        for (int t = 0; t < NM; ++t) load_slice(P[t], (uint32_t)(r * nb + b), po[t], q, st.w[t]);
+        const uint4 *src = reinterpret_cast<const uint4 *>(bq + b * 256 + 64 * q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) st.bq[j] = src[j];
+        st.d8 = bd[b];
+    };
+    float ch[NM][4];
+#pragma unroll
+    for (int t = 0; t < NM; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ch[t][i] = 0.0f;
+    auto process = [&](int s, const MxStep<TY, NM> &st) {
+        constexpr int CH = mx_chain<TY>();
+        const int k = s / nb, b = s - k * nb;
+        int32_t bs[NM][4];
+        mx_f4 acc[NM];
+#pragma unroll
+        for (int t = 0; t < NM; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bs[t][i] = 0;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            const uint4 v = st.bq[m >> 1];
+            const mx_h8 bo = (m & 1) ? mx_b(v.z, v.w) : mx_b(v.x, v.y);
+#pragma unroll
+            for (int t = 0; t < NM; ++t) {
+                const mx_h8 ao = mx_a(st.w[t], tab, m);
+                const mx_f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ao, bo, m % CH == 0 ? zero : acc[t], 0, 0, 0);
+                if (m % CH == CH - 1 || m == 7) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) bs[t][i] += (int32_t)acc[t][i];
+                }
+            }
+        }
+        // Result i of the lane is (row 4q + i, token c); row 4q + i's d is in lane 4q + i.
+#pragma unroll
+        for (int t = 0; t < NM; ++t) {
+            const float da = f16_to_f32(st.w[t].d);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float dr = __shfl(da, 4 * q + i, 64);
+                ch[t][i] = __fadd_rn(ch[t][i], __fmul_rn(__fmul_rn(dr, st.d8), (float)bs[t][i]));
+            }
+        }
+        if (b == nb - 1) {
+            const int rt0 = r0 + 16 * (wid + MX_WAVES * k);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float res[NM];
+#pragma unroll
+                for (int t = 0; t < NM; ++t) {
+                    res[t] = TY == T_IQ2_S ? __fmul_rn(0.125f, ch[t][i]) : ch[t][i];  // q8_k.rs:369
+                    ch[t][i] = 0.0f;
+                }
+                out(c, rt0 + 4 * q + i, res);
+            }
+        }
+    };
+    MxStep<TY, NM> sa, sb;
+    issue(0, sa);
+    prologue();
+    for (int s = 0; s < steps; s += 2) {
+        issue(s + 1, sb);
+        process(s, sa);
+        if (s + 1 >= steps) break;
+        issue(s + 2, sa);
+        process(s + 1, sb);
+    }
+}
+
+// Gate/up + SwiGLU on the matrix cores (as k_mb_gate_up): workgroup (chunk, row tile).
+template <int TY, bool SHARED>
+__global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
+    __shared__ __align__(16) uint8_t tab[MxTab<TY>::BYTES];
+    if (a.plan[1]) return;
+    const int nb = a.hidden / 256;
+    const int ffn = SHARED ? a.ffn_s : a.ffn_r, rt = a.mx_rt_gu;
+    const int tiles = (ffn + rt - 1) / rt;
+    const int ci = blockIdx.x / tiles, tile = blockIdx.x - ci * tiles;
+    const int r0 = tile * rt, r1 = r0 + rt < ffn ? r0 + rt : ffn;
+    int p0, n;
+    MatView mv[2];
+    if constexpr (SHARED) {
+        p0 = ci * a.tc;
+        n = a.n_tokens - p0 < a.tc ? a.n_tokens - p0 : a.tc;
+        mv[0] = a.shared.gate, mv[1] = a.shared.up;
+    } else {
+        if (ci >= a.plan[0]) return;
+        p0 = a.chunk_p0[ci], n = a.chunk_n[ci];
+        const ExpertDev &E = a.experts[a.chunk_expert[ci]];
+        mv[0] = E.gate, mv[1] = E.up;
+    }
+    if (n < a.mx_min) return;
+    const int c = (int)(threadIdx.x & 15) < n ? (int)(threadIdx.x & 15) : n - 1;
+    const long long tok = SHARED ? (long long)(p0 + c) : (long long)a.pair_token[p0 + c];
+    float *h = SHARED ? a.h_s : a.h_r;
+    mx_rows<TY, 2>(
+        mv, r0, r1, nb, a.xq_mx + tok * nb * 256, a.xd_mx + tok * nb, tab,
+        [&]() {
+            mx_fill<TY>(tab);
+            __syncthreads();
+        },
+        [&](int i, int r, const float *res) {
+            if (i < n && r < r1) h[(long long)(p0 + i) * ffn + r] = swiglu_ref(res[0], res[1]);
+        });
+}
+
+// Down on the matrix cores (as k_mb_down).
+template <int TY, bool SHARED>
+__global__ void __launch_bounds__(MX_THREADS) k_mx_down(BatchArgs a) {
+    __shared__ __align__(16) uint8_t tab[MxTab<TY>::BYTES];
+    if (a.plan[1]) return;
+    const int nb = (SHARED ? a.ffn_s : a.ffn_r) / 256;
+    const int rt = a.mx_rt_d;
+    const int tiles = (a.hidden + rt - 1) / rt;
+    const int ci = blockIdx.x / tiles, tile = blockIdx.x - ci * tiles;
+    const int r0 = tile * rt, r1 = r0 + rt < a.hidden ? r0 + rt : a.hidden;
+    int p0, n;
+    MatView mv[1];
+    if constexpr (SHARED) {
+        p0 = ci * a.tc;
+        n = a.n_tokens - p0 < a.tc ? a.n_tokens - p0 : a.tc;
+        mv[0] = a.shared.down;
+    } else {
+        if (ci >= a.plan[0]) return;
+        p0 = a.chunk_p0[ci], n = a.chunk_n[ci];
+        mv[0] = a.experts[a.chunk_expert[ci]].down;
+    }
+    if (n < a.mx_min) return;
+    const int c = (int)(threadIdx.x & 15) < n ? (int)(threadIdx.x & 15) : n - 1;
+    const long long row = p0 + c;
+    const uint8_t *bq = (SHARED ? a.hq_mx_s : a.hq_mx_r) + row * nb * 256;
+    const float *bd = (SHARED ? a.hd_mx_s : a.hd_mx_r) + row * nb;
+    float *d = SHARED ? a.d_s : a.d_r;
+    mx_rows<TY, 1>(
+        mv, r0, r1, nb, bq, bd, tab,
+        [&]() {
+            mx_fill<TY>(tab);
+            __syncthreads();
+        },
+        [&](int i, int r, const float *res) {
+            if (i < n && r < r1) d[(long long)(p0 + i) * a.hidden + r] = res[0];
+        });
 }
 
 // Ordered combine of one token's routed outputs in its slot (ascending id)
@@ -708,10 +1062,10 @@ int batch_lds_bytes(const BatchArgs &a, int stage) {
         const int sort = (a.n_experts * W + 3 * a.n_experts + 2 * MB_THREADS + 4) * 4;
         return sort > MB_WAVES * 4 * 292 ? sort : MB_WAVES * 4 * 292;
     }
-    case 1: return stream_lds_of(a.type_gate_r, 2, a.tc, nbh);
-    case 2: return a.has_shared ? stream_lds_of(a.shared.gate.type, 2, a.tc, nbh) : 0;
-    case 3: return stream_lds_of(a.type_down_r, 1, a.tc, nbr);
-    default: return a.has_shared ? stream_lds_of(a.shared.down.type, 1, a.tc, nbs) : 0;
+    case 1: return stream_lds_of(a.type_gate_r, 2, valu_cap(a, a.type_gate_r), nbh);
+    case 2: return a.has_shared ? stream_lds_of(a.shared.gate.type, 2, valu_cap(a, a.shared.gate.type), nbh) : 0;
+    case 3: return stream_lds_of(a.type_down_r, 1, valu_cap(a, a.type_down_r), nbr);
+    default: return a.has_shared ? stream_lds_of(a.shared.down.type, 1, valu_cap(a, a.shared.down.type), nbs) : 0;
     }
 }
 
@@ -739,10 +1093,35 @@ static hipError_t down_typed(const BatchArgs &a, int lds, hipStream_t s) {
     return hipGetLastError();
 }
 
+// An IQ stream with the matrix cores on: the matrix-core launch when some
+// chunk can reach mx_min tokens, then the VALU launch when some chunk can stay
+// below it (each kernel returns early on the other's chunks).
+template <int TY, bool SHARED>
+static hipError_t mx_gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
+    if (a.mx_min <= a.tc) {
+        const int grid = (SHARED ? cdiv(a.n_tokens, a.tc) : a.max_chunks) * cdiv(SHARED ? a.ffn_s : a.ffn_r, a.mx_rt_gu);
+        hipLaunchKernelGGL((k_mx_gate_up<TY, SHARED>), dim3(grid), dim3(MX_THREADS), 0, s, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return a.mx_min > 1 ? gate_up_typed<TY, SHARED>(a, lds, s) : hipSuccess;
+}
+
+template <int TY, bool SHARED>
+static hipError_t mx_down_typed(const BatchArgs &a, int lds, hipStream_t s) {
+    if (a.mx_min <= a.tc) {
+        const int grid = (SHARED ? cdiv(a.n_tokens, a.tc) : a.max_chunks) * cdiv(a.hidden, a.mx_rt_d);
+        hipLaunchKernelGGL((k_mx_down<TY, SHARED>), dim3(grid), dim3(MX_THREADS), 0, s, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return a.mx_min > 1 ? down_typed<TY, SHARED>(a, lds, s) : hipSuccess;
+}
+
 template <bool SHARED>
 static hipError_t gate_up_any(int ty, const BatchArgs &a, int lds, hipStream_t s) {
     switch (ty) {
-    case T_IQ2_S: return gate_up_typed<T_IQ2_S, SHARED>(a, lds, s);
+    case T_IQ2_S: return a.mx ? mx_gate_up_typed<T_IQ2_S, SHARED>(a, lds, s) : gate_up_typed<T_IQ2_S, SHARED>(a, lds, s);
     case T_Q4_K: return gate_up_typed<T_Q4_K, SHARED>(a, lds, s);
     default: return hipErrorInvalidValue;
     }
@@ -751,8 +1130,8 @@ static hipError_t gate_up_any(int ty, const BatchArgs &a, int lds, hipStream_t s
 template <bool SHARED>
 static hipError_t down_any(int ty, const BatchArgs &a, int lds, hipStream_t s) {
     switch (ty) {
-    case T_IQ2_S: return down_typed<T_IQ2_S, SHARED>(a, lds, s);
-    case T_IQ3_S: return down_typed<T_IQ3_S, SHARED>(a, lds, s);
+    case T_IQ2_S: return a.mx ? mx_down_typed<T_IQ2_S, SHARED>(a, lds, s) : down_typed<T_IQ2_S, SHARED>(a, lds, s);
+    case T_IQ3_S: return a.mx ? mx_down_typed<T_IQ3_S, SHARED>(a, lds, s) : down_typed<T_IQ3_S, SHARED>(a, lds, s);
     case T_Q5_K: return down_typed<T_Q5_K, SHARED>(a, lds, s);
     default: return hipErrorInvalidValue;
     }

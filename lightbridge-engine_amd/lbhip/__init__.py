@@ -117,6 +117,7 @@ def lib() -> C.CDLL:
             "lbh_gemm_workspace_bytes": ([sz, sz], sz),
             "lbh_gemm_q8_k": ([p, p, p, sz, p, p, sz], i32),
             "lbh_moe_set_batch_tiles": ([p, i32, i32, i32, i32, i32], i32),
+            "lbh_moe_set_batch_engine": ([p, i32, i32, i32], i32),
             "lbh_moe_forward_batch": ([p, p, p, p, sz, sz, p, p], i32),
             "lbh_moe_routed_by_id_batch_into": ([p, p, p, p, sz, sz, p, sz, p, sz, E], i32),
             "lbh_route_experts_batch": ([p, p, sz, sz, sz, i32, C.c_float, p, p, p], i32),
@@ -401,6 +402,14 @@ class MoeLayer:
                         rows_gate_up_shared: int = 128, rows_down_routed: int = 320, rows_down_shared: int = 128) -> None:
         st = lib().lbh_moe_set_batch_tiles(self.handle, tokens_per_chunk, rows_gate_up_routed, rows_gate_up_shared,
                                            rows_down_routed, rows_down_shared)
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def set_batch_engine(self, mx_min_tokens: int = 5, mx_rows_gate_up: int = 0, mx_rows_down: int = 0) -> None:
+        """Batched IQ chunks of at least mx_min_tokens tokens on the matrix cores, the
+        rest on the VALU dot4 path (0: all on the VALU); resets the batch launch shapes
+        to their defaults."""
+        st = lib().lbh_moe_set_batch_engine(self.handle, mx_min_tokens, mx_rows_gate_up, mx_rows_down)
         if st:
             raise KernelError(LbhError(status=st))
 

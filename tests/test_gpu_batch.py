@@ -111,6 +111,22 @@ def test_batch_launch_shapes_give_the_same_bits(be, oracle, small, tiles):
     assert all(_same(got[t], want[t]) for t in range(21))
 
 
+@pytest.mark.parametrize("engine", [(0, 0, 0), (1, 0, 0), (5, 0, 0), (3, 32, 48), (16, 16, 16)])
+def test_batch_engines_bit_exact(be, oracle, small, engine):
+    """The IQ streams on the VALU integer dots (0), all chunks on the f16 matrix
+    cores (1), the per-chunk split at several thresholds and row tiles, with hot
+    experts past one 16-token chunk and single-token experts."""
+    _, ids, coefs = zipf_routing(oracle, 40, 12, 4, seed=15)
+    xs = np.random.default_rng(16).standard_normal((40, 512)).astype(np.float32)
+    want = oracle_batch(oracle, small, ids, coefs, xs)
+    small.moe.set_batch_engine(*engine)
+    try:
+        got = run_checked(be, small, ids, coefs, xs)
+    finally:
+        small.moe.set_batch_engine()
+    assert all(_same(got[t], want[t]) for t in range(40))
+
+
 @pytest.mark.parametrize("types", [(IQ2_S, IQ3_S, IQ2_S, IQ3_S), (IQ2_S, IQ2_S, IQ2_S, IQ2_S),
                                    (IQ2_S, IQ2_S, IQ2_S, IQ3_S)])
 def test_batch_type_sets(be, oracle, types):
