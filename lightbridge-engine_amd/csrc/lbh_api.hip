@@ -524,7 +524,7 @@ namespace {
 // Batched launch shapes measured on MI355X at the configs[3] shapes (64 tokens,
 // hidden 4096, routed ffn 1536): with the matrix cores on, chunks of 16 tokens
 // (one instruction's width); the VALU streams alone do best with chunks of 8.
-constexpr int MX_MIN_DEFAULT = 5;
+constexpr int MX_MIN_DEFAULT = 6;
 void set_batch_defaults(lbh_moe *m, int mx_min) {
     m->mx_min = mx_min;
     m->mx_rt_gu = 64, m->mx_rt_d = 128;

@@ -719,6 +719,11 @@ typedef uint32_t mx_u4 __attribute__((ext_vector_type(4)));
 
 constexpr int MX_THREADS = 256;
 constexpr int MX_WAVES = MX_THREADS / 64;
+// Steps in flight per wave (measured on MI355X at the configs[3] shapes: 2
+// beats 3 and 4, whose extra loads crowd the vector L1, each 16-row step
+// touching about 16 cache lines per load instruction).
+constexpr int MX_DEPTH_GU = 2;
+constexpr int MX_DEPTH_D = 2;
 
 // LDS tables: the f16 magnitudes of every codebook entry (IQ2_S 1024 x 8,
 // IQ3_S 512 x 4), then 256 sign masks of eight f16 (bit 15 of element i is
@@ -829,7 +834,7 @@ struct MxStep {
 // (table fill, ended by a workgroup barrier); then each step's loads are in
 // flight while the one before is computed.  out(token column, row, values)
 // is called by every lane for its four (row, token) results of each tile.
-template <int TY, int NM, class Prologue, class Out>
+template <int TY, int NM, int D, class Prologue, class Out>
 __device__ __forceinline__ void mx_rows(const MatView (&mv)[NM], int r0, int r1, int nb, const uint8_t *bq,
                                         const float *bd, const uint8_t *tab, Prologue prologue, Out out) {
     const int lane = threadIdx.x & 63;
@@ -914,15 +919,20 @@ __device__ __forceinline__ void mx_rows(const MatView (&mv)[NM], int r0, int r1,
             }
         }
     };
-    MxStep<TY, NM> sa, sb;
-    issue(0, sa);
+    // Ring of D steps, unrolled D times so the buffers rotate without copies:
+    // while step s is computed, the loads of steps s + 1 .. s + D - 1 are in
+    // flight; the buffer just consumed is refilled with step s + D.
+    MxStep<TY, NM> st[D];
+    issue(0, st[0]);
     prologue();
-    for (int s = 0; s < steps; s += 2) {
-        issue(s + 1, sb);
-        process(s, sa);
-        if (s + 1 >= steps) break;
-        issue(s + 2, sa);
-        process(s + 1, sb);
+#pragma unroll
+    for (int d = 1; d < D; ++d) issue(d, st[d]);
+    for (int s = 0; s < steps; s += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (s + d < steps) process(s + d, st[d]);
+            issue(s + d + D, st[d]);
+        }
     }
 }
 
@@ -952,7 +962,7 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
     const int c = (int)(threadIdx.x & 15) < n ? (int)(threadIdx.x & 15) : n - 1;
     const long long tok = SHARED ? (long long)(p0 + c) : (long long)a.pair_token[p0 + c];
     float *h = SHARED ? a.h_s : a.h_r;
-    mx_rows<TY, 2>(
+    mx_rows<TY, 2, MX_DEPTH_GU>(
         mv, r0, r1, nb, a.xq_mx + tok * nb * 256, a.xd_mx + tok * nb, tab,
         [&]() {
             mx_fill<TY>(tab);
@@ -990,7 +1000,7 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_down(BatchArgs a) {
     const uint8_t *bq = (SHARED ? a.hq_mx_s : a.hq_mx_r) + row * nb * 256;
     const float *bd = (SHARED ? a.hd_mx_s : a.hd_mx_r) + row * nb;
     float *d = SHARED ? a.d_s : a.d_r;
-    mx_rows<TY, 1>(
+    mx_rows<TY, 1, MX_DEPTH_D>(
         mv, r0, r1, nb, bq, bd, tab,
         [&]() {
             mx_fill<TY>(tab);
