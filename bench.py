@@ -57,7 +57,7 @@ BATCH_TOKENS = 64
 # HBM bytes per launch (read + write) measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain copy of
 # known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2384059 + 6144, "down": 2981354 + 19648, "prefill": 324295660 + 25175088}
+MEASURED_TRAFFIC = {"gate": 2384040 + 6144, "down": 2981326 + 19648, "prefill": 324282199 + 25177968}
 
 
 def parse():
@@ -603,6 +603,11 @@ def cpu_prefill(check, seconds):
                       f"{threads} threads; the full 512-token step would take {512 * el / n:.2f} s"}
 
 
+def _progress(msg):
+    """One line on stderr per finished leg (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def pmc_workloads():
     """A few dispatches of every hot-path kernel at the bench shapes, for the
     rocprofv3 --pmc passes (one counter set per run), plus a plain 64 MiB copy
@@ -693,16 +698,24 @@ def main():
     timer = Timer(torch, stream)
 
     mv = bench_matvec_step(args, be, timer, torch, np, synth)
+    _progress(f"configs[1] step {mv['ms_per_step'] * 1e3:.2f} us")
     w_q4k, q4k = bench_q4k(args, be, timer, torch, np, synth)
+    _progress(f"configs[0] {q4k['us_per_matvec']} us")
     model_mv = bench_model_shapes(args, be, timer, torch, np, synth)
+    _progress("model shapes done")
     ingest = bench_ingest(args, be, torch, np, synth, lbhip)
+    _progress("gguf ingest done")
     moe = state = batch = batch_check = streaming = None
     prefill, pf_check = bench_prefill(args, be, timer, torch, np, synth)
+    _progress(f"configs[4] {prefill['us_per_step']} us")
     if not args.no_moe:
         moe, state = bench_moe(args, be, timer, torch, np, synth, lbhip)
+        _progress("configs[2] done")
         batch, batch_check = bench_batch(args, be, timer, torch, np, synth, state)
+        _progress(f"configs[3] {batch['us_per_step']} us")
         if args.stream_tokens > 0:
             streaming = bench_streaming(args, be, torch, np, synth, lbhip, state)
+            _progress("expert streaming done")
 
     value = STEP_BYTES / (mv["ms_per_step"] * 1e-3) / 1e9
     if mv["down_us"] >= mv["gate_us"]:
@@ -745,7 +758,9 @@ def main():
     if streaming is not None:
         line["expert_streaming"] = streaming
     if not args.no_cpu:
+        _progress("CPU baselines")
         line["cpu_baseline"] = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds)
+        _progress("CPU configs[1] done")
         cq = cpu_q4k(w_q4k, args.cpu_seconds / 2)
         q4k["cpu_baseline"] = cq
         q4k["speedup_vs_cpu"] = round(q4k["GB/s"] / cq["value"], 1)
@@ -754,9 +769,11 @@ def main():
             moe["cpu_baseline"] = cm
             moe["speedup_vs_cpu"] = round(moe["with_device_router"]["tokens_per_s"] / cm["value"], 1)
             moe["speedup_vs_cpu_routing_given"] = round(moe["routing_given"]["tokens_per_s"] / cm["value"], 1)
+            _progress("CPU configs[2] done")
             cb = cpu_batch(state["experts_np"], state["shared_np"], batch_check, args.cpu_seconds / 2)
             batch["cpu_baseline"] = cb
             batch["speedup_vs_cpu"] = round(batch["tokens_per_s"] / cb["value"], 1)
+        _progress("CPU configs[3] done")
         cp = cpu_prefill(pf_check, args.cpu_seconds / 2)
         prefill["cpu_baseline"] = cp
         prefill["speedup_vs_cpu"] = round(prefill["dot_TOPS"] / cp["value"], 1)
