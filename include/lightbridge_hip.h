@@ -272,7 +272,8 @@ lbh_status lbh_moe_set_batch_tiles(lbh_moe *moe, int32_t tokens_per_chunk, int32
  * whose batch is a loop over tokens).  Chunks of at least mx_min_tokens tokens
  * (1..16; default 6) run on the f16 matrix cores, one 16-row x 16-token product
  * per codebook step, with mx_rows_gate_up / mx_rows_down rows per workgroup
- * (0: default); smaller chunks run on the VALU integer dots; mx_min_tokens = 0
+ * (16, 32 or 64; 0: the defaults 16 and 32); smaller chunks run on the VALU
+ * integer dots; mx_min_tokens = 0
  * keeps every chunk on the VALU.  Every choice gives the same bits.  Resets the
  * tokens per chunk (16 with the matrix cores, 8 without) and the VALU row tiles
  * to their defaults. */

@@ -514,7 +514,7 @@ struct lbh_moe {
     int32_t *plan_host;       // pinned
     int tc, rt_gu_r, rt_gu_s, rt_d_r, rt_d_s;
     int mx_min;               // batched IQ chunks of >= mx_min tokens on the matrix cores (0: none)
-    int mx_rt_gu, mx_rt_d;    // their rows per workgroup
+    int mx_split_gu, mx_split_d;   // waves sharing a 16-row tile of those streams (1, 2, 4)
     uint8_t *shared_gemm_mem; // MFMA-ready copies of a K-quant shared expert (batched calls)
     size_t gemm_off[3];       // A offsets of gate, up, down in shared_gemm_mem
 };
@@ -527,7 +527,7 @@ namespace {
 constexpr int MX_MIN_DEFAULT = 6;
 void set_batch_defaults(lbh_moe *m, int mx_min) {
     m->mx_min = mx_min;
-    m->mx_rt_gu = 64, m->mx_rt_d = 128;
+    m->mx_split_gu = 4, m->mx_split_d = 2;
     m->tc = mx_min > 0 ? 16 : 8;
     m->rt_gu_r = 64, m->rt_gu_s = 64, m->rt_d_r = 160, m->rt_d_s = 64;
 }
@@ -985,8 +985,8 @@ BatchArgs batch_args(const lbh_moe *m, const uint32_t *ids, const float *coefs, 
     a.type_down_r = m->type_down_r;
     a.mx = m->mx_min > 0 ? 1 : 0;
     a.mx_min = m->mx_min > 0 ? m->mx_min : BATCH_MAX_TC + 1;
-    a.mx_rt_gu = m->mx_rt_gu;
-    a.mx_rt_d = m->mx_rt_d;
+    a.mx_split_gu = m->mx_split_gu;
+    a.mx_split_d = m->mx_split_d;
     a.vc = a.mx ? (a.tc < a.mx_min - 1 ? a.tc : a.mx_min - 1) : a.tc;
     if (a.vc < 1) a.vc = 1;
     return a;
@@ -1137,13 +1137,13 @@ lbh_status lbh_moe_set_batch_tiles(lbh_moe *m, int32_t tokens_per_chunk, int32_t
 lbh_status lbh_moe_set_batch_engine(lbh_moe *m, int32_t mx_min_tokens, int32_t mx_rows_gate_up,
                                     int32_t mx_rows_down) {
     if (!m) return LBH_NULL_ARGUMENT;
-    if (mx_min_tokens < 0 || mx_min_tokens > BATCH_MAX_TC || mx_rows_gate_up < 0 || mx_rows_gate_up > 65536 ||
-        mx_rows_down < 0 || mx_rows_down > 65536)
+    auto rows_ok = [](int32_t r) { return r == 0 || r == 16 || r == 32 || r == 64; };
+    if (mx_min_tokens < 0 || mx_min_tokens > BATCH_MAX_TC || !rows_ok(mx_rows_gate_up) || !rows_ok(mx_rows_down))
         return LBH_INVALID_PARAMETER;
     const lbh_moe saved = *m;
     set_batch_defaults(m, mx_min_tokens);
-    if (mx_rows_gate_up) m->mx_rt_gu = mx_rows_gate_up;
-    if (mx_rows_down) m->mx_rt_d = mx_rows_down;
+    if (mx_rows_gate_up) m->mx_split_gu = 64 / mx_rows_gate_up;
+    if (mx_rows_down) m->mx_split_d = 64 / mx_rows_down;
     const BatchArgs probe = batch_args(m, nullptr, nullptr, 1, 1, nullptr, nullptr);
     for (int st = 0; st < 5; ++st)
         if (batch_lds_bytes(probe, st) > 160 * 1024) {

@@ -719,15 +719,11 @@ typedef uint32_t mx_u4 __attribute__((ext_vector_type(4)));
 
 constexpr int MX_THREADS = 256;
 constexpr int MX_WAVES = MX_THREADS / 64;
-// Steps in flight per wave (measured on MI355X at the configs[3] shapes: 2
-// beats 3 and 4, whose extra loads crowd the vector L1, each 16-row step
-// touching about 16 cache lines per load instruction).
-constexpr int MX_DEPTH_GU = 2;
-constexpr int MX_DEPTH_D = 2;
+
 
 // LDS tables: the f16 magnitudes of every codebook entry (IQ2_S 1024 x 8,
 // IQ3_S 512 x 4), then 256 sign masks of eight f16 (bit 15 of element i is
-// bit i of the sign byte).
+// bit i of the sign byte); built at compile time, copied to LDS per workgroup.
 template <int TY>
 struct MxTab {
     static constexpr int ENTRY = TY == T_IQ2_S ? 16 : 8;
@@ -735,36 +731,53 @@ struct MxTab {
     static constexpr int BYTES = GRID + 256 * 16;
 };
 
+// f16 bits of a non-negative integer below 2048 (exact).
+constexpr uint32_t f16_bits_of(uint32_t v) {
+    if (v == 0) return 0;
+    int e = 0;
+    while ((v >> (e + 1)) != 0) ++e;
+    return ((uint32_t)(e + 15) << 10) | ((v << (10 - e)) & 0x3ffu);
+}
+
+constexpr uint64_t k_iq2s_vals[1024] = {LBH_IQ2S_GRID_VALUES};
+constexpr uint32_t k_iq3s_vals[512] = {LBH_IQ3S_GRID_VALUES};
+
+struct MxTables {
+    uint32_t iq2[1024][4];
+    uint32_t iq3[512][2];
+    uint32_t sign[256][4];
+};
+
+constexpr uint32_t f16_pair_of(uint32_t lo, uint32_t hi) { return f16_bits_of(lo) | (f16_bits_of(hi) << 16); }
+
+constexpr MxTables make_mx_tables() {
+    MxTables t{};
+    for (int i = 0; i < 1024; ++i)
+        for (int k = 0; k < 4; ++k)
+            t.iq2[i][k] = f16_pair_of((uint32_t)(k_iq2s_vals[i] >> (16 * k)) & 0xffu,
+                                      (uint32_t)(k_iq2s_vals[i] >> (16 * k + 8)) & 0xffu);
+    for (int i = 0; i < 512; ++i)
+        for (int k = 0; k < 2; ++k)
+            t.iq3[i][k] = f16_pair_of((k_iq3s_vals[i] >> (16 * k)) & 0xffu, (k_iq3s_vals[i] >> (16 * k + 8)) & 0xffu);
+    for (uint32_t v = 0; v < 256; ++v)
+        for (int k = 0; k < 4; ++k)
+            t.sign[v][k] = (((v >> (2 * k)) & 1u) << 15) | (((v >> (2 * k + 1)) & 1u) << 31);
+    return t;
+}
+
+static __constant__ MxTables c_mx_tab = make_mx_tables();
+
 __device__ __forceinline__ uint32_t mx_bits(mx_h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ mx_h2 mx_pair(uint32_t v) { return __builtin_bit_cast(mx_h2, v); }
 
-// Bytes i, i + 1 of v as an f16 pair.
-__device__ __forceinline__ uint32_t mx_f16_bytes(uint32_t v, int i) {
-    return mx_bits(mx_h2{(_Float16)(float)byte_of(v, i), (_Float16)(float)byte_of(v, i + 1)});
-}
-
+// Copies TY's tables into LDS (all threads; the caller synchronises).
 template <int TY>
 __device__ __forceinline__ void mx_fill(uint8_t *tab) {
-    if constexpr (TY == T_IQ2_S) {
-        for (int i = threadIdx.x; i < 1024; i += MX_THREADS) {
-            const uint64_t v = c_iq2s_grid[i];
-            const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-            reinterpret_cast<uint4 *>(tab)[i] =
-                make_uint4(mx_f16_bytes(lo, 0), mx_f16_bytes(lo, 2), mx_f16_bytes(hi, 0), mx_f16_bytes(hi, 2));
-        }
-    } else {
-        for (int i = threadIdx.x; i < 512; i += MX_THREADS) {
-            const uint32_t v = c_iq3s_grid[i];
-            reinterpret_cast<uint2 *>(tab)[i] = make_uint2(mx_f16_bytes(v, 0), mx_f16_bytes(v, 2));
-        }
-    }
-    for (int s = threadIdx.x; s < 256; s += MX_THREADS) {
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            w[k] = ((((uint32_t)s >> (2 * k)) & 1u) << 15) | ((((uint32_t)s >> (2 * k + 1)) & 1u) << 31);
-        reinterpret_cast<uint4 *>(tab + MxTab<TY>::GRID)[s] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    const uint4 *g = reinterpret_cast<const uint4 *>(TY == T_IQ2_S ? &c_mx_tab.iq2[0][0] : &c_mx_tab.iq3[0][0]);
+    const uint4 *sg = reinterpret_cast<const uint4 *>(&c_mx_tab.sign[0][0]);
+    uint4 *o = reinterpret_cast<uint4 *>(tab);
+    for (int i = threadIdx.x; i < MxTab<TY>::GRID / 16; i += MX_THREADS) o[i] = g[i];
+    for (int i = threadIdx.x; i < 256; i += MX_THREADS) o[MxTab<TY>::GRID / 16 + i] = sg[i];
 }
 
 // Eight f16 magnitudes with their signs applied, times the integer scale ls.
@@ -828,18 +841,33 @@ struct MxStep {
     float d8;
 };
 
-// Rows [r0, r1) of NM matrices (K = 256 nb) against the chunk's tokens: wave w
-// takes the 16-row tiles w, w + MX_WAVES, ...; lane l's token column holds the
-// operand row bq / bd.  The first step's loads are issued before `prologue`
-// (table fill, ended by a workgroup barrier); then each step's loads are in
-// flight while the one before is computed.  out(token column, row, values)
-// is called by every lane for its four (row, token) results of each tile.
-template <int TY, int NM, int D, class Prologue, class Out>
-__device__ __forceinline__ void mx_rows(const MatView (&mv)[NM], int r0, int r1, int nb, const uint8_t *bq,
-                                        const float *bd, const uint8_t *tab, Prologue prologue, Out out) {
+// LDS of a matrix-core stream workgroup: the tables, then per tile the
+// per-block f32 terms [matrix][block][token][row].
+__host__ __device__ constexpr int mx_lds_bytes(int ty, int nm, int split, int nb) {
+    return (ty == T_IQ2_S ? MxTab<T_IQ2_S>::BYTES : MxTab<T_IQ3_S>::BYTES) + (MX_WAVES / split) * nm * nb * 256 * 4;
+}
+
+// Rows [r0, r1) (r1 - r0 <= 16 * MX_WAVES / S) of NM matrices (K = 256 nb)
+// against the chunk's tokens.  The workgroup holds MX_WAVES / S tiles of 16
+// rows; the S waves of a tile take its blocks j, j + S, ...: together they
+// read S consecutive blocks of each row (adjacent 16-byte pieces of the same
+// lines) per step.  Each wave writes the f32 term (d * d8) * (float)bsum of
+// each (row, token, block) it computes to LDS; after a workgroup barrier one
+// thread per (tile, token, row) folds its terms in block order (lbh_rows.h:
+// chain = 0 + t_0 + t_1 + ...; IQ2_S result = 0.125 * chain) and calls
+// out(token column, row, values).  Lane l's token column holds the operand
+// row bq / bd.  The first step's loads are issued before `prologue` (table
+// fill, ended by a workgroup barrier); then each step's loads are in flight
+// while the one before is computed.
+template <int TY, int NM, int S, class Prologue, class Out>
+__device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1, int nb, const uint8_t *bq,
+                                         const float *bd, const uint8_t *tab, float *terms, Prologue prologue, Out out) {
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q = lane >> 4;
+    const int tl = wid / S, j = wid - tl * S;
+    const int rt0 = r0 + 16 * tl;
+    const int steps = rt0 < r1 && j < nb ? (nb - j + S - 1) / S : 0;
     Planes P[NM];
     uint32_t po[NM];
 #pragma unroll
@@ -847,33 +875,26 @@ __device__ __forceinline__ void mx_rows(const MatView (&mv)[NM], int r0, int r1,
         P[t] = make_planes(mv[t].planes, mv[t].units, mv[t].bytes);
         po[t] = part_offset<TY, 4>(P[t], q);
     }
-    const int ntile = (r1 - r0 + 15) >> 4;
-    const int mine = ntile > wid ? (ntile - wid + MX_WAVES - 1) / MX_WAVES : 0;
-    const int steps = mine * nb;
-    // Rows past r1 load the last row (every register defined; not stored).
-    // The loads are unconditional: a step past the wave's last one reloads the
-    // last step (in bounds, never used), so the compiler's wait before a step's
-    // use counts exactly the younger step's loads instead of draining them.
+    // Rows past r1 load the last row (every register defined; never output).
+    int r = rt0 + c;
+    r = r < r1 ? r : r1 - 1;
+    // The loads are unconditional: a step past the wave's last one reloads a
+    // block of the row (in bounds, never used), so the compiler's wait before
+    // a step's use counts exactly the younger step's loads.
     auto issue = [&](int s, MxStep<TY, NM> &st) {
-        const int sc = s < steps ? s : (steps > 0 ? steps - 1 : 0);
-        const int k = sc / nb, b = sc - k * nb;
-        int r = r0 + 16 * (wid + MX_WAVES * k) + c;
-        r = r < r1 ? r : r1 - 1;
+        int b = j + S * (s < steps ? s : steps - 1);
+        b = b < 0 ? 0 : b < nb ? b : nb - 1;
 #pragma unroll
         for (int t = 0; t < NM; ++t) load_slice(P[t], (uint32_t)(r * nb + b), po[t], q, st.w[t]);
         const uint4 *src = reinterpret_cast<const uint4 *>(bq + b * 256 + 64 * q);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st.bq[j] = src[j];
+        for (int k = 0; k < 4; ++k) st.bq[k] = src[k];
         st.d8 = bd[b];
     };
-    float ch[NM][4];
-#pragma unroll
-    for (int t = 0; t < NM; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ch[t][i] = 0.0f;
+    float *tt = terms + tl * NM * nb * 256;
     auto process = [&](int s, const MxStep<TY, NM> &st) {
         constexpr int CH = mx_chain<TY>();
-        const int k = s / nb, b = s - k * nb;
+        const int b = j + S * s;
         int32_t bs[NM][4];
         mx_f4 acc[NM];
 #pragma unroll
@@ -899,50 +920,48 @@ __device__ __forceinline__ void mx_rows(const MatView (&mv)[NM], int r0, int r1,
 #pragma unroll
         for (int t = 0; t < NM; ++t) {
             const float da = f16_to_f32(st.w[t].d);
+            float *o = tt + ((t * nb + b) * 16 + c) * 16 + 4 * q;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float dr = __shfl(da, 4 * q + i, 64);
-                ch[t][i] = __fadd_rn(ch[t][i], __fmul_rn(__fmul_rn(dr, st.d8), (float)bs[t][i]));
-            }
-        }
-        if (b == nb - 1) {
-            const int rt0 = r0 + 16 * (wid + MX_WAVES * k);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float res[NM];
-#pragma unroll
-                for (int t = 0; t < NM; ++t) {
-                    res[t] = TY == T_IQ2_S ? __fmul_rn(0.125f, ch[t][i]) : ch[t][i];  // q8_k.rs:369
-                    ch[t][i] = 0.0f;
-                }
-                out(c, rt0 + 4 * q + i, res);
+                o[i] = __fmul_rn(__fmul_rn(dr, st.d8), (float)bs[t][i]);
             }
         }
     };
-    // Ring of D steps, unrolled D times so the buffers rotate without copies:
-    // while step s is computed, the loads of steps s + 1 .. s + D - 1 are in
-    // flight; the buffer just consumed is refilled with step s + D.
-    MxStep<TY, NM> st[D];
-    issue(0, st[0]);
+    MxStep<TY, NM> sa, sb;
+    issue(0, sa);
     prologue();
+    for (int s = 0; s < steps; s += 2) {
+        issue(s + 1, sb);
+        process(s, sa);
+        if (s + 1 >= steps) break;
+        issue(s + 2, sa);
+        process(s + 1, sb);
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < (MX_WAVES / S) * 256; p += MX_THREADS) {
+        const int ptl = p >> 8, cc = (p >> 4) & 15, row = p & 15;
+        const float *src = terms + ptl * NM * nb * 256 + cc * 16 + row;
+        float res[NM];
 #pragma unroll
-    for (int d = 1; d < D; ++d) issue(d, st[d]);
-    for (int s = 0; s < steps; s += D) {
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (s + d < steps) process(s + d, st[d]);
-            issue(s + d + D, st[d]);
+        for (int t = 0; t < NM; ++t) {
+            float ch = 0.0f;
+            for (int b = 0; b < nb; ++b) ch = __fadd_rn(ch, src[(t * nb + b) * 256]);
+            res[t] = TY == T_IQ2_S ? __fmul_rn(0.125f, ch) : ch;  // q8_k.rs:369
         }
+        out(cc, r0 + 16 * ptl + row, res);
     }
 }
 
 // Gate/up + SwiGLU on the matrix cores (as k_mb_gate_up): workgroup (chunk, row tile).
-template <int TY, bool SHARED>
+template <int TY, bool SHARED, int S>
 __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
-    __shared__ __align__(16) uint8_t tab[MxTab<TY>::BYTES];
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *tab = smem;
+    float *terms = reinterpret_cast<float *>(smem + MxTab<TY>::BYTES);
     if (a.plan[1]) return;
     const int nb = a.hidden / 256;
-    const int ffn = SHARED ? a.ffn_s : a.ffn_r, rt = a.mx_rt_gu;
+    const int ffn = SHARED ? a.ffn_s : a.ffn_r, rt = 16 * MX_WAVES / S;
     const int tiles = (ffn + rt - 1) / rt;
     const int ci = blockIdx.x / tiles, tile = blockIdx.x - ci * tiles;
     const int r0 = tile * rt, r1 = r0 + rt < ffn ? r0 + rt : ffn;
@@ -962,8 +981,8 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
     const int c = (int)(threadIdx.x & 15) < n ? (int)(threadIdx.x & 15) : n - 1;
     const long long tok = SHARED ? (long long)(p0 + c) : (long long)a.pair_token[p0 + c];
     float *h = SHARED ? a.h_s : a.h_r;
-    mx_rows<TY, 2, MX_DEPTH_GU>(
-        mv, r0, r1, nb, a.xq_mx + tok * nb * 256, a.xd_mx + tok * nb, tab,
+    mx_tiles<TY, 2, S>(
+        mv, r0, r1, nb, a.xq_mx + tok * nb * 256, a.xd_mx + tok * nb, tab, terms,
         [&]() {
             mx_fill<TY>(tab);
             __syncthreads();
@@ -974,12 +993,14 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
 }
 
 // Down on the matrix cores (as k_mb_down).
-template <int TY, bool SHARED>
+template <int TY, bool SHARED, int S>
 __global__ void __launch_bounds__(MX_THREADS) k_mx_down(BatchArgs a) {
-    __shared__ __align__(16) uint8_t tab[MxTab<TY>::BYTES];
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *tab = smem;
+    float *terms = reinterpret_cast<float *>(smem + MxTab<TY>::BYTES);
     if (a.plan[1]) return;
     const int nb = (SHARED ? a.ffn_s : a.ffn_r) / 256;
-    const int rt = a.mx_rt_d;
+    const int rt = 16 * MX_WAVES / S;
     const int tiles = (a.hidden + rt - 1) / rt;
     const int ci = blockIdx.x / tiles, tile = blockIdx.x - ci * tiles;
     const int r0 = tile * rt, r1 = r0 + rt < a.hidden ? r0 + rt : a.hidden;
@@ -1000,8 +1021,8 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_down(BatchArgs a) {
     const uint8_t *bq = (SHARED ? a.hq_mx_s : a.hq_mx_r) + row * nb * 256;
     const float *bd = (SHARED ? a.hd_mx_s : a.hd_mx_r) + row * nb;
     float *d = SHARED ? a.d_s : a.d_r;
-    mx_rows<TY, 1, MX_DEPTH_D>(
-        mv, r0, r1, nb, bq, bd, tab,
+    mx_tiles<TY, 1, S>(
+        mv, r0, r1, nb, bq, bd, tab, terms,
         [&]() {
             mx_fill<TY>(tab);
             __syncthreads();
@@ -1063,6 +1084,15 @@ static int stream_lds_of(int ty, int nm, int tc, int nb) {
     }
 }
 
+// LDS of the launches of one stream: the VALU kernel's, and the matrix-core
+// kernel's when it runs that type.
+static int stream_max(const BatchArgs &a, int ty, int nm, int nb, int split) {
+    const int v = stream_lds_of(ty, nm, valu_cap(a, ty), nb);
+    if (!a.mx || (ty != T_IQ2_S && ty != T_IQ3_S)) return v;
+    const int m = mx_lds_bytes(ty, nm, split < 1 ? 1 : split, nb);
+    return v > m ? v : m;
+}
+
 // stage 0: sort + quantize; 1/2: routed / shared gate-up; 3/4: routed / shared down.
 int batch_lds_bytes(const BatchArgs &a, int stage) {
     const int nbh = a.hidden / 256, nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
@@ -1072,10 +1102,10 @@ int batch_lds_bytes(const BatchArgs &a, int stage) {
         const int sort = (a.n_experts * W + 3 * a.n_experts + 2 * MB_THREADS + 4) * 4;
         return sort > MB_WAVES * 4 * 292 ? sort : MB_WAVES * 4 * 292;
     }
-    case 1: return stream_lds_of(a.type_gate_r, 2, valu_cap(a, a.type_gate_r), nbh);
-    case 2: return a.has_shared ? stream_lds_of(a.shared.gate.type, 2, valu_cap(a, a.shared.gate.type), nbh) : 0;
-    case 3: return stream_lds_of(a.type_down_r, 1, valu_cap(a, a.type_down_r), nbr);
-    default: return a.has_shared ? stream_lds_of(a.shared.down.type, 1, valu_cap(a, a.shared.down.type), nbs) : 0;
+    case 1: return stream_max(a, a.type_gate_r, 2, nbh, a.mx_split_gu);
+    case 2: return a.has_shared ? stream_max(a, a.shared.gate.type, 2, nbh, a.mx_split_gu) : 0;
+    case 3: return stream_max(a, a.type_down_r, 1, nbr, a.mx_split_d);
+    default: return a.has_shared ? stream_max(a, a.shared.down.type, 1, nbs, a.mx_split_d) : 0;
     }
 }
 
@@ -1106,12 +1136,38 @@ static hipError_t down_typed(const BatchArgs &a, int lds, hipStream_t s) {
 // An IQ stream with the matrix cores on: the matrix-core launch when some
 // chunk can reach mx_min tokens, then the VALU launch when some chunk can stay
 // below it (each kernel returns early on the other's chunks).
+template <int TY, bool SHARED, int S>
+static hipError_t mx_gate_up_split(const BatchArgs &a, hipStream_t s) {
+    const int nb = a.hidden / 256;
+    const int lds = mx_lds_bytes(TY, 2, S, nb);
+    hipError_t e = allow_lds(k_mx_gate_up<TY, SHARED, S>, lds);
+    if (e != hipSuccess) return e;
+    const int grid = (SHARED ? cdiv(a.n_tokens, a.tc) : a.max_chunks) * cdiv(SHARED ? a.ffn_s : a.ffn_r, 16 * MX_WAVES / S);
+    hipLaunchKernelGGL((k_mx_gate_up<TY, SHARED, S>), dim3(grid), dim3(MX_THREADS), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int TY, bool SHARED, int S>
+static hipError_t mx_down_split(const BatchArgs &a, hipStream_t s) {
+    const int nb = (SHARED ? a.ffn_s : a.ffn_r) / 256;
+    const int lds = mx_lds_bytes(TY, 1, S, nb);
+    hipError_t e = allow_lds(k_mx_down<TY, SHARED, S>, lds);
+    if (e != hipSuccess) return e;
+    const int grid = (SHARED ? cdiv(a.n_tokens, a.tc) : a.max_chunks) * cdiv(a.hidden, 16 * MX_WAVES / S);
+    hipLaunchKernelGGL((k_mx_down<TY, SHARED, S>), dim3(grid), dim3(MX_THREADS), lds, s, a);
+    return hipGetLastError();
+}
+
+// An IQ stream with the matrix cores on: the matrix-core launch when some
+// chunk can reach mx_min tokens, then the VALU launch when some chunk can stay
+// below it (each kernel returns early on the other's chunks).  mx_split_* is
+// the number of waves that share a 16-row tile (1, 2 or 4).
 template <int TY, bool SHARED>
 static hipError_t mx_gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
     if (a.mx_min <= a.tc) {
-        const int grid = (SHARED ? cdiv(a.n_tokens, a.tc) : a.max_chunks) * cdiv(SHARED ? a.ffn_s : a.ffn_r, a.mx_rt_gu);
-        hipLaunchKernelGGL((k_mx_gate_up<TY, SHARED>), dim3(grid), dim3(MX_THREADS), 0, s, a);
-        const hipError_t e = hipGetLastError();
+        const hipError_t e = a.mx_split_gu == 4   ? mx_gate_up_split<TY, SHARED, 4>(a, s)
+                             : a.mx_split_gu == 2 ? mx_gate_up_split<TY, SHARED, 2>(a, s)
+                                                  : mx_gate_up_split<TY, SHARED, 1>(a, s);
         if (e != hipSuccess) return e;
     }
     return a.mx_min > 1 ? gate_up_typed<TY, SHARED>(a, lds, s) : hipSuccess;
@@ -1120,9 +1176,9 @@ static hipError_t mx_gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
 template <int TY, bool SHARED>
 static hipError_t mx_down_typed(const BatchArgs &a, int lds, hipStream_t s) {
     if (a.mx_min <= a.tc) {
-        const int grid = (SHARED ? cdiv(a.n_tokens, a.tc) : a.max_chunks) * cdiv(a.hidden, a.mx_rt_d);
-        hipLaunchKernelGGL((k_mx_down<TY, SHARED>), dim3(grid), dim3(MX_THREADS), 0, s, a);
-        const hipError_t e = hipGetLastError();
+        const hipError_t e = a.mx_split_d == 4   ? mx_down_split<TY, SHARED, 4>(a, s)
+                             : a.mx_split_d == 2 ? mx_down_split<TY, SHARED, 2>(a, s)
+                                                 : mx_down_split<TY, SHARED, 1>(a, s);
         if (e != hipSuccess) return e;
     }
     return a.mx_min > 1 ? down_typed<TY, SHARED>(a, lds, s) : hipSuccess;

@@ -181,11 +181,11 @@ struct BatchArgs {
     float *g_s, *u_s;           // [n_tokens][ffn_s]
     uint8_t *bx, *bh;           // GEMM activation tiles of x and of h_s
     // mx = 1: chunks of at least mx_min tokens of the IQ2_S / IQ3_S streams run
-    // on the f16 matrix cores (row tiles mx_rt_gu / mx_rt_d) and read the
+    // on the f16 matrix cores (mx_split_* waves share each 16-row tile) and read the
     // operand copies of the Q8_K rows (quants XOR 0x80 at 256 bytes a block,
     // scales apart) of x, h_r and h_s; the VALU streams take the smaller chunks
     // and stage vc = min(tc, mx_min - 1) tokens (tc when mx = 0).
-    int32_t mx, mx_min, mx_rt_gu, mx_rt_d, vc;
+    int32_t mx, mx_min, mx_split_gu, mx_split_d, vc;
     uint8_t *xq_mx, *hq_mx_r, *hq_mx_s;
     float *xd_mx, *hd_mx_r, *hd_mx_s;
 };

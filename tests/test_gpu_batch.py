@@ -111,7 +111,7 @@ def test_batch_launch_shapes_give_the_same_bits(be, oracle, small, tiles):
     assert all(_same(got[t], want[t]) for t in range(21))
 
 
-@pytest.mark.parametrize("engine", [(0, 0, 0), (1, 0, 0), (5, 0, 0), (3, 32, 48), (16, 16, 16)])
+@pytest.mark.parametrize("engine", [(0, 0, 0), (1, 0, 0), (6, 0, 0), (3, 32, 64), (1, 64, 16), (16, 16, 32)])
 def test_batch_engines_bit_exact(be, oracle, small, engine):
     """The IQ streams on the VALU integer dots (0), all chunks on the f16 matrix
     cores (1), the per-chunk split at several thresholds and row tiles, with hot
