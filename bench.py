@@ -367,7 +367,7 @@ def bench_batch(args, be, timer, torch, np, synth, state):
            "algorithmic_bytes_per_step": int(bytes_step),
            "GB/s": round(bytes_step / us / 1e3, 1), "roofline_frac": round(bytes_step / us / 1e3 / HBM_PEAK_GBS, 4),
            "note": "the 33.5 MB shared expert is read once per step (K-quant GEMM on the f16 matrix cores); routed "
-                   "experts once per chunk of up to 16 tokens, chunks of 6+ tokens on the f16 matrix cores (exact "
+                   "experts once per chunk of up to 16 tokens, chunks of 4+ tokens on the f16 matrix cores (exact "
                    "integer block sums), smaller ones on the VALU integer dots"}
     check = dict(ids=ids_h[0].copy(), coefs=coefs[0].cpu().numpy(), xs=xs[0].cpu().numpy(), ys=ys[0].cpu().numpy())
     return res, check

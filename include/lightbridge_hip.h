@@ -270,7 +270,7 @@ lbh_status lbh_moe_set_batch_tiles(lbh_moe *moe, int32_t tokens_per_chunk, int32
 
 /* Engine of the batched IQ2_S / IQ3_S streams (no counterpart in the reference,
  * whose batch is a loop over tokens).  Chunks of at least mx_min_tokens tokens
- * (1..16; default 6) run on the f16 matrix cores, one 16-row x 16-token product
+ * (1..16; default 4) run on the f16 matrix cores, one 16-row x 16-token product
  * per codebook step, with mx_rows_gate_up / mx_rows_down rows per workgroup
  * (16, 32 or 64; 0: the defaults 16 and 32); smaller chunks run on the VALU
  * integer dots; mx_min_tokens = 0

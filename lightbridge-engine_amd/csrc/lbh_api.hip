@@ -515,6 +515,8 @@ struct lbh_moe {
     int tc, rt_gu_r, rt_gu_s, rt_d_r, rt_d_s;
     int mx_min;               // batched IQ chunks of >= mx_min tokens on the matrix cores (0: none)
     int mx_split_gu, mx_split_d;   // waves sharing a 16-row tile of those streams (1, 2, 4)
+    hipStream_t side;         // batched calls: second stream and fork/join events
+    hipEvent_t ev[4];
     uint8_t *shared_gemm_mem; // MFMA-ready copies of a K-quant shared expert (batched calls)
     size_t gemm_off[3];       // A offsets of gate, up, down in shared_gemm_mem
 };
@@ -524,7 +526,7 @@ namespace {
 // Batched launch shapes measured on MI355X at the configs[3] shapes (64 tokens,
 // hidden 4096, routed ffn 1536): with the matrix cores on, chunks of 16 tokens
 // (one instruction's width); the VALU streams alone do best with chunks of 8.
-constexpr int MX_MIN_DEFAULT = 6;
+constexpr int MX_MIN_DEFAULT = 4;
 void set_batch_defaults(lbh_moe *m, int mx_min) {
     m->mx_min = mx_min;
     m->mx_split_gu = 4, m->mx_split_d = 2;
@@ -540,6 +542,9 @@ void free_moe(lbh_moe *m) {
     if (m->batch_mem) (void)hipFree(m->batch_mem);
     if (m->shared_gemm_mem) (void)hipFree(m->shared_gemm_mem);
     if (m->plan_host) (void)hipHostFree(m->plan_host);
+    for (int i = 0; i < 4; ++i)
+        if (m->ev[i]) (void)hipEventDestroy(m->ev[i]);
+    if (m->side) (void)hipStreamDestroy(m->side);
     if (m->h) (void)hipFree(m->h);
     if (m->status) (void)hipFree(m->status);
     if (m->status_host) (void)hipHostFree(m->status_host);
@@ -994,6 +999,13 @@ BatchArgs batch_args(const lbh_moe *m, const uint32_t *ids, const float *coefs, 
 
 bool is_kquant(int ty) { return ty == LBH_Q4_K || ty == LBH_Q5_K; }
 
+BatchStreams batch_streams(const lbh_moe *m) {
+    BatchStreams b{};
+    b.side = m->side;
+    b.fork[0] = m->ev[0], b.fork[1] = m->ev[1], b.join[0] = m->ev[2], b.join[1] = m->ev[3];
+    return b;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1045,6 +1057,10 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     }
     hipError_t e = hipMalloc(&m->batch_mem, off);
     if (e == hipSuccess) e = hipMemset(m->batch_mem, 0, off);
+    // default priority, non-blocking: it only ever waits on the caller's stream through events
+    if (e == hipSuccess && !m->side) e = hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking);
+    for (int i = 0; i < 4 && e == hipSuccess; ++i)
+        if (!m->ev[i]) e = hipEventCreateWithFlags(&m->ev[i], hipEventDisableTiming);
     if (e == hipSuccess && !m->plan_host) e = hipHostMalloc(&m->plan_host, 16, hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -1161,7 +1177,8 @@ lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, 
     DeviceGuard g(ctx->device);
     BatchArgs a = batch_args(m, ids, coefs, n_tokens, top_k, x, y);
     a.gemm_shape = ctx->gemm_shape;
-    if (launch_moe_batch(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    const BatchStreams bs = batch_streams(m);
+    if (launch_moe_batch(a, ctx->stream, &bs) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;
 }
 
@@ -1205,7 +1222,8 @@ lbh_status lbh_moe_routed_by_id_batch_into(lbh_ctx *ctx, lbh_moe *m, const uint3
     HIP_TRY(hipMemcpyAsync(m->batch_coefs, coefs, n_tokens * top_k * 4, hipMemcpyHostToDevice, ctx->stream));
     BatchArgs a = batch_args(m, m->batch_ids, m->batch_coefs, n_tokens, top_k, input, output);
     a.gemm_shape = ctx->gemm_shape;
-    HIP_TRY(launch_moe_batch(a, ctx->stream));
+    const BatchStreams bs = batch_streams(m);
+    HIP_TRY(launch_moe_batch(a, ctx->stream, &bs));
     HIP_TRY(hipMemcpyAsync(m->plan_host, a.plan, 8, hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipStreamSynchronize(ctx->stream));
     if (m->plan_host[1]) return fail(err, LBH_INVALID_PARAMETER, 0, (uint64_t)m->plan_host[1]);

@@ -1163,41 +1163,45 @@ static hipError_t mx_down_split(const BatchArgs &a, hipStream_t s) {
 // below it (each kernel returns early on the other's chunks).  mx_split_* is
 // the number of waves that share a 16-row tile (1, 2 or 4).
 template <int TY, bool SHARED>
-static hipError_t mx_gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
+static hipError_t mx_gate_up_typed(const BatchArgs &a, int lds, hipStream_t s_mx, hipStream_t s_valu) {
     if (a.mx_min <= a.tc) {
-        const hipError_t e = a.mx_split_gu == 4   ? mx_gate_up_split<TY, SHARED, 4>(a, s)
-                             : a.mx_split_gu == 2 ? mx_gate_up_split<TY, SHARED, 2>(a, s)
-                                                  : mx_gate_up_split<TY, SHARED, 1>(a, s);
+        const hipError_t e = a.mx_split_gu == 4   ? mx_gate_up_split<TY, SHARED, 4>(a, s_mx)
+                             : a.mx_split_gu == 2 ? mx_gate_up_split<TY, SHARED, 2>(a, s_mx)
+                                                  : mx_gate_up_split<TY, SHARED, 1>(a, s_mx);
         if (e != hipSuccess) return e;
     }
-    return a.mx_min > 1 ? gate_up_typed<TY, SHARED>(a, lds, s) : hipSuccess;
+    return a.mx_min > 1 ? gate_up_typed<TY, SHARED>(a, lds, s_valu) : hipSuccess;
 }
 
 template <int TY, bool SHARED>
-static hipError_t mx_down_typed(const BatchArgs &a, int lds, hipStream_t s) {
+static hipError_t mx_down_typed(const BatchArgs &a, int lds, hipStream_t s_mx, hipStream_t s_valu) {
     if (a.mx_min <= a.tc) {
-        const hipError_t e = a.mx_split_d == 4   ? mx_down_split<TY, SHARED, 4>(a, s)
-                             : a.mx_split_d == 2 ? mx_down_split<TY, SHARED, 2>(a, s)
-                                                 : mx_down_split<TY, SHARED, 1>(a, s);
+        const hipError_t e = a.mx_split_d == 4   ? mx_down_split<TY, SHARED, 4>(a, s_mx)
+                             : a.mx_split_d == 2 ? mx_down_split<TY, SHARED, 2>(a, s_mx)
+                                                 : mx_down_split<TY, SHARED, 1>(a, s_mx);
         if (e != hipSuccess) return e;
     }
-    return a.mx_min > 1 ? down_typed<TY, SHARED>(a, lds, s) : hipSuccess;
+    return a.mx_min > 1 ? down_typed<TY, SHARED>(a, lds, s_valu) : hipSuccess;
 }
 
+// The matrix-core part of an IQ stream goes to s_mx, its VALU part to s_valu.
 template <bool SHARED>
-static hipError_t gate_up_any(int ty, const BatchArgs &a, int lds, hipStream_t s) {
+static hipError_t gate_up_any(int ty, const BatchArgs &a, int lds, hipStream_t s_mx, hipStream_t s_valu) {
+    const hipStream_t s = s_valu;
     switch (ty) {
-    case T_IQ2_S: return a.mx ? mx_gate_up_typed<T_IQ2_S, SHARED>(a, lds, s) : gate_up_typed<T_IQ2_S, SHARED>(a, lds, s);
+    case T_IQ2_S:
+        return a.mx ? mx_gate_up_typed<T_IQ2_S, SHARED>(a, lds, s_mx, s_valu) : gate_up_typed<T_IQ2_S, SHARED>(a, lds, s);
     case T_Q4_K: return gate_up_typed<T_Q4_K, SHARED>(a, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
 template <bool SHARED>
-static hipError_t down_any(int ty, const BatchArgs &a, int lds, hipStream_t s) {
+static hipError_t down_any(int ty, const BatchArgs &a, int lds, hipStream_t s_mx, hipStream_t s_valu) {
+    const hipStream_t s = s_valu;
     switch (ty) {
-    case T_IQ2_S: return a.mx ? mx_down_typed<T_IQ2_S, SHARED>(a, lds, s) : down_typed<T_IQ2_S, SHARED>(a, lds, s);
-    case T_IQ3_S: return a.mx ? mx_down_typed<T_IQ3_S, SHARED>(a, lds, s) : down_typed<T_IQ3_S, SHARED>(a, lds, s);
+    case T_IQ2_S: return a.mx ? mx_down_typed<T_IQ2_S, SHARED>(a, lds, s_mx, s_valu) : down_typed<T_IQ2_S, SHARED>(a, lds, s);
+    case T_IQ3_S: return a.mx ? mx_down_typed<T_IQ3_S, SHARED>(a, lds, s_mx, s_valu) : down_typed<T_IQ3_S, SHARED>(a, lds, s);
     case T_Q5_K: return down_typed<T_Q5_K, SHARED>(a, lds, s);
     default: return hipErrorInvalidValue;
     }
@@ -1208,7 +1212,7 @@ bool batch_types_supported(int gate_r, int down_r, int gate_s, int down_s) {
            (down_s == T_IQ2_S || down_s == T_IQ3_S || down_s == T_Q5_K);
 }
 
-hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
+hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s, const BatchStreams *streams) {
     if (a.n_tokens < 1 || a.n_tokens > BATCH_MAX_TOKENS || a.top_k < 1 || a.top_k > MOE_MAX_ROUTED ||
         a.n_experts < 1 || a.n_experts > BATCH_MAX_EXPERTS || a.tc < 1 || a.tc > BATCH_MAX_TC)
         return hipErrorInvalidValue;
@@ -1226,8 +1230,23 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(k_mb_prep, dim3(1 + cdiv((long long)a.n_tokens * nbh, 4 * MB_WAVES)), dim3(MB_THREADS), lds[0],
                        s, a);
     if ((e = hipGetLastError()) != hipSuccess) return e;
+    // Stage 1 (gate/up) and stage 2 (down) each fork the side stream after the
+    // main stream's last dependency and join it before the next dependent launch.
+    const bool two = streams && streams->side;
+    const hipStream_t s2 = two ? streams->side : s;
+    auto fork = [&](int i) -> hipError_t {
+        if (!two) return hipSuccess;
+        hipError_t r = hipEventRecord(streams->fork[i], s);
+        return r == hipSuccess ? hipStreamWaitEvent(s2, streams->fork[i], 0) : r;
+    };
+    auto join = [&](int i) -> hipError_t {
+        if (!two) return hipSuccess;
+        hipError_t r = hipEventRecord(streams->join[i], s2);
+        return r == hipSuccess ? hipStreamWaitEvent(s, streams->join[i], 0) : r;
+    };
+    if ((e = fork(0)) != hipSuccess) return e;
     if (a.has_shared && a.shared_gemm) {
-        // shared gate/up on the matrix cores, beside nothing: they only need Q8_K(x)
+        // shared gate/up on the matrix cores: they only need Q8_K(x)
         GemmArgs gm{};
         gm.b = a.bx;
         gm.nb = nbh;
@@ -1236,12 +1255,13 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
         gm.n_mat = 2;
         gm.mat[0] = a.sg;
         gm.mat[1] = a.su;
-        if ((e = launch_prep_b(a.q8x, a.n_tokens, nbh, a.bx, s)) != hipSuccess) return e;
-        if ((e = launch_kq_gemm(gm, s)) != hipSuccess) return e;
-    } else if (a.has_shared && (e = gate_up_any<true>(tsg, a, lds[2], s)) != hipSuccess) {
+        if ((e = launch_prep_b(a.q8x, a.n_tokens, nbh, a.bx, s2)) != hipSuccess) return e;
+        if ((e = launch_kq_gemm(gm, s2)) != hipSuccess) return e;
+    } else if (a.has_shared && (e = gate_up_any<true>(tsg, a, lds[2], s2, s2)) != hipSuccess) {
         return e;
     }
-    if ((e = gate_up_any<false>(a.type_gate_r, a, lds[1], s)) != hipSuccess) return e;
+    if ((e = gate_up_any<false>(a.type_gate_r, a, lds[1], s2, s)) != hipSuccess) return e;
+    if ((e = join(0)) != hipSuccess) return e;
 
     const bool rm = tsd == T_Q4_K || tsd == T_Q5_K;
     const int mode = !a.has_shared ? 0 : a.shared_gemm ? 2 : rm ? 1 : 0;
@@ -1250,6 +1270,7 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
     hipLaunchKernelGGL(k_mb_quant_h, dim3(cdiv(((br + 3) & ~3ll) + bs, 4 * MB_WAVES)), dim3(MB_THREADS), 0, s, a, mode);
     if ((e = hipGetLastError()) != hipSuccess) return e;
 
+    if ((e = fork(1)) != hipSuccess) return e;
     if (a.has_shared && a.shared_gemm) {
         const int nbs = a.ffn_s / 256;
         GemmArgs gm{};
@@ -1259,12 +1280,13 @@ hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s) {
         gm.shape = a.gemm_shape;
         gm.n_mat = 1;
         gm.mat[0] = a.sd;
-        if ((e = launch_prep_b(a.q8h_s, a.n_tokens, nbs, a.bh, s)) != hipSuccess) return e;
-        if ((e = launch_kq_gemm(gm, s)) != hipSuccess) return e;
-    } else if (a.has_shared && (e = down_any<true>(tsd, a, lds[4], s)) != hipSuccess) {
+        if ((e = launch_prep_b(a.q8h_s, a.n_tokens, nbs, a.bh, s2)) != hipSuccess) return e;
+        if ((e = launch_kq_gemm(gm, s2)) != hipSuccess) return e;
+    } else if (a.has_shared && (e = down_any<true>(tsd, a, lds[4], s2, s2)) != hipSuccess) {
         return e;
     }
-    if ((e = down_any<false>(a.type_down_r, a, lds[3], s)) != hipSuccess) return e;
+    if ((e = down_any<false>(a.type_down_r, a, lds[3], s2, s)) != hipSuccess) return e;
+    if ((e = join(1)) != hipSuccess) return e;
 
     const long long total = (long long)a.n_tokens * a.hidden;
     int g = cdiv(total, MB_THREADS);

@@ -208,7 +208,15 @@ hipError_t launch_prep_b(const uint8_t *q8, int n_tokens, int nb, uint8_t *b, hi
 hipError_t launch_kq_gemm(const GemmArgs &g, hipStream_t s);
 
 hipError_t launch_route_batch(const RouteBatchArgs &a, hipStream_t s);
-hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s);
+// A second stream and fork/join events for a batched call: the launches that
+// do not depend on each other (the shared expert's GEMMs, the matrix-core
+// chunks) run on `side` beside the main stream's VALU chunks, and the main
+// stream waits for them before the next stage.  NULL: all on the main stream.
+struct BatchStreams {
+    hipStream_t side;
+    hipEvent_t fork[2], join[2];
+};
+hipError_t launch_moe_batch(const BatchArgs &a, hipStream_t s, const BatchStreams *bs);
 int batch_lds_bytes(const BatchArgs &a, int stage);
 bool batch_types_supported(int gate_r, int down_r, int gate_s, int down_s);
 

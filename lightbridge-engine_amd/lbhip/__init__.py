@@ -405,7 +405,7 @@ class MoeLayer:
         if st:
             raise KernelError(LbhError(status=st))
 
-    def set_batch_engine(self, mx_min_tokens: int = 6, mx_rows_gate_up: int = 0, mx_rows_down: int = 0) -> None:
+    def set_batch_engine(self, mx_min_tokens: int = 4, mx_rows_gate_up: int = 0, mx_rows_down: int = 0) -> None:
         """Batched IQ chunks of at least mx_min_tokens tokens on the matrix cores, the
         rest on the VALU dot4 path (0: all on the VALU); resets the batch launch shapes
         to their defaults."""
