@@ -263,8 +263,9 @@ lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, cons
  * once, activation.rs:146-168; no allocation happens per call). */
 lbh_status lbh_moe_reserve_batch(lbh_moe *moe, size_t max_tokens, size_t top_k, lbh_error *err);
 
-/* Launch-shape knob of the batched kernels: tokens staged per chunk (1..16) and
- * rows per workgroup of the routed/shared gate-up and down streams. */
+/* Launch-shape knob of the batched kernels: tokens per chunk (1..16) and rows per
+ * workgroup of the VALU routed/shared gate-up and down streams (the matrix-core
+ * streams' tiles are set by lbh_moe_set_batch_engine). */
 lbh_status lbh_moe_set_batch_tiles(lbh_moe *moe, int32_t tokens_per_chunk, int32_t rows_gate_up_routed,
                                    int32_t rows_gate_up_shared, int32_t rows_down_routed, int32_t rows_down_shared);
 

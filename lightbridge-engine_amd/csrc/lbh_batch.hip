@@ -339,7 +339,6 @@ __device__ __forceinline__ void batch_rows(const MatView (&mv)[NM], int r0, int 
     auto issue = [&](int j, W (&w)[NM]) {
         int r = r0 + j * rpw + L.slot;
         r = L.lane_on && r < r1 ? r : r1 - 1;
-        r = r < r1 ? r : r1 - 1;
 #pragma unroll
         for (int m = 0; m < NM; ++m) load_slice(P[m], (uint32_t)(r * nb + L.b), po[m], L.part, w[m]);
     };

@@ -171,8 +171,8 @@ struct BatchArgs {
     float *d_s;                 // [n_tokens][hidden] shared down outputs
     int32_t max_chunks;         // routed chunks the launches cover
     int32_t tc;                 // tokens per chunk (1..BATCH_MAX_TC)
-    int32_t rt_gu_r, rt_gu_s;   // gate/up rows per workgroup (routed, shared)
-    int32_t rt_d_r, rt_d_s;     // down rows per workgroup (routed, shared)
+    int32_t rt_gu_r, rt_gu_s;   // VALU streams: gate/up rows per workgroup (routed, shared)
+    int32_t rt_d_r, rt_d_s;     // VALU streams: down rows per workgroup (routed, shared)
     int32_t type_gate_r, type_down_r;
     // K-quant shared expert on the matrix cores: gate/up -> g_s/u_s, SwiGLU
     // fused into the h quantization, down -> d_s.
