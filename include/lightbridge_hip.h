@@ -284,7 +284,9 @@ lbh_status lbh_moe_set_batch_engine(lbh_moe *moe, int32_t mx_min_tokens, int32_t
 /* [async] Batched form of lbh_moe_forward: ids_dev / coefs_dev are device arrays
  * [n_tokens][top_k] (each token's ids ascending and distinct), x_dev [n_tokens][hidden],
  * y_dev [n_tokens][hidden].  Unchecked; a routing with an id >= n_experts or a token
- * naming an expert twice leaves y unchanged. */
+ * naming an expert twice leaves y unchanged.  The layer's batch scratch and its second
+ * stream (independent launches run there, joined back to ctx's stream before the
+ * call's work ends) are per layer: batched calls on one layer must not overlap. */
 lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids_dev, const float *coefs_dev,
                                  size_t n_tokens, size_t top_k, const float *x_dev, float *y_dev);
 

@@ -127,6 +127,15 @@ def test_batch_engines_bit_exact(be, oracle, small, engine):
     assert all(_same(got[t], want[t]) for t in range(40))
 
 
+@pytest.mark.parametrize("bad", [(-1, 0, 0), (17, 0, 0), (4, 48, 0), (4, 0, 8), (4, 128, 0)])
+def test_batch_engine_rejects_bad_settings(small, bad):
+    import lbhip
+    with pytest.raises(lbhip.KernelError) as e:
+        small.moe.set_batch_engine(*bad)
+    assert e.value.variant == "InvalidParameter"
+    small.moe.set_batch_engine()
+
+
 @pytest.mark.parametrize("types", [(IQ2_S, IQ3_S, IQ2_S, IQ3_S), (IQ2_S, IQ2_S, IQ2_S, IQ2_S),
                                    (IQ2_S, IQ2_S, IQ2_S, IQ3_S)])
 def test_batch_type_sets(be, oracle, types):
