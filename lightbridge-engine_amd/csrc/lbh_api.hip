@@ -1037,7 +1037,8 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     const size_t o_plan = take(16), o_ce = take(P * 4), o_cp = take(P * 4), o_cn = take(P * 4);
     const size_t o_pt = take(P * 4), o_po = take(P * 4);
     const size_t o_q8x = take(T * nbh * 292), o_q8xr = take(T * nbh * 292);
-    const size_t o_hr = take(P * m->ffn_r * 4), o_hs = take(T * ffn_s * 4);
+    const size_t o_gr = take(P * m->ffn_r * 4), o_ur = take(P * m->ffn_r * 4);
+    const size_t o_gs = take(T * ffn_s * 4), o_us = take(T * ffn_s * 4);
     const size_t o_q8hr = take(P * nbr * 292), o_q8hs = take(T * nbs * 292);
     const size_t o_dr = take(P * m->hidden * 4), o_ds = take(T * m->hidden * 4);
     const size_t o_ids = take(P * 4), o_coefs = take(P * 4);
@@ -1046,12 +1047,10 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     const size_t o_hqr = take(P * nbr * 256), o_hdr = take(P * nbr * 4);
     const size_t o_hqs = take(T * nbs * 256), o_hds = take(T * nbs * 4);
     // A K-quant shared expert runs on the matrix cores: gate/up outputs and the
-    // GEMM activation tiles of x and h_s.
+    // GEMM activation tiles of x and of the shared h.
     const bool sgemm = m->has_shared && is_kquant(m->shared.gate.type) && is_kquant(m->shared.down.type);
-    size_t o_gs = 0, o_us = 0, o_bx = 0, o_bh = 0;
+    size_t o_bx = 0, o_bh = 0;
     if (sgemm) {
-        o_gs = take(T * ffn_s * 4);
-        o_us = take(T * ffn_s * 4);
         o_bx = take(gemm_b_bytes((int)T, (int)nbh));
         o_bh = take(gemm_b_bytes((int)T, (int)nbs));
     }
@@ -1080,8 +1079,10 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     a.pair_of = reinterpret_cast<int32_t *>(b + o_po);
     a.q8x = b + o_q8x;
     a.q8x_rm = b + o_q8xr;
-    a.h_r = reinterpret_cast<float *>(b + o_hr);
-    a.h_s = reinterpret_cast<float *>(b + o_hs);
+    a.g_r = reinterpret_cast<float *>(b + o_gr);
+    a.u_r = reinterpret_cast<float *>(b + o_ur);
+    a.g_s = reinterpret_cast<float *>(b + o_gs);
+    a.u_s = reinterpret_cast<float *>(b + o_us);
     a.q8h_r = b + o_q8hr;
     a.q8h_s = b + o_q8hs;
     a.d_r = reinterpret_cast<float *>(b + o_dr);
@@ -1096,8 +1097,6 @@ lbh_status lbh_moe_reserve_batch(lbh_moe *m, size_t max_tokens, size_t top_k, lb
     m->batch_coefs = reinterpret_cast<float *>(b + o_coefs);
     a.shared_gemm = sgemm ? 1 : 0;
     if (sgemm) {
-        a.g_s = reinterpret_cast<float *>(b + o_gs);
-        a.u_s = reinterpret_cast<float *>(b + o_us);
         a.bx = b + o_bx;
         a.bh = b + o_bh;
         if (!m->shared_gemm_mem) {

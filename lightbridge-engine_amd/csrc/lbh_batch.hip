@@ -571,7 +571,9 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
                 __syncthreads();
             },
             [&](int i, int r, const float *res) {
-                a.h_s[(long long)(t0 + i) * a.ffn_s + r] = swiglu_ref(res[0], res[1]);
+                const long long o = (long long)(t0 + i) * a.ffn_s + r;
+                a.g_s[o] = res[0];
+                a.u_s[o] = res[1];
             });
     } else {
         const int tiles = (a.ffn_r + a.rt_gu_r - 1) / a.rt_gu_r;
@@ -589,15 +591,20 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
                 __syncthreads();
             },
             [&](int i, int r, const float *res) {
-                a.h_r[(long long)(p0 + i) * a.ffn_r + r] = swiglu_ref(res[0], res[1]);
+                const long long o = (long long)(p0 + i) * a.ffn_r + r;
+                a.g_r[o] = res[0];
+                a.u_r[o] = res[1];
             });
     }
 }
 
-// Q8_K of every h row (quantize_row_q8_k_into of each down projection's
-// input): routed rows [0, pairs), then the shared rows.  shared_mode 1: the
-// shared copy has residue-major qs (VALU K-quant down); 2: the shared h is
-// SwiGLU(g_s, u_s) of the matrix-core gate/up, formed here (activation.rs:170-178).
+// h = SwiGLU(gate, up) (activation.rs:170-178) and its Q8_K (quantize_row_q8_k_into
+// of each down projection's input, gemv.rs:161-163) for every routed pair row
+// [0, pairs), then the shared rows.  The gate/up streams leave gate and up
+// apart, so no exp runs inside their weight loops (its table load would wait
+// for every weight load in flight).  shared_mode 0: the shared copy is GGML
+// bytes plus the matrix-core operand copy (IQ down); 1: residue-major qs only
+// (VALU K-quant down); 2: GGML bytes (K-quant GEMM down).
 __global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shared_mode) {
     __shared__ __align__(16) uint8_t lds[MB_WAVES * 4 * 292];
     __shared__ __align__(16) float hbuf[MB_WAVES][4 * 256];
@@ -609,26 +616,26 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shar
     const long long bs = a.has_shared ? (long long)a.n_tokens * nbs : 0;
     const long long chunk = ((long long)blockIdx.x * MB_WAVES + wid) * 4;
     uint8_t *lw = lds + wid * 4 * 292;
+    // Lane (block first + lane / 16, elements 16 (lane % 16) ..) forms the
+    // sixteen values it quantizes below.
+    auto swiglu_blocks = [&](const float *g, const float *u, long long first, long long nblocks) {
+        const long long blk = first + (lane >> 4);
+        if (blk < nblocks) {
+            const long long base = blk * 256 + 16 * (lane & 15);
+            float *hb = &hbuf[wid][(lane >> 4) * 256 + 16 * (lane & 15)];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) hb[i] = swiglu_ref(g[base + i], u[base + i]);
+        }
+        wave_sync();
+    };
     if (chunk < br) {
-        quantize_rows_out(a.h_r + chunk * 256, br, chunk, a.q8h_r, nullptr, lw, MxRows{a.mx ? a.hq_mx_r : nullptr, a.hd_mx_r});
+        swiglu_blocks(a.g_r, a.u_r, chunk, br);
+        quantize_rows_out(&hbuf[wid][0], br, chunk, a.q8h_r, nullptr, lw, MxRows{a.mx ? a.hq_mx_r : nullptr, a.hd_mx_r});
     } else if (chunk >= brp && chunk - brp < bs) {
         const long long f = chunk - brp;
-        if (shared_mode == 2) {
-            // lane (block q = lane / 16, elements 16 (lane % 16) ..) forms the
-            // sixteen values it quantizes below
-            const long long blk = f + (lane >> 4);
-            if (blk < bs) {
-                const long long base = blk * 256 + 16 * (lane & 15);
-                float *hb = &hbuf[wid][(lane >> 4) * 256 + 16 * (lane & 15)];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) hb[i] = swiglu_ref(a.g_s[base + i], a.u_s[base + i]);
-            }
-            wave_sync();
-            quantize_rows_out(&hbuf[wid][0], bs, f, a.q8h_s, nullptr, lw);
-        } else {
-            quantize_rows_out(a.h_s + f * 256, bs, f, shared_mode ? nullptr : a.q8h_s, shared_mode ? a.q8h_s : nullptr,
-                              lw, MxRows{a.mx && !shared_mode ? a.hq_mx_s : nullptr, a.hd_mx_s});
-        }
+        swiglu_blocks(a.g_s, a.u_s, f, bs);
+        quantize_rows_out(&hbuf[wid][0], bs, f, shared_mode == 1 ? nullptr : a.q8h_s, shared_mode == 1 ? a.q8h_s : nullptr,
+                          lw, MxRows{a.mx && shared_mode == 0 ? a.hq_mx_s : nullptr, a.hd_mx_s});
     }
 }
 
@@ -979,7 +986,7 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
     if (n < a.mx_min) return;
     const int c = (int)(threadIdx.x & 15) < n ? (int)(threadIdx.x & 15) : n - 1;
     const long long tok = SHARED ? (long long)(p0 + c) : (long long)a.pair_token[p0 + c];
-    float *h = SHARED ? a.h_s : a.h_r;
+    float *g = SHARED ? a.g_s : a.g_r, *u = SHARED ? a.u_s : a.u_r;
     mx_tiles<TY, 2, S>(
         mv, r0, r1, nb, a.xq_mx + tok * nb * 256, a.xd_mx + tok * nb, tab, terms,
         [&]() {
@@ -987,7 +994,11 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
             __syncthreads();
         },
         [&](int i, int r, const float *res) {
-            if (i < n && r < r1) h[(long long)(p0 + i) * ffn + r] = swiglu_ref(res[0], res[1]);
+            if (i < n && r < r1) {
+                const long long o = (long long)(p0 + i) * ffn + r;
+                g[o] = res[0];
+                u[o] = res[1];
+            }
         });
 }
 

@@ -163,8 +163,7 @@ struct BatchArgs {
     int32_t *pair_of;           // token * top_k + slot -> sorted pair
     uint8_t *q8x;               // [n_tokens][hidden / 256] Q8_K blocks of x
     uint8_t *q8x_rm;            // the same with residue-major qs (K-quant consumers)
-    float *h_r;                 // [pairs][ffn_r]  SwiGLU outputs, sorted pair order
-    float *h_s;                 // [n_tokens][ffn_s]
+    float *g_r, *u_r;           // [pairs][ffn_r] gate / up outputs, sorted pair order
     uint8_t *q8h_r;             // [pairs][ffn_r / 256] Q8_K of h_r
     uint8_t *q8h_s;             // [n_tokens][ffn_s / 256] Q8_K of h_s (residue-major for K-quants)
     float *d_r;                 // [pairs][hidden] routed down outputs
@@ -174,16 +173,17 @@ struct BatchArgs {
     int32_t rt_gu_r, rt_gu_s;   // VALU streams: gate/up rows per workgroup (routed, shared)
     int32_t rt_d_r, rt_d_s;     // VALU streams: down rows per workgroup (routed, shared)
     int32_t type_gate_r, type_down_r;
-    // K-quant shared expert on the matrix cores: gate/up -> g_s/u_s, SwiGLU
-    // fused into the h quantization, down -> d_s.
+    // The shared expert's gate / up outputs (every stream type; SwiGLU is
+    // formed in the h quantization, as for the routed pairs); on the K-quant
+    // types its gate/up and down run on the matrix cores (-> d_s).
     int32_t shared_gemm, gemm_shape;
     MatGemm sg, su, sd;         // MFMA-ready copies of the shared gate / up / down
     float *g_s, *u_s;           // [n_tokens][ffn_s]
-    uint8_t *bx, *bh;           // GEMM activation tiles of x and of h_s
+    uint8_t *bx, *bh;           // GEMM activation tiles of x and of the shared h
     // mx = 1: chunks of at least mx_min tokens of the IQ2_S / IQ3_S streams run
     // on the f16 matrix cores (mx_split_* waves share each 16-row tile) and read the
     // operand copies of the Q8_K rows (quants XOR 0x80 at 256 bytes a block,
-    // scales apart) of x, h_r and h_s; the VALU streams take the smaller chunks
+    // scales apart) of x and of the routed and shared h; the VALU streams take the smaller chunks
     // and stage vc = min(tc, mx_min - 1) tokens (tc when mx = 0).
     int32_t mx, mx_min, mx_split_gu, mx_split_d, vc;
     uint8_t *xq_mx, *hq_mx_r, *hq_mx_s;
