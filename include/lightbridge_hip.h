@@ -60,6 +60,7 @@ typedef enum lbh_status {
     LBH_HIP_ERROR = 100,
     LBH_NULL_ARGUMENT = 101,
     LBH_UNSUPPORTED_SHAPE = 102,
+    LBH_DEVICE_TIMEOUT = 103,   /* a bounded in-kernel wait gave up (the result was discarded) */
 } lbh_status;
 
 /* Error payload: the fields of the corresponding QuantError/KernelError variant. */
@@ -190,6 +191,62 @@ lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x_dev, u
  * block_sum (one int32) or the Q4_K/Q5_K lane_sums[8] + minimum_sum (nine int32)
  * of q8_k.rs:295-312, :337-364, :380-428.  out_dev holds rows * (k/256) * {1|9} int32. */
 lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, int32_t *out_dev);
+
+/* ---- checked dots over caller-supplied Q8_K ----------------------------------
+ * The reference's dot API takes a packed weight row and an already-quantized
+ * Q8_K row (crates/bridge-quant-layout/src/lib.rs:16-19): vec_dot_q8_k,
+ * validate_vec_dot_q8_k and the typed vec_dot_{q4_k,q5_k,iq2_s,iq3_s}_q8_k
+ * (q8_k.rs:80-101, :172-186).  These entry points take `rows` consecutive raw
+ * GGML rows (rows = 1 is exactly the reference call) in device memory, no
+ * upload needed, any byte alignment.  Checks, in the order of
+ * validate_vec_dot_q8_k_inner (q8_k.rs:121-161): type (UnsupportedType),
+ * logical_elements (ZeroLogicalElements / LogicalElementsNotDivisible),
+ * weights_len == rows * row bytes and q8_len == (n/256) * 292
+ * (EncodedLengthMismatch, ty = the weight type / Q8_K), then per row in order
+ * the weights' f16 d / dmin (NonFiniteScale: index = block, field, bits, row)
+ * and the Q8_K d of every block (NonFiniteQ8Scale: index = block, bits).
+ * logical_elements is limited to 64 blocks (UnsupportedShape). */
+
+/* [sync] validate_vec_dot_q8_k (q8_k.rs:91-101). */
+lbh_status lbh_validate_vec_dot_q8_k(lbh_ctx *ctx, int32_t ggml_type, const uint8_t *weights_dev, size_t weights_len,
+                                     size_t rows, const uint8_t *q8_dev, size_t q8_len, size_t logical_elements,
+                                     lbh_error *err);
+
+/* [sync] vec_dot_q8_k (q8_k.rs:80-89) per row: out_dev[r] = dot(row r, q8), bit-identical;
+ * out_len must equal rows (OutputLengthMismatch).  On any error out_dev is unchanged. */
+lbh_status lbh_vec_dot_q8_k_into(lbh_ctx *ctx, int32_t ggml_type, const uint8_t *weights_dev, size_t weights_len,
+                                 size_t rows, const uint8_t *q8_dev, size_t q8_len, size_t logical_elements,
+                                 float *out_dev, size_t out_len, lbh_error *err);
+
+/* [sync] Checked lbh_gemv_q8_k over an uploaded matrix (its weight scales were checked
+ * at upload): accumulate == 0: y[r] = dot(row r, q8); else y[r] += coef * dot(row r, q8)
+ * after the checks of gemv_accumulate_scaled_into (finite coef, finite destination:
+ * NonFiniteValue, field 2 / 3).  Then y_len == rows (DimensionMismatch, index 1),
+ * q8_len == (k/256) * 292 (EncodedLengthMismatch) and the Q8_K scales
+ * (NonFiniteQ8Scale).  On any error y_dev is unchanged. */
+lbh_status lbh_gemv_q8_k_into(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, size_t q8_len, float *y_dev,
+                              size_t y_len, float coef, int32_t accumulate, lbh_error *err);
+
+/* ---- DequantF32 execution mode ----------------------------------------------
+ * ReferenceExecutionMode::DequantF32 (crates/bridge-kernels-reference/src/gemv.rs:12-16):
+ * output[r] = the sequential f32 sum over every element of decode(w[r][i]) * input[i]
+ * (dot_dequant_row, gemv.rs:305-328, with the exact decoders of k_quants.rs:242-300,
+ * iq2_s.rs:9-39, iq3_s.rs:9-53), bit-identical.  No Q8_K quantization is involved. */
+
+/* [sync] gemv_dequant_f32_into (gemv.rs:33-41): validate_dimensions (DimensionMismatch,
+ * NonFiniteValue on the input) as lbh_gemv_into. */
+lbh_status lbh_gemv_dequant_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input_dev, size_t input_len,
+                                 float *output_dev, size_t output_len, lbh_error *err);
+
+/* [sync] The DequantF32 arm of gemv_accumulate_scaled_into (gemv.rs:117-151):
+ * destination[r] += scale * dot_dequant_row(r). */
+lbh_status lbh_gemv_dequant_accumulate_scaled_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input_dev,
+                                                   size_t input_len, float *destination_dev, size_t dest_len,
+                                                   float scale, lbh_error *err);
+
+/* [async] Unchecked form: accumulate == 0: y = dot; else y += coef * dot. */
+lbh_status lbh_gemv_dequant_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x_dev, float *y_dev, float coef,
+                                int32_t accumulate);
 
 /* ---- token batches on the matrix cores (prefill) ----------------------------------
  * The reference has no batched path ("grouped prefill unavailable", docs/STATUS.md:29):
@@ -329,7 +386,8 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *router, const float *
 
 /* [async] One MoE block decode step entirely on the device: router + top-k, then the
  * routed and shared experts (lbh_moe_forward semantics) reading the device routing.
- * Unchecked: x must be finite. */
+ * Unchecked: x must be finite.  A routing the selection rejects (a non-finite logit,
+ * or a router chain whose bounded wait gave up) leaves y unchanged. */
 lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev, size_t top_k,
                                  int32_t mode, float weight_scale, float *y_dev);
 
@@ -431,6 +489,12 @@ lbh_status lbh_moe_forward_leased(lbh_ctx *ctx, lbh_moe *moe, const lbh_expert_l
                                   size_t n_routed, const float *x_dev, float *y_dev);
 
 /* ---- diagnostics ------------------------------------------------------------- */
+
+/* Polls of the router chains' bounded LDS-ring waits before they give up (0: the
+ * default, 2^22; negative: every wait gives up at once, which lets a test drive
+ * the give-up path deterministically: lbh_router_route_into then returns
+ * LBH_DEVICE_TIMEOUT and lbh_moe_block_forward leaves y unchanged). */
+lbh_status lbh_router_set_spin_limit(lbh_router *router, int64_t limit);
 
 /* [sync] The device expf used by SwiGLU and the routers (swiglu == 0), or the
  * SwiGLU element gate / (1 + exp(-gate)) * up (swiglu != 0, up_dev required). */

@@ -377,27 +377,73 @@ size_t lbh_matrix_bytes(const lbh_matrix *m) { return m ? m->bytes : 0; }
 
 namespace {
 
-// prepare_llama_q8k (crates/bridge-kernels-reference/src/gemv.rs:245-272) minus the
-// per-row scale scan, which matrix upload performed once.
-lbh_status gemv_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
-                        size_t out_len, uint8_t *q8, size_t q8_len, int accumulate, float scale, lbh_error *err) {
-    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
-    // gemv_accumulate_scaled_into validates the scale before anything else (gemv.rs:126).
+// The device scans of a checked matvec report in the reference's order: the
+// destination (gemv_accumulate_scaled_into, gemv.rs:127) before the
+// dimensions, the input (validate_dimensions, gemv.rs:195-211) before the
+// scratch size (prepare_llama_q8k, gemv.rs:258-264).  A host-side error that
+// the reference checks after a scan is reported only once the scan is known
+// clean, which costs a synchronisation on error paths only.
+lbh_status dest_error(lbh_ctx *ctx, int ty, const float *dest, lbh_error *err) {
+    const unsigned long long i = ctx->status_host->first_bad_dest;
+    return fail(err, LBH_NON_FINITE_VALUE, ty, i, 0, 0, read_f32_bits(ctx, dest + i), 3);
+}
+
+lbh_status input_error(lbh_ctx *ctx, int ty, const float *input, lbh_error *err) {
+    const unsigned long long i = ctx->status_host->first_bad_input;
+    return fail(err, LBH_NON_FINITE_VALUE, ty, i, 0, 0, read_f32_bits(ctx, input + i), 0);
+}
+
+// Scale and destination checks of an accumulating call (gemv.rs:126-127), then
+// validate_dimensions (gemv.rs:195-211) including the input scan.  On success
+// the scans are queued (not yet read) and the status words are live.
+lbh_status check_gemv_args(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
+                           size_t out_len, int accumulate, float scale, lbh_error *err) {
     if (accumulate && !std::isfinite(scale)) {
         uint32_t bits;
         std::memcpy(&bits, &scale, 4);
         return fail(err, LBH_NON_FINITE_VALUE, m->type, 0, 0, 0, bits, 2);
     }
-    // validate_dimensions (gemv.rs:195-211).
-    if (input_len != m->k) return fail(err, LBH_DIMENSION_MISMATCH, m->type, 0, m->k, input_len);
-    if (out_len != m->rows) return fail(err, LBH_DIMENSION_MISMATCH, m->type, 1, m->rows, out_len);
-    const size_t need = m->k / 256 * 292;
-    if (q8_len < need) return fail(err, LBH_SCRATCH_TOO_SMALL, LBH_Q8_K, 0, need, q8_len);
-    if (!input || !out || !q8) return fail(err, LBH_NULL_ARGUMENT);
-    DeviceGuard g(ctx->device);
+    if (!input || !out) return fail(err, LBH_NULL_ARGUMENT);
     HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
     if (accumulate) HIP_TRY(launch_find_nonfinite(out, (long long)out_len, &ctx->status->first_bad_dest, ctx->stream));
+    if (input_len != m->k || out_len != m->rows) {
+        if (accumulate) {
+            lbh_status st = read_status(ctx, err);
+            if (st) return st;
+            if (ctx->status_host->first_bad_dest != ~0ull) return dest_error(ctx, m->type, out, err);
+        }
+        if (input_len != m->k) return fail(err, LBH_DIMENSION_MISMATCH, m->type, 0, m->k, input_len);
+        return fail(err, LBH_DIMENSION_MISMATCH, m->type, 1, m->rows, out_len);
+    }
     HIP_TRY(launch_find_nonfinite(input, (long long)input_len, &ctx->status->first_bad_input, ctx->stream));
+    return LBH_OK;
+}
+
+// The scans' verdict after the compute launch (which skipped its writes if
+// any scan fired): destination first, then input.
+lbh_status scan_verdict(lbh_ctx *ctx, int ty, const float *input, const float *out, lbh_error *err) {
+    lbh_status st = read_status(ctx, err);
+    if (st) return st;
+    if (ctx->status_host->first_bad_dest != ~0ull) return dest_error(ctx, ty, out, err);
+    if (ctx->status_host->first_bad_input != ~0ull) return input_error(ctx, ty, input, err);
+    return ok(err);
+}
+
+// prepare_llama_q8k (crates/bridge-kernels-reference/src/gemv.rs:245-272) minus the
+// per-row scale scan, which matrix upload performed once.
+lbh_status gemv_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
+                        size_t out_len, uint8_t *q8, size_t q8_len, int accumulate, float scale, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    DeviceGuard g(ctx->device);
+    lbh_status st = check_gemv_args(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
+    if (st) return st;
+    const size_t need = m->k / 256 * 292;
+    if (q8_len < need || !q8) {
+        st = scan_verdict(ctx, m->type, input, out, err);
+        if (st) return st;
+        if (!q8) return fail(err, LBH_NULL_ARGUMENT);
+        return fail(err, LBH_SCRATCH_TOO_SMALL, LBH_Q8_K, 0, need, q8_len);
+    }
     GemvArgs a{};
     a.m = view_of(m);
     a.x = input;        // quantized inside the matvec kernel ...
@@ -408,16 +454,58 @@ lbh_status gemv_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, s
     a.block_sums = nullptr;
     a.status = ctx->status;
     HIP_TRY(launch_gemv(a, ctx->tuning, ctx->stream));
-    lbh_status st = read_status(ctx, err);
+    return scan_verdict(ctx, m->type, input, out, err);
+}
+
+// validate_vec_dot_q8_k_inner (crates/bridge-quant-layout/src/q8_k.rs:121-161)
+// for `rows` consecutive rows of raw GGML bytes: type, logical elements, exact
+// weight and Q8_K lengths, then per row in order the weight scales
+// (validate_scales, k_quants.rs:178-208) and the Q8_K scales
+// (validate_q8_scales, q8_k.rs:208-222).  Queues the scans (and, when y is
+// given, the dot kernel, which skips its writes if a scan fires) and reports
+// the first failure in the reference's order.
+lbh_status vec_dot_checked(lbh_ctx *ctx, int32_t ty, const uint8_t *w, size_t w_len, size_t rows, const uint8_t *q8,
+                           size_t q8_len, size_t n, float *y, size_t y_len, lbh_error *err) {
+    if (!ctx) return fail(err, LBH_NULL_ARGUMENT);
+    if (!is_dot_type(ty)) return fail(err, LBH_UNSUPPORTED_TYPE, ty);
+    lbh_status st = check_elements(ty, n, err);
     if (st) return st;
-    if (ctx->status_host->first_bad_dest != ~0ull) {
-        const unsigned long long i = ctx->status_host->first_bad_dest;
-        return fail(err, LBH_NON_FINITE_VALUE, m->type, i, 0, 0, read_f32_bits(ctx, out + i), 3);
+    if (rows == 0) return fail(err, LBH_DIMENSION_MISMATCH, ty, 0, 1, 0);
+    const size_t nb = n / 256, bb = block_bytes(ty);
+    if (rows > SIZE_MAX / (nb * bb)) return fail(err, LBH_ARITHMETIC_OVERFLOW, ty);
+    const size_t want_w = rows * nb * bb, want_q8 = nb * 292;
+    if (w_len != want_w) return fail(err, LBH_ENCODED_LENGTH_MISMATCH, ty, 0, want_w, w_len);
+    if (q8_len != want_q8) return fail(err, LBH_ENCODED_LENGTH_MISMATCH, LBH_Q8_K, 0, want_q8, q8_len);
+    if (y && y_len != rows) return fail(err, LBH_OUTPUT_LENGTH_MISMATCH, ty, 0, rows, y_len);
+    if (!w || !q8) return fail(err, LBH_NULL_ARGUMENT);
+    if (nb > 64) return fail(err, LBH_UNSUPPORTED_SHAPE, ty, 0, 64, nb);
+    DeviceGuard g(ctx->device);
+    const long long U = (long long)(rows * nb);
+    HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+    HIP_TRY(launch_validate_scales(ty, w, U, &ctx->status->first_bad_scale, ctx->stream));
+    // The first non-finite Q8_K block goes to the input word: the dot kernel skips on it.
+    HIP_TRY(launch_find_nonfinite_q8(q8, (long long)nb, &ctx->status->first_bad_input, ctx->stream));
+    if (y) HIP_TRY(launch_dot_ggml(ty, w, (long long)rows, (int)nb, q8, y, ctx->status, ctx->stream));
+    st = read_status(ctx, err);
+    if (st) return st;
+    const unsigned long long bad_w = ctx->status_host->first_bad_scale, bad_q8 = ctx->status_host->first_bad_input;
+    auto scale_error = [&]() {
+        const unsigned long long u = bad_w / 2;
+        const uint32_t field = (uint32_t)(bad_w & 1);
+        uint16_t bits = 0;
+        (void)hipMemcpy(&bits, w + u * bb + 2 * field, 2, hipMemcpyDeviceToHost);
+        // NonFiniteScale { ty, block_index, field, bits } (k_quants.rs:196-204) of row u / nb.
+        return fail(err, LBH_NON_FINITE_SCALE, ty, u % nb, 0, 0, bits, field, u / nb);
+    };
+    // Row 0's weight scales precede the Q8_K scales, which precede later rows' weights.
+    if (bad_w != ~0ull && bad_w / 2 < nb) return scale_error();
+    if (bad_q8 != ~0ull) {
+        uint32_t bits = 0;
+        (void)hipMemcpy(&bits, q8 + bad_q8 * 292, 4, hipMemcpyDeviceToHost);
+        // NonFiniteQ8Scale { block_index, bits } (q8_k.rs:216-219).
+        return fail(err, LBH_NON_FINITE_Q8_SCALE, LBH_Q8_K, bad_q8, 0, 0, bits);
     }
-    if (ctx->status_host->first_bad_input != ~0ull) {
-        const unsigned long long i = ctx->status_host->first_bad_input;
-        return fail(err, LBH_NON_FINITE_VALUE, m->type, i, 0, 0, read_f32_bits(ctx, input + i), 0);
-    }
+    if (bad_w != ~0ull) return scale_error();
     return ok(err);
 }
 
@@ -475,6 +563,99 @@ lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t 
     hipError_t e = launch_gemv(a, ctx->tuning, ctx->stream);
     (void)hipFreeAsync(y, ctx->stream);
     return e == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+}
+
+lbh_status lbh_validate_vec_dot_q8_k(lbh_ctx *ctx, int32_t ty, const uint8_t *weights, size_t weights_len,
+                                     size_t rows, const uint8_t *q8, size_t q8_len, size_t logical_elements,
+                                     lbh_error *err) {
+    return vec_dot_checked(ctx, ty, weights, weights_len, rows, q8, q8_len, logical_elements, nullptr, 0, err);
+}
+
+lbh_status lbh_vec_dot_q8_k_into(lbh_ctx *ctx, int32_t ty, const uint8_t *weights, size_t weights_len, size_t rows,
+                                 const uint8_t *q8, size_t q8_len, size_t logical_elements, float *out, size_t out_len,
+                                 lbh_error *err) {
+    if (!out) return fail(err, LBH_NULL_ARGUMENT);
+    return vec_dot_checked(ctx, ty, weights, weights_len, rows, q8, q8_len, logical_elements, out, out_len, err);
+}
+
+lbh_status lbh_gemv_q8_k_into(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t q8_len, float *y,
+                              size_t y_len, float coef, int32_t accumulate, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    if (accumulate && !std::isfinite(coef)) {
+        uint32_t bits;
+        std::memcpy(&bits, &coef, 4);
+        return fail(err, LBH_NON_FINITE_VALUE, m->type, 0, 0, 0, bits, 2);
+    }
+    if (!y) return fail(err, LBH_NULL_ARGUMENT);
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+    if (accumulate) HIP_TRY(launch_find_nonfinite(y, (long long)y_len, &ctx->status->first_bad_dest, ctx->stream));
+    const size_t want_q8 = m->nb * 292;
+    if (y_len != m->rows || q8_len != want_q8 || !q8) {
+        if (accumulate) {
+            lbh_status st = read_status(ctx, err);
+            if (st) return st;
+            if (ctx->status_host->first_bad_dest != ~0ull) return dest_error(ctx, m->type, y, err);
+        }
+        if (y_len != m->rows) return fail(err, LBH_DIMENSION_MISMATCH, m->type, 1, m->rows, y_len);
+        if (!q8) return fail(err, LBH_NULL_ARGUMENT);
+        return fail(err, LBH_ENCODED_LENGTH_MISMATCH, LBH_Q8_K, 0, want_q8, q8_len);
+    }
+    HIP_TRY(launch_find_nonfinite_q8(q8, (long long)m->nb, &ctx->status->first_bad_input, ctx->stream));
+    GemvArgs a{};
+    a.m = view_of(m);
+    a.q8 = q8;
+    a.y = y;
+    a.coef = coef;
+    a.accumulate = accumulate;
+    a.status = ctx->status;
+    HIP_TRY(launch_gemv(a, ctx->tuning, ctx->stream));
+    lbh_status st = read_status(ctx, err);
+    if (st) return st;
+    if (ctx->status_host->first_bad_dest != ~0ull) return dest_error(ctx, m->type, y, err);
+    const unsigned long long b = ctx->status_host->first_bad_input;
+    if (b != ~0ull) {
+        uint32_t bits = 0;
+        (void)hipMemcpy(&bits, q8 + b * 292, 4, hipMemcpyDeviceToHost);
+        return fail(err, LBH_NON_FINITE_Q8_SCALE, LBH_Q8_K, b, 0, 0, bits);
+    }
+    return ok(err);
+}
+
+// DequantF32 mode: gemv_dequant_f32_into (gemv.rs:33-41) and the DequantF32 arm of
+// gemv_accumulate_scaled_into (gemv.rs:146-151).  prepare_dequant's per-block
+// weight check (gemv.rs:232-240) cannot fire here: upload required finite d /
+// dmin, and with finite scales every decoded weight is finite (at most
+// 65504 * 63 * 31 in magnitude).  The reference's decoded-block scratch has no
+// device counterpart (the kernel decodes into registers).
+static lbh_status dequant_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
+                                  size_t out_len, int accumulate, float scale, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    DeviceGuard g(ctx->device);
+    lbh_status st = check_gemv_args(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
+    if (st) return st;
+    HIP_TRY(launch_gemv_dequant(view_of(m), input, out, scale, accumulate, ctx->status, ctx->stream));
+    return scan_verdict(ctx, m->type, input, out, err);
+}
+
+lbh_status lbh_gemv_dequant_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len,
+                                 float *output, size_t output_len, lbh_error *err) {
+    return dequant_checked(ctx, m, input, input_len, output, output_len, 0, 0.0f, err);
+}
+
+lbh_status lbh_gemv_dequant_accumulate_scaled_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input,
+                                                   size_t input_len, float *dest, size_t dest_len, float scale,
+                                                   lbh_error *err) {
+    return dequant_checked(ctx, m, input, input_len, dest, dest_len, 1, scale, err);
+}
+
+lbh_status lbh_gemv_dequant_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x, float *y, float coef,
+                                int32_t accumulate) {
+    if (!ctx || !m || !x || !y) return LBH_NULL_ARGUMENT;
+    DeviceGuard g(ctx->device);
+    return launch_gemv_dequant(view_of(m), x, y, coef, accumulate, nullptr, ctx->stream) == hipSuccess
+               ? LBH_OK
+               : LBH_HIP_ERROR;
 }
 
 lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in, float *out, size_t n, lbh_error *err) {
@@ -650,6 +831,17 @@ lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_exper
         m->wg_r = total;
     }
     m->tile_d = 16;
+    // The down kernel stages the Q8_K of every routed expert's h (up to
+    // MOE_MAX_ROUTED) and the shared expert's in LDS: refuse layers whose
+    // largest launch would not fit a workgroup.
+    {
+        const int lds = moe_down_lds_bytes(td, has_shared ? shared_down->type : td, MOE_MAX_ROUTED, has_shared,
+                                           (int)ffn_r, (int)ffn_s, m->tile_d);
+        if (lds > MOE_MAX_LDS) {
+            free_moe(m);   // owns the table
+            return fail(err, LBH_UNSUPPORTED_SHAPE, td, 0, MOE_MAX_LDS, (uint64_t)lds);
+        }
+    }
     set_batch_defaults(m, MX_MIN_DEFAULT);
     const size_t max_ffn = ffn_r > ffn_s ? ffn_r : ffn_s;
     m->h_stride = (int)max_ffn;
@@ -718,6 +910,9 @@ lbh_status lbh_moe_set_tiles(lbh_moe *m, int32_t wg_routed, int32_t wg_shared, i
     if (!m) return LBH_NULL_ARGUMENT;
     if (wg_routed < 1 || wg_routed > 65536 || wg_shared < 1 || wg_shared > 65536 || tile_d < 1 || tile_d > 256)
         return LBH_INVALID_PARAMETER;
+    if (moe_down_lds_bytes(m->type_down_r, m->has_shared ? m->shared.down.type : m->type_down_r, MOE_MAX_ROUTED,
+                           m->has_shared, (int)m->ffn_r, (int)m->ffn_s, tile_d) > MOE_MAX_LDS)
+        return LBH_UNSUPPORTED_SHAPE;
     m->wg_r = wg_routed;
     m->wg_s = wg_shared;
     m->tile_d = tile_d;
@@ -785,6 +980,9 @@ lbh_status lbh_moe_forward_leased(lbh_ctx *ctx, lbh_moe *m, const lbh_expert_lea
     a.n_launch = (int32_t)n_routed;
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
+    // The slots are read on this call's stream, whichever stream the cache was created on.
+    for (size_t i = 0; i < n_routed; ++i)
+        if (!cache_note_use(m->cache, &leases[i], ctx->stream)) return LBH_HIP_ERROR;
     return LBH_OK;
 }
 
@@ -1262,8 +1460,9 @@ struct lbh_router {
     float *logits;
     MoeRoute *route;     // device
     MoeRoute *route_host;
-    unsigned long long *status;
+    unsigned long long *status;        // [0] first invalid selection input, [1] ring give-up (sticky)
     unsigned long long *status_host;
+    long long spin_limit;              // RouterArgs::spin_limit (0: default)
 };
 
 namespace {
@@ -1293,6 +1492,8 @@ RouterArgs router_args(const lbh_router *r, const float *x, size_t top_k, int32_
     a.top_k = (int32_t)top_k;
     a.mode = mode;
     a.weight_scale = scale;
+    a.spin_limit = r->spin_limit;
+    a.timeout = r->status + 1;
     return a;
 }
 
@@ -1348,6 +1549,12 @@ lbh_status lbh_router_create(lbh_ctx *ctx, const float *weights, size_t n_expert
     return ok(err);
 }
 
+lbh_status lbh_router_set_spin_limit(lbh_router *r, int64_t limit) {
+    if (!r) return LBH_NULL_ARGUMENT;
+    r->spin_limit = limit;
+    return LBH_OK;
+}
+
 lbh_status lbh_router_destroy(lbh_router *r) {
     if (!r) return LBH_NULL_ARGUMENT;
     free_router(r);
@@ -1372,8 +1579,10 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, si
     // The router matvec is gemv_into on an F32 matrix: its input must be finite (gemv.rs:195-211).
     HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
     HIP_TRY(launch_find_nonfinite(x, (long long)x_len, &ctx->status->first_bad_input, ctx->stream));
+    HIP_TRY(hipMemsetAsync(r->status + 1, 0, sizeof(unsigned long long), ctx->stream));
     HIP_TRY(launch_router(a, ctx->stream));
-    HIP_TRY(hipMemcpyAsync(r->status_host, r->status, sizeof(unsigned long long), hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemcpyAsync(r->status_host, r->status, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                           ctx->stream));
     HIP_TRY(hipMemcpyAsync(r->route_host, r->route, sizeof(MoeRoute), hipMemcpyDeviceToHost, ctx->stream));
     lbh_status st = read_status(ctx, err);
     if (st) return st;
@@ -1381,6 +1590,8 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, si
         const unsigned long long i = ctx->status_host->first_bad_input;
         return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, i, 0, 0, read_f32_bits(ctx, x + i), 0);
     }
+    // A router chain whose bounded ring wait gave up left NaN logits behind.
+    if (r->status_host[1] != 0) return fail(err, LBH_DEVICE_TIMEOUT, LBH_F32);
     const unsigned long long bad = r->status_host[0];
     if (bad != ~0ull) {
         const uint64_t e = bad >> 2;

@@ -22,4 +22,9 @@ bool cache_shape(const lbh_expert_cache *c, CacheShape *out);
 bool cache_lease_planes(lbh_expert_cache *c, const lbh_expert_lease *lease, const uint8_t *planes[3],
                         hipEvent_t *ready);
 
+// Records, on `stream`, that the work enqueued there so far reads the lease's
+// slot: an upload that later refills the slot waits for it.  Call after
+// enqueueing the readers and before releasing the lease.
+bool cache_note_use(lbh_expert_cache *c, const lbh_expert_lease *lease, hipStream_t stream);
+
 }  // namespace lbh

@@ -54,7 +54,8 @@ struct Entry {
 struct Slot {
     uint8_t *base;
     hipEvent_t ready;      // recorded on the copy stream after the entry's upload
-    hipEvent_t last_use;   // recorded on the context's stream at each release
+    hipEvent_t last_use;   // recorded on the reading stream by every forward that reads the slot
+    hipStream_t use_stream;  // the stream last_use was last recorded on
     bool used;             // last_use has been recorded at least once
 };
 
@@ -239,6 +240,24 @@ bool cache_lease_planes(lbh_expert_cache *c, const lbh_expert_lease *lease, cons
     return true;
 }
 
+bool cache_note_use(lbh_expert_cache *c, const lbh_expert_lease *lease, hipStream_t stream) {
+    if (!c || !lease || lease->reserved != LEASE_LIVE) return false;
+    std::lock_guard<std::mutex> lk(c->mu);
+    const auto it = c->entries.find(key_of(lease->layer, lease->expert));
+    if (it == c->entries.end() || it->second.state != State::Ready || it->second.slot != lease->slot ||
+        it->second.pins == 0)
+        return false;
+    Slot &s = c->slots[lease->slot];
+    DeviceGuard g(c->device);
+    // One event per slot: a use on a second stream first waits for the use
+    // recorded on the other one, so the new record covers both readers.
+    if (s.used && s.use_stream != stream && hipStreamWaitEvent(stream, s.last_use, 0) != hipSuccess) return false;
+    if (hipEventRecord(s.last_use, stream) != hipSuccess) return false;
+    s.used = true;
+    s.use_stream = stream;
+    return true;
+}
+
 }  // namespace lbh
 
 extern "C" {
@@ -293,6 +312,7 @@ lbh_status lbh_expert_cache_create(lbh_ctx *ctx, const lbh_expert_cache_config *
         s.base = c->slab + i * c->slot_stride;
         s.used = false;
         s.ready = s.last_use = nullptr;
+        s.use_stream = nullptr;
         e = hipEventCreateWithFlags(&s.ready, hipEventDisableTiming);
         if (e == hipSuccess) e = hipEventCreateWithFlags(&s.last_use, hipEventDisableTiming);
     }
@@ -398,14 +418,9 @@ lbh_status lbh_expert_cache_release(lbh_expert_cache *c, lbh_expert_lease *lease
     if (it == c->entries.end() || it->second.state != State::Ready || it->second.slot != lease->slot ||
         it->second.pins == 0)
         return LBH_INVALID_PARAMETER;
-    // The slot's readers so far are on the context's stream: a later upload into
-    // it waits for this point (recorded before the pin goes).
-    Slot &s = c->slots[lease->slot];
-    {
-        DeviceGuard g(c->device);
-        if (hipEventRecord(s.last_use, c->ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
-    }
-    s.used = true;
+    // Every kernel that reads the slot recorded its use when it was enqueued
+    // (cache_note_use, on the stream it runs on), so a later upload into the
+    // slot waits for it whichever stream it was: nothing to record here.
     it->second.pins -= 1;
     if (it->second.pins == 0 && !it->second.resident) {   // ephemeral entry (lib.rs:429-440)
         c->free_slots.push_back(it->second.slot);

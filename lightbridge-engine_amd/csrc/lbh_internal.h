@@ -75,6 +75,12 @@ struct RouterArgs {
     int32_t n_experts, hidden, top_k, mode;
     float weight_scale;
     int32_t pad;
+    // Bounded waits of the router chains' LDS ring: polls before giving up
+    // (0: the default 2^22; < 0: give up at once, a host-forced test of that
+    // path).  A chain that gives up stores a NaN logit (the selection then
+    // rejects the route) and sets *timeout to 1 (sticky; optional).
+    long long spin_limit;
+    unsigned long long *timeout;
 };
 
 // Device status of one MoE call (~0 when clean).
@@ -226,6 +232,10 @@ hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_gate_up(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_down(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_reset_status(MoeStatus *st, hipStream_t s);
+// LDS of one single-token MoE down launch (gfx950 gives a workgroup at most MOE_MAX_LDS).
+constexpr int MOE_MAX_LDS = 160 * 1024;
+int moe_down_lds_bytes(int type_down_r, int type_down_s, int n_routed, int has_shared, int ffn_r, int ffn_s,
+                       int tile_d);
 hipError_t launch_expf(const float *in, float *out, long long n, int swiglu, const float *up, hipStream_t s);
 
 hipError_t launch_quantize_q8k(const float *x, uint8_t *out, long long nblocks, const DevStatus *st,
@@ -240,5 +250,13 @@ hipError_t launch_repack_range(int ty, const uint8_t *src, uint8_t *dst, long lo
 hipError_t launch_validate_scales(int ty, const uint8_t *ggml, long long units,
                                   unsigned long long *first, hipStream_t s);
 hipError_t launch_f16_to_f32(const uint16_t *in, float *out, long long n, hipStream_t s);
+
+// Raw GGML row dots (vec_dot_q8_k per row; 1 <= nb <= 64), the Q8_K scale scan
+// and the DequantF32 matvec (lbh_dot.hip).  `st` words set -> no writes.
+hipError_t launch_dot_ggml(int ty, const uint8_t *w, long long rows, int nb, const uint8_t *q8, float *y,
+                           const DevStatus *st, hipStream_t s);
+hipError_t launch_find_nonfinite_q8(const uint8_t *q8, long long nblocks, unsigned long long *first, hipStream_t s);
+hipError_t launch_gemv_dequant(const MatView &m, const float *x, float *y, float coef, int accumulate,
+                               const DevStatus *st, hipStream_t s);
 
 }  // namespace lbh

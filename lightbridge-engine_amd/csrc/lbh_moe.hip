@@ -213,16 +213,24 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
     if (a.select_in_kernel) {
         // Every workgroup selects the same route from the finished logits;
         // workgroup wg_s publishes it for the down kernel.
+        // A non-finite logit (or a router chain that gave up) makes the route
+        // invalid: it is published with n = -1, nothing is computed and the
+        // down kernel leaves y unchanged.
+        __shared__ int s_invalid;
         if (threadIdx.x < 64) {
             MoeRoute r;
             unsigned long long bad;
             select_route(a.router, r, bad);
+            if (bad != ~0ull) r.n = -1;
             if (threadIdx.x == 0) {
 #pragma unroll
                 for (int q = 0; q < MOE_MAX_ROUTED; ++q) s_ids[q] = r.ids[q];
+                s_invalid = bad != ~0ull;
                 if ((int)blockIdx.x == wg_s) *const_cast<MoeRoute *>(a.route_dev) = r;
             }
         }
+        __syncthreads();
+        if (s_invalid) return;
     } else if (threadIdx.x < MOE_MAX_ROUTED) {
         s_ids[threadIdx.x] = route_id(a, threadIdx.x < route_n(a) ? threadIdx.x : 0);
     }
@@ -318,6 +326,7 @@ template <int TYR, int LPUR, int TYS, int LPUS>
 __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     if (a.status && (a.status->first_bad_input != ~0ull || a.status->first_bad_swiglu != ~0ull)) return;
+    if (a.route_dev && a.route_dev->n < 0) return;   // invalid device route: y unchanged
     // Wave index and route count through readfirstlane: the task choice below
     // (and every descriptor derived from it) is wave-uniform.
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -480,17 +489,43 @@ static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Dynamic LDS of a down launch over n routed experts: the codebooks, one fold
+// table per wave, the per-row down outputs of every expert and the Q8_K of
+// every expert's h.
+template <int TYR, int TYS>
+static int down_lds(int n, int has_shared, int ffn_r, int ffn_s, int tile_d) {
+    const int waves = n + (has_shared ? DOWN_SHARED_WAVES : 0);
+    const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
+    const int q8 = (n * (ffn_r / 256) + (has_shared ? ffn_s / 256 : 0)) * 292;
+    return align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES) +
+           nw * down_fold_bytes<TYR, TYS>() + (MOE_MAX_ROUTED + 1) * tile_d * 4 + align16(q8);
+}
+
 template <int TYR, int TYS>
 static hipError_t down_typed(const MoeArgs &a, hipStream_t s) {
     const int n = a.route_dev ? a.n_launch : a.route.n;
     const int waves = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
     const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
-    const int q8 = (n * (a.ffn_r / 256) + (a.has_shared ? a.ffn_s / 256 : 0)) * 292;
-    const int lds = align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES) +
-                    nw * down_fold_bytes<TYR, TYS>() + (MOE_MAX_ROUTED + 1) * a.tile_d * 4 + align16(q8);
-    hipLaunchKernelGGL((k_moe_down<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>), dim3(cdiv(a.hidden, a.tile_d)),
-                       dim3(64 * nw), lds, s, a);
+    const int lds = down_lds<TYR, TYS>(n, a.has_shared, a.ffn_r, a.ffn_s, a.tile_d);
+    if (lds > MOE_MAX_LDS) return hipErrorInvalidValue;
+    auto kernel = k_moe_down<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>;
+    if (lds > 64 * 1024) {
+        const hipError_t e =
+            hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(kernel, dim3(cdiv(a.hidden, a.tile_d)), dim3(64 * nw), lds, s, a);
     return hipGetLastError();
+}
+
+int moe_down_lds_bytes(int type_down_r, int type_down_s, int n_routed, int has_shared, int ffn_r, int ffn_s,
+                       int tile_d) {
+    const int tyr = type_down_r, ts = has_shared ? type_down_s : type_down_r;
+    if (tyr == T_IQ3_S && ts == T_Q5_K) return down_lds<T_IQ3_S, T_Q5_K>(n_routed, has_shared, ffn_r, ffn_s, tile_d);
+    if (tyr == T_IQ3_S && ts == T_IQ3_S) return down_lds<T_IQ3_S, T_IQ3_S>(n_routed, has_shared, ffn_r, ffn_s, tile_d);
+    if (tyr == T_IQ2_S && ts == T_IQ2_S) return down_lds<T_IQ2_S, T_IQ2_S>(n_routed, has_shared, ffn_r, ffn_s, tile_d);
+    if (tyr == T_IQ2_S && ts == T_IQ3_S) return down_lds<T_IQ2_S, T_IQ3_S>(n_routed, has_shared, ffn_r, ffn_s, tile_d);
+    return 0x7fffffff;
 }
 
 hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s) {

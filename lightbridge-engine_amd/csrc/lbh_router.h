@@ -23,7 +23,11 @@ __device__ __forceinline__ unsigned long long sel_key(float score, uint32_t id) 
 // four inputs each), producer wave w owning the chunks congruent to w - 1
 // mod 3.  Slots change hands through workgroup-scope release/acquire flags:
 // ready[slot] = index of the chunk it holds, done = last chunk consumed.
-// Each wait is bounded, so no wave can wait forever.
+// Each wait is bounded, so no wave can wait forever.  A wave whose wait gives
+// up reports it: the consumer stores NaN logits (which the selection rejects
+// as non-finite, routing.rs:72-77) and marks done as past every chunk so the
+// producers stop waiting; a producer stops producing (the consumer's wait for
+// its chunk then gives up too).  Either sets the sticky *timeout word.
 constexpr int RT_EXPERTS = 8;
 constexpr int RT_STEPS = 64;
 constexpr int RT_SLOTS = 4;
@@ -43,7 +47,12 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
     const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
     const int n = a.n_experts;
     const int nch = a.hidden / (4 * RT_STEPS);   // hidden is a multiple of 256
-    constexpr long long SPIN = 1ll << 22;
+    // spin_limit < 0 forces every wait to give up (a deterministic test of that path).
+    const bool force = a.spin_limit < 0;
+    const long long SPIN = a.spin_limit > 0 ? a.spin_limit : force ? 0 : (1ll << 22);
+    auto gave_up = [&]() {
+        if (lane == 0 && a.timeout) __hip_atomic_store(a.timeout, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
     if (tid < RT_SLOTS) ready[tid] = -1;
     if (tid == 0) *done = -1;
     __syncthreads();
@@ -53,6 +62,10 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
         const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
         for (int c = wid - 1; c < nch; c += 3) {
             for (long long k = 0; k < SPIN && lds_acquire(done) < c - RT_SLOTS; ++k) __builtin_amdgcn_s_sleep(1);
+            if (force || lds_acquire(done) < c - RT_SLOTS) {
+                gave_up();
+                break;
+            }
             float4 v[RT_STEPS * RT_EXPERTS / 64], xv[RT_STEPS * RT_EXPERTS / 64];
 #pragma unroll
             for (int k = 0; k < RT_STEPS * RT_EXPERTS / 64; ++k) {
@@ -78,6 +91,12 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
         float sum = 0.0f;
         for (int c = 0; c < nch; ++c) {
             for (long long k = 0; k < SPIN && lds_acquire(&ready[c % RT_SLOTS]) != c; ++k) __builtin_amdgcn_s_sleep(1);
+            if (force || lds_acquire(&ready[c % RT_SLOTS]) != c) {
+                gave_up();
+                sum = __int_as_float(0x7fc00000);
+                if (lane == 0) lds_release(done, 0x7fffffff);
+                break;
+            }
             const float4 *slot = ring + (c % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
             // Rolling eight-step read-ahead over the fully unrolled chunk: every
             // index is a compile-time constant, so reads stay in registers.

@@ -30,7 +30,7 @@ STATUS = {
     20: "DimensionMismatch", 21: "ScratchTooSmall", 22: "NonFiniteValue",
     23: "RoutedExpertOrder", 24: "DuplicateRoutedExpert", 25: "InvalidParameter",
     36: "SourceReadFailed",
-    100: "HipError", 101: "NullArgument", 102: "UnsupportedShape",
+    100: "HipError", 101: "NullArgument", 102: "UnsupportedShape", 103: "DeviceTimeout",
 }
 QUANT_ERRORS = {1, 2, 3, 4, 6, 7, 8, 9, 10}
 
@@ -100,6 +100,12 @@ def lib() -> C.CDLL:
             "lbh_gemv_q8_k": ([p, p, p, p, C.c_float, i32], i32),
             "lbh_gemv_f32": ([p, p, p, p, p, C.c_float, i32], i32),
             "lbh_gemv_block_sums": ([p, p, p, p], i32),
+            "lbh_validate_vec_dot_q8_k": ([p, i32, p, sz, sz, p, sz, sz, E], i32),
+            "lbh_vec_dot_q8_k_into": ([p, i32, p, sz, sz, p, sz, sz, p, sz, E], i32),
+            "lbh_gemv_q8_k_into": ([p, p, p, sz, p, sz, C.c_float, i32, E], i32),
+            "lbh_gemv_dequant_into": ([p, p, p, sz, p, sz, E], i32),
+            "lbh_gemv_dequant_accumulate_scaled_into": ([p, p, p, sz, p, sz, C.c_float, E], i32),
+            "lbh_gemv_dequant_f32": ([p, p, p, p, C.c_float, i32], i32),
             "lbh_debug_f16_to_f32": ([p, p, p, sz, E], i32),
             "lbh_moe_create": ([p, p, p, p, sz, p, p, p, C.POINTER(p), E], i32),
             "lbh_moe_destroy": ([p], i32),
@@ -110,6 +116,7 @@ def lib() -> C.CDLL:
             "lbh_debug_expf_host": ([p, p, sz, i32, p], None),
             "lbh_router_create": ([p, p, sz, sz, p, i32, C.POINTER(p), E], i32),
             "lbh_router_destroy": ([p], i32),
+            "lbh_router_set_spin_limit": ([p, C.c_int64], i32),
             "lbh_router_route_into": ([p, p, p, sz, sz, i32, C.c_float, p, p, p, E], i32),
             "lbh_moe_block_forward": ([p, p, p, p, sz, i32, C.c_float, p], i32),
             "lbh_moe_reserve_batch": ([p, sz, sz, E], i32),
@@ -249,6 +256,53 @@ class HipBackend:
         if st:
             raise KernelError(LbhError(status=st))
 
+    def gemv_q8_k_into(self, m: "DeviceMatrix", q8, y, coef: float = 0.0, accumulate: bool = False) -> None:
+        """Checked matvec over caller-supplied Q8_K bytes (validate_q8_scales,
+        crates/bridge-quant-layout/src/q8_k.rs:208-222, before any write)."""
+        _call(lib().lbh_gemv_q8_k_into, self.ctx, m.handle, _dev_ptr(q8), q8.numel(), _dev_ptr(y), y.numel(), coef,
+              1 if accumulate else 0)
+
+    # -- the reference's dot API over raw GGML rows (q8_k.rs:80-101, :172-186) --------------
+    def validate_vec_dot_q8_k(self, ty: int, weights, q8, logical_elements: int, rows: int = 1) -> None:
+        _call(lib().lbh_validate_vec_dot_q8_k, self.ctx, ty, _dev_ptr(weights), weights.numel(), rows, _dev_ptr(q8),
+              q8.numel(), logical_elements)
+
+    def vec_dot_q8_k_into(self, ty: int, weights, q8, logical_elements: int, out, rows: int = 1) -> None:
+        """out[r] = vec_dot_q8_k(ty, row r of `weights`, q8, logical_elements)."""
+        _call(lib().lbh_vec_dot_q8_k_into, self.ctx, ty, _dev_ptr(weights), weights.numel(), rows, _dev_ptr(q8),
+              q8.numel(), logical_elements, _dev_ptr(out), out.numel())
+
+    def vec_dot_q8_k(self, ty: int, weights, q8, logical_elements: int) -> float:
+        import torch
+        out = torch.zeros(1, dtype=torch.float32, device=weights.device)
+        self.vec_dot_q8_k_into(ty, weights, q8, logical_elements, out)
+        return float(out.item())
+
+    def vec_dot_q4_k_q8_k(self, weights, q8, logical_elements: int) -> float:
+        return self.vec_dot_q8_k(Q4_K, weights, q8, logical_elements)
+
+    def vec_dot_q5_k_q8_k(self, weights, q8, logical_elements: int) -> float:
+        return self.vec_dot_q8_k(Q5_K, weights, q8, logical_elements)
+
+    def vec_dot_iq2_s_q8_k(self, weights, q8, logical_elements: int) -> float:
+        return self.vec_dot_q8_k(IQ2_S, weights, q8, logical_elements)
+
+    def vec_dot_iq3_s_q8_k(self, weights, q8, logical_elements: int) -> float:
+        return self.vec_dot_q8_k(IQ3_S, weights, q8, logical_elements)
+
+    # -- DequantF32 execution mode (gemv.rs:12-16, :305-328) ------------------------------
+    def gemv_dequant_into(self, m: "DeviceMatrix", x, y) -> None:
+        _call(lib().lbh_gemv_dequant_into, self.ctx, m.handle, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel())
+
+    def gemv_dequant_accumulate_scaled_into(self, m: "DeviceMatrix", x, dest, scale: float) -> None:
+        _call(lib().lbh_gemv_dequant_accumulate_scaled_into, self.ctx, m.handle, _dev_ptr(x), x.numel(),
+              _dev_ptr(dest), dest.numel(), scale)
+
+    def gemv_dequant_f32(self, m: "DeviceMatrix", x, y, coef: float = 0.0, accumulate: bool = False) -> None:
+        st = lib().lbh_gemv_dequant_f32(self.ctx, m.handle, _dev_ptr(x), _dev_ptr(y), coef, 1 if accumulate else 0)
+        if st:
+            raise KernelError(LbhError(status=st))
+
     def gemm_q8_k(self, m: "DeviceMatrix", q8, n_tokens: int, y, workspace) -> None:
         """y[t, r] = vec_dot_q8_k(row r, token t) for a batch of Q8_K rows on the
         matrix cores (the matrix must be prepared with DeviceMatrix.prepare_gemm)."""
@@ -349,6 +403,10 @@ class Router:
               weight_scale, C.c_void_p(ids.ctypes.data), C.c_void_p(coefs.ctypes.data),
               C.c_void_p(logits.ctypes.data) if logits is not None else None)
         return (ids, coefs, logits) if want_logits else (ids, coefs)
+
+    def set_spin_limit(self, limit: int) -> None:
+        """Polls of the router chains' bounded waits (0 default, < 0 give up at once: a test knob)."""
+        lib().lbh_router_set_spin_limit(self.handle, limit)
 
     def close(self) -> None:
         if self.handle:

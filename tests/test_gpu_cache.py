@@ -291,3 +291,44 @@ def test_forward_leased_rejects_bad_leases(be, oracle, tmp_path):
         be.moe_forward(layer, np.array([0], np.uint32), np.array([1.0], np.float32), x, y)
     layer.close()
     cache.close()
+
+
+def test_forward_leased_on_another_stream_keeps_slots_until_read(be, oracle, tmp_path):
+    """The layer runs on a second stream (its own context) while the cache was
+    created on the first: each slot's last use is recorded on the stream that
+    reads it, so a refill on the copy stream waits for the second stream's
+    queued forward, not for the cache context's idle stream.  A bounded spin
+    before each forward keeps the readers queued while later misses evict."""
+    import lbhip
+    from lbhip.cache import CachedMoeLayer
+    s = Streamed(be, oracle, tmp_path, 12)
+    cache = make_cache(be, 5)
+    side = torch.cuda.Stream()
+    be2 = lbhip.HipBackend(0, stream=side)
+    layer = CachedMoeLayer(be2, cache, s.shared)
+    rng = np.random.default_rng(21)
+    xs = rng.standard_normal((10, HID)).astype(np.float32)
+    xd = dev(xs)
+    ys = torch.full((10, HID), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    routes = []
+    for t in range(10):
+        ids = np.sort(rng.choice(12, 4, replace=False)).astype(np.uint32)
+        coefs = rng.random(4).astype(np.float32)
+        routes.append((ids, coefs))
+        leases = [s.lease(cache, int(e)) for e in ids]
+        with torch.cuda.stream(side):
+            if hasattr(torch.cuda, "_sleep"):
+                torch.cuda._sleep(2_000_000)      # ~1 ms of bounded spinning on the side stream
+        layer.forward_leased(leases, coefs, xd[t], ys[t])
+        for lease in leases:
+            lease.release()
+    torch.cuda.synchronize()
+    got = ys.cpu().numpy()
+    for t, (ids, coefs) in enumerate(routes):
+        want = s.want(oracle, ids, coefs, xs[t])
+        assert np.array_equal(got[t].view(np.uint32), want.view(np.uint32)), f"token {t}"
+    assert cache.stats()["evictions"] > 0
+    layer.close()
+    cache.close()
+    be2.close()
