@@ -108,17 +108,55 @@ class Timer:
         return e0.elapsed_time(e1) * 1e-3   # seconds
 
 
+def logical_cpus():
+    """Logical CPUs this process may run on (the box's share, not the machine's count)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_threads():
-    from oracle import lb_oracle as orc
-    return min(orc.default_threads(), 16)
+    """recommended_thread_count (crates/bridge-kernels-cpu/src/lib.rs:121-126): ceil(logical / 2)."""
+    return max(1, (logical_cpus() + 1) // 2)
 
 
-def cpu_matvec_step(w_gate, w_down, seconds):
+def host_cpu():
+    """lscpu-style facts of the host the CPU baselines ran on: model name, physical
+    cores (distinct (package, core) pairs among the CPUs this process may use) and
+    logical CPUs."""
+    model, cores = "unknown", set()
+    allowed = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else None
+    try:
+        cpu, phys = None, None
+        for line in Path("/proc/cpuinfo").read_text().splitlines() + [""]:
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "processor":
+                cpu = int(v)
+            elif k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id" and cpu is not None and (allowed is None or cpu in allowed):
+                cores.add((phys, v))
+    except OSError:
+        pass
+    return {"cpu_model": model, "physical_cores": len(cores) or None, "logical_cpus": logical_cpus()}
+
+
+def _cpu_fields(threads):
+    d = {"cores": threads, "threads": threads}
+    d.update(host_cpu())
+    return d
+
+
+def cpu_matvec_step(w_gate, w_down, seconds, threads=None):
     """Oracle AVX2 path for the headline step: gemv_into (quantize + row dots) of
     the gate, then of the down projection on its output."""
     import numpy as np
     from oracle import lb_oracle as orc
-    threads = cpu_threads()
+    threads = threads or cpu_threads()
     ex = orc.make_exec(orc.MODE_CPU_PARALLEL_Q8K, threads, True)
     mg = orc.make_matrix(22, FFN, HIDDEN, w_gate)
     md = orc.make_matrix(21, HIDDEN, FFN, w_down)
@@ -132,11 +170,11 @@ def cpu_matvec_step(w_gate, w_down, seconds):
         el = time.perf_counter() - t0
         if (el >= seconds and n >= 3) or el >= 4 * seconds:
             break
-    return {"value": round(STEP_BYTES * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(STEP_BYTES * n / el / 1e9, 3), "unit": "GB/s", **_cpu_fields(threads), "kind": "port",
             "ms_per_step": round(el / n * 1e3, 4),
             "sample": f"{n} steps of the headline step (Q8_K + IQ2_S gate 1536x4096, Q8_K + IQ3_S down "
                       f"4096x1536) in {el:.2f} s; oracle AVX2 restatement, rows over {threads} threads "
-                      f"(ceil(nproc/2), the reference's default) of {os.cpu_count()} logical CPUs"}
+                      f"of {logical_cpus()} logical CPUs"}
 
 
 def cpu_q4k(w, seconds):
@@ -154,7 +192,7 @@ def cpu_q4k(w, seconds):
         el = time.perf_counter() - t0
         if (el >= seconds and n >= 3) or el >= 4 * seconds:
             break
-    return {"value": round(Q4K_BYTES * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(Q4K_BYTES * n / el / 1e9, 3), "unit": "GB/s", **_cpu_fields(threads), "kind": "port",
             "sample": f"{n} Q4_K 4096x4096 gemv_into calls in {el:.2f} s, {threads} threads"}
 
 
@@ -180,7 +218,7 @@ def cpu_moe(experts_np, shared_np, router_w, xs, seconds):
                 break
         out["preflight" if preflight else "single_pass"] = (n / el, n, el)
     best = max(v[0] for v in out.values())
-    return {"value": round(best, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(best, 3), "unit": "tokens/s", **_cpu_fields(threads), "kind": "port",
             "faithful_with_preflight_tokens_per_s": round(out["preflight"][0], 3),
             "single_pass_tokens_per_s": round(out["single_pass"][0], 3),
             "sample": f"{out['preflight'][1]} + {out['single_pass'][1]} tokens through the 192-expert block "
@@ -283,15 +321,12 @@ def bench_model_shapes(args, be, timer, torch, np, synth):
 
 
 def bench_moe(args, be, timer, torch, np, synth, lbhip):
-    g = torch.from_numpy(synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, 301).reshape(-1)).cuda()
-    u = torch.from_numpy(synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, 302).reshape(-1)).cuda()
-    d = torch.from_numpy(synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, 303).reshape(-1)).cuda()
-    # 192 distinct experts: block-rotated copies of three seeded matrices.
-    gate_t = [torch.roll(g, 82 * e) for e in range(N_EXPERTS)]
-    up_t = [torch.roll(u, 82 * e) for e in range(N_EXPERTS)]
-    down_t = [torch.roll(d, 110 * e) for e in range(N_EXPERTS)]
-    experts = [(be.upload(synth.IQ2_S, FFN, HIDDEN, gate_t[e]), be.upload(synth.IQ2_S, FFN, HIDDEN, up_t[e]),
-                be.upload(synth.IQ3_S, HIDDEN, FFN, down_t[e])) for e in range(N_EXPERTS)]
+    # 192 experts, every matrix random from its own seed.
+    experts_np = [(synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, 3000 + 3 * e),
+                   synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, 3001 + 3 * e),
+                   synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, 3002 + 3 * e)) for e in range(N_EXPERTS)]
+    experts = [(be.upload(synth.IQ2_S, FFN, HIDDEN, g), be.upload(synth.IQ2_S, FFN, HIDDEN, u),
+                be.upload(synth.IQ3_S, HIDDEN, FFN, d)) for g, u, d in experts_np]
     shared_np = (synth.random_matrix(synth.Q4_K, HIDDEN, HIDDEN, 304), synth.random_matrix(synth.Q4_K, HIDDEN, HIDDEN, 305),
                  synth.random_matrix(synth.Q5_K, HIDDEN, HIDDEN, 306))
     shared = (be.upload(synth.Q4_K, HIDDEN, HIDDEN, shared_np[0]), be.upload(synth.Q4_K, HIDDEN, HIDDEN, shared_np[1]),
@@ -316,7 +351,6 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
 
     torch.cuda.synchronize()
     host = lambda t: t.cpu().numpy()  # noqa: E731
-    experts_np = [(host(gate_t[e]), host(up_t[e]), host(down_t[e])) for e in range(N_EXPERTS)]
     res = {"workload": "configs[2]: MoE FFN block, 1 token: 192 experts (IQ2_S gate/up 1536x4096, IQ3_S down "
                        "4096x1536), top-8 softmax of an F32 4096x192 router, Q4_K/Q5_K shared expert ffn 4096",
            "tokens_timed": T * reps, "distinct_experts_hit": hit,
@@ -488,7 +522,7 @@ def cpu_batch(experts_np, shared_np, check, seconds):
         el = time.perf_counter() - t0
         if (el >= seconds and n >= 2) or el >= 2 * seconds:
             break
-    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(n / el, 3), "unit": "tokens/s", **_cpu_fields(threads), "kind": "port",
             "sample": f"{n} tokens of the configs[3] batch (its Zipf routes) through moe_routed_by_id_into, single "
                       f"pass, one token at a time as the reference decodes, in {el:.2f} s, {threads} threads"}
 
@@ -598,7 +632,7 @@ def cpu_prefill(check, seconds):
         if (el >= seconds and n >= 2) or el >= 2 * seconds:
             break
     ops = 2.0 * PF_ROWS * HIDDEN * n
-    return {"value": round(ops / el / 1e12, 5), "unit": "TOP/s", "cores": threads, "kind": "port",
+    return {"value": round(ops / el / 1e12, 5), "unit": "TOP/s", **_cpu_fields(threads), "kind": "port",
             "sample": f"{n} tokens x 12288 rows of Q5_K dots (gemv over pre-quantized Q8_K) in {el:.2f} s, "
                       f"{threads} threads; the full 512-token step would take {512 * el / n:.2f} s"}
 
@@ -740,6 +774,8 @@ def main():
                                "(one routed expert's decode pass, one token)",
                    "step": "Q8_K(x)+IQ2_S gate -> Q8_K(h)+IQ3_S down: 2 fused kernels per step, HIP graph",
                    "weight_copies_in_rotation": mv["copies"],
+                   "steps_note": "the timed steps are rounded up to whole rotations of the weight copies, so "
+                                 "`steps` can exceed --steps",
                    "rotation_bytes": mv["copies"] * (mv["w_gate"].nbytes + mv["w_down"].nbytes),
                    "algorithmic_bytes_per_step": STEP_BYTES, "lpu": args.lpu},
         "roofline": {"bound": "hbm", "kernel": dom[0], "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
@@ -759,7 +795,11 @@ def main():
         line["expert_streaming"] = streaming
     if not args.no_cpu:
         _progress("CPU baselines")
-        line["cpu_baseline"] = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds)
+        line["cpu_baseline"] = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds / 2)
+        allc = cpu_matvec_step(mv["w_gate"], mv["w_down"], args.cpu_seconds / 2, threads=logical_cpus())
+        line["cpu_baseline"]["all_cores"] = {k: allc[k] for k in ("value", "unit", "threads", "ms_per_step", "sample")}
+        line["cpu_baseline"]["threads_rule"] = ("ceil(logical CPUs / 2), recommended_thread_count "
+                                                "(crates/bridge-kernels-cpu/src/lib.rs:121-126); all_cores beside it")
         _progress("CPU configs[1] done")
         cq = cpu_q4k(w_q4k, args.cpu_seconds / 2)
         q4k["cpu_baseline"] = cq

@@ -347,6 +347,11 @@ lbh_status lbh_moe_set_batch_engine(lbh_moe *moe, int32_t mx_min_tokens, int32_t
 lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids_dev, const float *coefs_dev,
                                  size_t n_tokens, size_t top_k, const float *x_dev, float *y_dev);
 
+/* [async] lbh_moe_forward_batch with the residual add of each token's block fused
+ * into the combine: hidden_dev[t][i] += ffn_delta[t][i] (layer.rs:464, norm.rs:83-98). */
+lbh_status lbh_moe_forward_batch_residual(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids_dev, const float *coefs_dev,
+                                          size_t n_tokens, size_t top_k, const float *x_dev, float *hidden_dev);
+
 /* [sync] Checked form with host routing: every token's ids/coefs are validated with
  * the rules and error variants of moe_routed_by_id_into (moe.rs:73-129; err->row =
  * the token), then x must be finite (NonFiniteValue, index = lane, row = token); on
@@ -390,6 +395,15 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *router, const float *
  * or a router chain whose bounded wait gave up) leaves y unchanged. */
 lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev, size_t top_k,
                                  int32_t mode, float weight_scale, float *y_dev);
+
+/* [async] lbh_moe_block_forward ending as hy3_block_forward_token does
+ * (crates/bridge-kernels-reference/src/layer.rs:429-464): the block's output is
+ * added to the hidden state in place, hidden[i] = hidden[i] + ffn_delta[i]
+ * (residual_add_in_place, norm.rs:83-98, fused into the combine; its finiteness
+ * checks are not made: unchecked like the forward).  x_dev is the normalized
+ * FFN input, hidden_dev the residual stream [hidden]. */
+lbh_status lbh_moe_block_forward_residual(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev,
+                                          size_t top_k, int32_t mode, float weight_scale, float *hidden_dev);
 
 /* ---- HBM expert cache ---------------------------------------------------------
  * Counterpart of CompressedCache<ExpertKey> (crates/bridge-cache/src/lib.rs:32-595)

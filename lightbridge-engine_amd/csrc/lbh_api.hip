@@ -1366,17 +1366,28 @@ lbh_status lbh_moe_set_batch_engine(lbh_moe *m, int32_t mx_min_tokens, int32_t m
     return LBH_OK;
 }
 
-lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_tokens,
-                                 size_t top_k, const float *x, float *y) {
+static lbh_status forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_tokens,
+                                size_t top_k, const float *x, float *y, int residual) {
     if (!ctx || !m || !ids || !coefs || !x || !y) return LBH_NULL_ARGUMENT;
     if (n_tokens == 0 || top_k == 0) return LBH_DIMENSION_MISMATCH;
     if (!m->batch_mem || n_tokens > m->cap_tokens || top_k > m->cap_k) return LBH_SCRATCH_TOO_SMALL;
     DeviceGuard g(ctx->device);
     BatchArgs a = batch_args(m, ids, coefs, n_tokens, top_k, x, y);
+    a.residual = residual;
     a.gemm_shape = ctx->gemm_shape;
     const BatchStreams bs = batch_streams(m);
     if (launch_moe_batch(a, ctx->stream, &bs) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;
+}
+
+lbh_status lbh_moe_forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_tokens,
+                                 size_t top_k, const float *x, float *y) {
+    return forward_batch(ctx, m, ids, coefs, n_tokens, top_k, x, y, 0);
+}
+
+lbh_status lbh_moe_forward_batch_residual(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs,
+                                          size_t n_tokens, size_t top_k, const float *x, float *hidden) {
+    return forward_batch(ctx, m, ids, coefs, n_tokens, top_k, x, hidden, 1);
 }
 
 lbh_status lbh_moe_routed_by_id_batch_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs,
@@ -1619,14 +1630,15 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, si
     return ok(err);
 }
 
-lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const float *x, size_t top_k, int32_t mode,
-                                 float weight_scale, float *y) {
+static lbh_status block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const float *x, size_t top_k, int32_t mode,
+                                float weight_scale, float *y, int residual) {
     if (!ctx || !m || !r || !x || !y) return LBH_NULL_ARGUMENT;
     if (r->n_experts != m->n_experts || r->hidden != m->hidden) return LBH_DIMENSION_MISMATCH;
     if (top_k == 0 || top_k > r->n_experts || top_k > MOE_MAX_ROUTED) return LBH_INVALID_PARAMETER;
     if (mode != 0 && (mode != 1 || !r->bias)) return LBH_INVALID_PARAMETER;
     DeviceGuard g(ctx->device);
     MoeArgs a = moe_args(m, x, y);
+    a.residual = residual;
     a.router = router_args(r, x, top_k, mode, weight_scale);
     a.route_dev = r->route;
     a.route.n = (int32_t)top_k;
@@ -1643,6 +1655,16 @@ lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const 
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;
+}
+
+lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const float *x, size_t top_k, int32_t mode,
+                                 float weight_scale, float *y) {
+    return block_forward(ctx, m, r, x, top_k, mode, weight_scale, y, 0);
+}
+
+lbh_status lbh_moe_block_forward_residual(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const float *x, size_t top_k,
+                                          int32_t mode, float weight_scale, float *hidden) {
+    return block_forward(ctx, m, r, x, top_k, mode, weight_scale, hidden, 1);
 }
 
 }  // extern "C"

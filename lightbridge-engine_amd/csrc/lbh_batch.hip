@@ -1056,7 +1056,7 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_combine(BatchArgs a) {
             acc = __fadd_rn(acc, __fmul_rn(a.coefs[t * a.top_k + s], a.d_r[(long long)p * a.hidden + r]));
         }
         if (a.has_shared) acc = __fadd_rn(acc, __fmul_rn(1.0f, a.d_s[(long long)t * a.hidden + r]));
-        a.y[k] = acc;
+        a.y[k] = a.residual ? __fadd_rn(a.y[k], acc) : acc;
     }
 }
 

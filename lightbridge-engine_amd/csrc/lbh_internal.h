@@ -122,6 +122,10 @@ struct MoeArgs {
     // travel in the arguments (no dependent load of the expert table before
     // the first weight loads); every routed expert has routed_shape's views.
     int32_t routed_given;
+    // residual != 0: the combine adds the block's output to y in place,
+    // y[r] = y[r] + delta[r] (residual_add_in_place, crates/bridge-kernels-
+    // reference/src/norm.rs:83-98, as hy3_block_forward_token ends, layer.rs:464).
+    int32_t residual;
     ExpertDev routed_shape;
     const uint8_t *routed_planes[MOE_MAX_ROUTED][3];   // gate, up, down
 };
@@ -192,6 +196,7 @@ struct BatchArgs {
     // scales apart) of x and of the routed and shared h; the VALU streams take the smaller chunks
     // and stage vc = min(tc, mx_min - 1) tokens (tc when mx = 0).
     int32_t mx, mx_min, mx_split_gu, mx_split_d, vc;
+    int32_t residual;           // y[t][r] += delta (as MoeArgs::residual)
     uint8_t *xq_mx, *hq_mx_r, *hq_mx_s;
     float *xd_mx, *hd_mx_r, *hd_mx_s;
 };

@@ -439,7 +439,7 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
             if (bad < 0 && !isfinite(acc)) bad = s;
         }
         if (a.has_shared && n <= a.stop_step) acc = __fadd_rn(acc, __fmul_rn(1.0f, s_y[n * ystride + t]));
-        a.y[r0 + t] = acc;
+        a.y[r0 + t] = a.residual ? __fadd_rn(a.y[r0 + t], acc) : acc;
         // A later accumulation call rejects a non-finite destination
         // (gemv.rs:126-127): record the step after which it first appeared.
         if (a.check && bad >= 0 && bad < last)

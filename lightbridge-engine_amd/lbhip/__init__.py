@@ -119,6 +119,8 @@ def lib() -> C.CDLL:
             "lbh_router_set_spin_limit": ([p, C.c_int64], i32),
             "lbh_router_route_into": ([p, p, p, sz, sz, i32, C.c_float, p, p, p, E], i32),
             "lbh_moe_block_forward": ([p, p, p, p, sz, i32, C.c_float, p], i32),
+            "lbh_moe_block_forward_residual": ([p, p, p, p, sz, i32, C.c_float, p], i32),
+            "lbh_moe_forward_batch_residual": ([p, p, p, p, sz, sz, p, p], i32),
             "lbh_moe_reserve_batch": ([p, sz, sz, E], i32),
             "lbh_matrix_prepare_gemm": ([p, p, E], i32),
             "lbh_gemm_workspace_bytes": ([sz, sz], sz),
@@ -349,6 +351,15 @@ class HipBackend:
         if st:
             raise KernelError(LbhError(status=st))
 
+    def moe_forward_batch_residual(self, moe: "MoeLayer", ids, coefs, x, hidden) -> None:
+        """moe_forward_batch adding each token's block output to hidden [n_tokens, hidden]
+        in place (residual_add_in_place, crates/bridge-kernels-reference/src/norm.rs:83-98)."""
+        n, k = ids.shape
+        st = lib().lbh_moe_forward_batch_residual(self.ctx, moe.handle, _dev_ptr(ids), _dev_ptr(coefs), n, k,
+                                                  _dev_ptr(x), _dev_ptr(hidden))
+        if st:
+            raise KernelError(LbhError(status=st))
+
     def moe_routed_by_id_batch_into(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
         """Checked batched decode with host routing [n_tokens, top_k] (each token as
         moe_routed_by_id_into, crates/bridge-kernels-reference/src/moe.rs:64-147)."""
@@ -425,6 +436,15 @@ def moe_block_forward(be: HipBackend, moe: "MoeLayer", router: Router, x, y, top
     """Device router + top-k + MoE experts of one token (asynchronous, unchecked)."""
     st = lib().lbh_moe_block_forward(be.ctx, moe.handle, router.handle, _dev_ptr(x), top_k, mode, weight_scale,
                                      _dev_ptr(y))
+    if st:
+        raise KernelError(LbhError(status=st))
+
+
+def moe_block_forward_residual(be: HipBackend, moe: "MoeLayer", router: Router, x, hidden, top_k: int, mode: int = 0,
+                               weight_scale: float = 1.0) -> None:
+    """moe_block_forward ending with hidden += ffn_delta in place (layer.rs:464)."""
+    st = lib().lbh_moe_block_forward_residual(be.ctx, moe.handle, router.handle, _dev_ptr(x), top_k, mode,
+                                              weight_scale, _dev_ptr(hidden))
     if st:
         raise KernelError(LbhError(status=st))
 

@@ -778,6 +778,28 @@ int lbo_gemv_accumulate(const lbo_exec *ex, const lbo_matrix *m, const float *in
     return LBO_OK;
 }
 
+/* residual_add_in_place (crates/bridge-kernels-reference/src/norm.rs:83-98):
+ * lengths, then a finite destination, a finite source and every sum finite
+ * (field 0 destination, 1 source, 2 output; index = lane), all before the
+ * first write; then destination[i] += residual[i]. */
+int lbo_residual_add_in_place(float *destination, size_t dest_len, const float *residual, size_t residual_len,
+                              lbo_error *err) {
+    if (dest_len != residual_len)
+        return set_err(err, LBO_DIMENSION_MISMATCH, LBO_F32, 0, dest_len, residual_len, 0, 0);
+    for (size_t i = 0; i < dest_len; ++i)
+        if (!f32_finite(destination[i]))
+            return set_err(err, LBO_NON_FINITE_VALUE, LBO_F32, i, 0, 0, f32_bits(destination[i]), 0);
+    for (size_t i = 0; i < dest_len; ++i)
+        if (!f32_finite(residual[i]))
+            return set_err(err, LBO_NON_FINITE_VALUE, LBO_F32, i, 0, 0, f32_bits(residual[i]), 1);
+    for (size_t i = 0; i < dest_len; ++i) {
+        float v = destination[i] + residual[i];
+        if (!f32_finite(v)) return set_err(err, LBO_NON_FINITE_VALUE, LBO_F32, i, 0, 0, f32_bits(v), 2);
+    }
+    for (size_t i = 0; i < dest_len; ++i) destination[i] += residual[i];
+    return LBO_OK;
+}
+
 /* --------------------------------------------------------------- SwiGLU */
 
 /* apply_swiglu (activation.rs:170-178).  On a non-finite product the

@@ -141,6 +141,11 @@ int lbo_moe_routed_by_id(const lbo_exec *ex, const uint32_t *ids, const float *c
                          const lbo_expert *shared, const float *input, float *output, int preflight,
                          lbo_error *err);
 
+/* residual_add_in_place (crates/bridge-kernels-reference/src/norm.rs:83-98), as
+ * hy3_block_forward_token ends (layer.rs:464): destination += residual. */
+int lbo_residual_add_in_place(float *destination, size_t dest_len, const float *residual, size_t residual_len,
+                              lbo_error *err);
+
 /* route_experts_into (crates/bridge-model-hy3/src/routing.rs:25-107). */
 int lbo_route_sigmoid_bias(const float *logits, const float *bias, size_t n_experts, size_t top_k,
                            float weight_scale, uint32_t *ids, float *coefs, lbo_error *err);

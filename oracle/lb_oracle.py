@@ -85,6 +85,7 @@ def lib():
         L.lbo_moe_routed_by_id.argtypes = [C.POINTER(LboExec), p, p, C.c_size_t, C.POINTER(LboExpert),
                                            C.c_size_t, C.POINTER(LboExpert), p, p, C.c_int,
                                            C.POINTER(LboError)]
+        L.lbo_residual_add_in_place.argtypes = [p, C.c_size_t, p, C.c_size_t, C.POINTER(LboError)]
         L.lbo_route_sigmoid_bias.argtypes = [p, p, C.c_size_t, C.c_size_t, C.c_float, p, p, C.POINTER(LboError)]
         L.lbo_route_softmax_topk.argtypes = [p, C.c_size_t, C.c_size_t, p, p, C.POINTER(LboError)]
         L.lbo_router_logits_f32.argtypes = [p, C.c_size_t, C.c_size_t, p, p]
@@ -219,6 +220,15 @@ def moe_routed_by_id_status(ex: LboExec, ids, coefs, experts: list, shared: LboE
     lib().lbo_moe_routed_by_id(C.byref(ex), _ptr(ids), _ptr(coefs), ids.size, arr, len(experts), C.byref(shared),
                                _ptr(x), _ptr(out), 1 if preflight else 0, C.byref(err))
     return err
+
+
+def residual_add_in_place(destination: np.ndarray, residual) -> None:
+    """residual_add_in_place (norm.rs:83-98): destination += residual; untouched on error."""
+    assert destination.dtype == np.float32 and destination.flags.c_contiguous
+    residual = np.ascontiguousarray(residual, dtype=np.float32)
+    err = LboError()
+    _check(lib().lbo_residual_add_in_place(_ptr(destination), destination.size, _ptr(residual), residual.size,
+                                           C.byref(err)), err)
 
 
 def route_sigmoid_bias(logits, bias, top_k: int, weight_scale: float):

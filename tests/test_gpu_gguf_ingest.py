@@ -91,3 +91,32 @@ def test_failing_reader_is_reported(be):
     with pytest.raises(lbhip.KernelError) as e:
         lbhip.DeviceMatrix.streamed(be, synth.Q5_K, 16384, 4096, broken)
     assert e.value.variant == "SourceReadFailed" and e.value.actual == 7 and e.value.index == (32 << 20) // 176 * 176
+
+
+def test_split_set_ingests_from_both_shards(be, oracle, tmp_path):
+    """A two-shard set (crates/bridge-gguf-split: open_set over any member): the
+    tensors of each shard stream into HBM from their own file, read back byte for
+    byte, and their matvecs equal the oracle's gemv_into."""
+    from lbhip import gguf_split as gs
+    mats = {"blk.0.ffn_gate.weight": (synth.IQ2_S, 1536, 4096, 0), "blk.0.ffn_down.weight": (synth.IQ3_S, 4096, 1536, 0),
+            "blk.0.attn_v.weight": (synth.Q4_K, 1024, 4096, 1), "output.weight": (synth.Q5_K, 8192, 4096, 1)}
+    arrs = {n: synth.random_matrix(t, r, k, seed=len(n) + 7) for n, (t, r, k, _) in mats.items()}
+    for shard in (0, 1):
+        meta = [("split.no", gg.U16, shard), ("split.count", gg.U16, 2), ("split.tensors.count", gg.I32, len(mats))]
+        tensors = [(n, (k, r), t, arrs[n].tobytes()) for n, (t, r, k, s) in mats.items() if s == shard]
+        gg.write_gguf(tmp_path / f"model-{shard + 1:05d}-of-00002.gguf", meta, tensors, alignment=4096)
+    gset = gs.open_set(tmp_path / "model-00002-of-00002.gguf")
+    assert [gset.tensors.get(n).shard_index for n in mats] == [s for (_, _, _, s) in mats.values()]
+    got = gs.ingest_set(be, gset)
+    assert set(got) == set(mats)
+    ex = oracle.make_exec(oracle.MODE_CPU_PARALLEL_Q8K, 8, True)
+    for name, (ty, rows, k, _) in mats.items():
+        m = got[name]
+        assert np.array_equal(m.read_ggml(), arrs[name].reshape(-1)), name
+        x = synth.random_activations(k, seed=rows + 1)
+        want = oracle.gemv(ex, oracle.make_matrix(ty, rows, k, arrs[name]), x)
+        y = torch.full((rows,), float("nan"), device="cuda")
+        be.gemv_f32(m, torch.from_numpy(x).cuda(), y)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), want.view(np.uint32)), name
+        m.close()

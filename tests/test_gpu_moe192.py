@@ -152,3 +152,46 @@ def test_down_launch_beyond_64k_lds_and_the_limit(be, oracle):
     with pytest.raises(lbhip.BackendError) as e:
         be.moe_create([(g, g, d)] * 2, sh)
     assert e.value.variant == "UnsupportedShape"
+
+
+def test_block_decode_with_the_residual_add(be, oracle, layer192):
+    """hy3_block_forward_token ends with residual_add_in_place(hidden, ffn_delta)
+    (crates/bridge-kernels-reference/src/layer.rs:464): the fused form equals the
+    oracle's block output added to the hidden state by its residual add."""
+    import lbhip
+    w = synth.router_weights(192, 4096, 331)
+    r = lbhip.Router(be, w)
+    rng = np.random.default_rng(332)
+    x = rng.standard_normal(4096).astype(np.float32)
+    hidden0 = rng.standard_normal(4096).astype(np.float32) * 3
+    ids, coefs = oracle.route_softmax_topk(oracle.router_logits_f32(w, x), 8)
+    delta, err = layer192.oracle_out(oracle, ids, coefs, x)
+    assert err.status == 0
+    want = hidden0.copy()
+    oracle.residual_add_in_place(want, delta)
+    h = dev(hidden0)
+    lbhip.moe_block_forward_residual(be, layer192.moe, r, dev(x), h, 8)
+    assert _same(host(h), want)
+    r.close()
+
+
+def test_batched_decode_with_the_residual_add(be, oracle, layer192):
+    logits = synth.zipf_routes(16, 192, 8, 1.1, 341)
+    ids = np.zeros((16, 8), np.uint32)
+    coefs = np.zeros((16, 8), np.float32)
+    for t in range(16):
+        ids[t], coefs[t] = oracle.route_softmax_topk(logits[t], 8)
+    rng = np.random.default_rng(342)
+    xs = rng.standard_normal((16, 4096)).astype(np.float32)
+    hidden0 = rng.standard_normal((16, 4096)).astype(np.float32)
+    ex = oracle.make_exec(oracle.MODE_CPU_PARALLEL_Q8K, 8, True)
+    want = hidden0.copy()
+    for t in range(16):
+        delta = oracle.moe_routed_by_id(ex, ids[t], coefs[t], layer192.orc_experts, layer192.orc_shared, xs[t],
+                                        preflight=False)
+        row = want[t].copy()
+        oracle.residual_add_in_place(row, delta)
+        want[t] = row
+    h = dev(hidden0)
+    be.moe_forward_batch_residual(layer192.moe, dev(ids.astype(np.int32)), dev(coefs), dev(xs), h)
+    assert _same(host(h), want)

@@ -363,3 +363,49 @@ def test_softmax_topk_router_matches_float64_softmax(oracle):
         p /= p.sum()
         assert np.allclose(coefs, p, rtol=1e-6, atol=0)
         assert abs(float(coefs.astype(np.float64).sum()) - 1.0) < 1e-6
+
+
+def test_residual_add_restates_the_reference_tests(oracle):
+    """crates/bridge-kernels-reference/tests/norm.rs:41-46 and :76-79."""
+    v = np.array([1.0, -2.0, 3.5], np.float32)
+    oracle.residual_add_in_place(v, [2.0, 1.0, -0.5])
+    assert v.tolist() == [3.0, -1.0, 3.0]
+    r = np.array([np.finfo(np.float32).max, 1.0], np.float32)
+    before = r.copy()
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.residual_add_in_place(r, [np.finfo(np.float32).max, 2.0])
+    assert e.value.status == "NonFiniteValue" and e.value.index == 0 and e.value.field == 2
+    assert np.array_equal(r.view(np.uint32), before.view(np.uint32))
+    with pytest.raises(oracle.OracleError, match="DimensionMismatch"):
+        oracle.residual_add_in_place(np.zeros(3, np.float32), [1.0, 2.0])
+    d = np.array([1.0, np.nan], np.float32)
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.residual_add_in_place(d, [1.0, 1.0])
+    assert (e.value.index, e.value.field) == (1, 0)
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.residual_add_in_place(np.ones(2, np.float32), [1.0, np.inf])
+    assert (e.value.index, e.value.field) == (1, 1)
+
+
+def test_dequant_sum_is_sequential_in_the_oracle(oracle):
+    """dot_dequant_row (gemv.rs:322-325) is one f32 chain in element order: a row
+    decoding to ones against [2^24, 1, 1, -2^24] sums to 0 (each +1 rounds back to
+    2^24); pairwise summation would give 1 and exact summation 2."""
+    from lbhip import synth
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    blk[4:16] = synth.pack_scale_min(np.ones((1, 8), np.int64), np.zeros((1, 8), np.int64))[0]
+    blk[16:144] = 0x11
+    assert np.all(oracle.decode_row(12, blk, 256) == 1.0)
+    x = np.zeros(256, np.float32)
+    x[:4] = [2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)]
+    y = oracle.gemv(oracle.make_exec(oracle.MODE_DEQUANT_F32), oracle.make_matrix(12, 1, 256, blk), x)
+    assert y[0] == 0.0
+
+
+def test_router_logits_are_a_sequential_sum_in_the_oracle(oracle):
+    """dot_f32_row (gemv.rs:286-303): ((2^24 + 1) + 1) - 2^24 = 0 in f32."""
+    w = np.ones((2, 256), np.float32)
+    x = np.zeros(256, np.float32)
+    x[:4] = [2.0 ** 24, 1.0, 1.0, -(2.0 ** 24)]
+    assert oracle.router_logits_f32(w, x).tolist() == [0.0, 0.0]
