@@ -271,6 +271,23 @@ size_t lbh_gemm_workspace_bytes(size_t n_tokens, size_t k);
 lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, size_t n_tokens, float *y_dev,
                          void *workspace_dev, size_t workspace_len);
 
+/* Bytes of the per-GPU static scratch that lbh_gemm_q8_k_noalloc stages its
+ * activation tiles in (lbh_gemm_workspace_bytes(n_tokens, k) must not exceed
+ * it: 896 tokens at k = 4096, 512 tokens up to k = 7168). */
+#define LBH_NOALLOC_SCRATCH_BYTES (8u << 20)
+
+/* [async] lbh_gemm_q8_k without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc); no counterpart in the reference.  Same results as lbh_gemm_q8_k.
+ * It allocates nothing: the activation tiles go to a static device array of
+ * LBH_NOALLOC_SCRATCH_BYTES that each GPU holds from library load to process
+ * end.  Calls whose tiles exceed it fail with LBH_SCRATCH_TOO_SMALL (expected =
+ * bytes needed, actual = the limit).  Every call on one GPU uses that GPU's one
+ * array: calls that overlap on one GPU (other streams, other contexts) race and
+ * must be ordered by the caller. */
+lbh_status lbh_gemm_q8_k_noalloc(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, size_t n_tokens,
+                                 float *y_dev, lbh_error *err);
+
 /* ---- SwiGLU mixture-of-experts block ---------------------------------------------
  * A resident MoE layer: routed experts (SwiGluExpert, crates/bridge-kernels-reference/
  * src/activation.rs:6-60: gate/up [ffn, hidden], down [hidden, ffn]) and an optional

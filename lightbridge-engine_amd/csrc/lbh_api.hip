@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "../../include/lightbridge_hip.h"
@@ -19,7 +20,32 @@
 
 using namespace lbh;
 
+// Device scratch of the entry points that allocate nothing (lbh_gemm_q8_k_noalloc):
+// one copy per GPU, held until the process ends.  Host code never uses this
+// name as an address: each device's copy is looked up once with
+// hipGetSymbolAddress (scratch_of_device) and only that pointer is passed on.
+static __device__ __align__(256) uint8_t scratch[LBH_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+// Per-device address of `scratch`, looked up once per device with that device
+// current (lbh_ctx_create makes it current before calling this).
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[MAX_DEVICES];
+
+hipError_t scratch_of_device(int device, uint8_t **out) {
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[device] = static_cast<uint8_t *>(p);
+    }
+    *out = g_scratch_ptr[device];
+    return hipSuccess;
+}
 
 size_t block_bytes(int ty) { return (size_t)layout_of(ty).block_bytes; }
 
@@ -90,7 +116,8 @@ lbh_status lbh_ctx_create(int32_t device, void *stream, lbh_ctx **out, lbh_error
     c->tuning.max_blocks = 0;
     c->tuning.cu_count = prop.multiProcessorCount;
     c->stream = static_cast<hipStream_t>(stream);
-    hipError_t e = hipMalloc(&c->status, sizeof(DevStatus));
+    hipError_t e = scratch_of_device(device, &c->scratch);
+    if (e == hipSuccess) e = hipMalloc(&c->status, sizeof(DevStatus));
     if (e == hipSuccess) e = hipHostMalloc(&c->status_host, sizeof(DevStatus), hipHostMallocDefault);
     if (e == hipSuccess) e = launch_reset_status(c->status, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -1130,17 +1157,17 @@ size_t lbh_gemm_workspace_bytes(size_t n_tokens, size_t k) {
     return gemm_b_bytes((int)n_tokens, (int)(k / 256));
 }
 
-lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t n_tokens, float *y,
-                         void *workspace, size_t workspace_len) {
-    if (!ctx || !m || !q8 || !y || !workspace) return LBH_NULL_ARGUMENT;
-    if (!m->gemm_a) return LBH_INVALID_PARAMETER;   // lbh_matrix_prepare_gemm first
-    if (n_tokens == 0 || n_tokens > (size_t)1 << 20) return LBH_UNSUPPORTED_SHAPE;
+}  // extern "C"
+
+namespace {
+
+// The activation tiles go to `bt` (the caller's workspace or this device's
+// static scratch), then the GEMM reads them: no allocation either way.
+lbh_status gemm_q8_k_into(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t n_tokens, float *y,
+                          uint8_t *bt) {
     const int nb = (int)m->nb;
-    const size_t need = gemm_b_bytes((int)n_tokens, nb);
-    if (workspace_len < need) return LBH_SCRATCH_TOO_SMALL;
     DeviceGuard g(ctx->device);
     GemmArgs a{};
-    uint8_t *bt = static_cast<uint8_t *>(workspace);
     a.b = bt;
     a.nb = nb;
     a.n_tokens = (int32_t)n_tokens;
@@ -1150,6 +1177,32 @@ lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, s
     if (launch_prep_b(q8, (int)n_tokens, nb, bt, ctx->stream) != hipSuccess)
         return LBH_HIP_ERROR;
     return launch_kq_gemm(a, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+}
+
+}  // namespace
+
+extern "C" {
+
+lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t n_tokens, float *y,
+                         void *workspace, size_t workspace_len) {
+    if (!ctx || !m || !q8 || !y || !workspace) return LBH_NULL_ARGUMENT;
+    if (!m->gemm_a) return LBH_INVALID_PARAMETER;   // lbh_matrix_prepare_gemm first
+    if (n_tokens == 0 || n_tokens > (size_t)1 << 20) return LBH_UNSUPPORTED_SHAPE;
+    if (workspace_len < gemm_b_bytes((int)n_tokens, (int)m->nb)) return LBH_SCRATCH_TOO_SMALL;
+    return gemm_q8_k_into(ctx, m, q8, n_tokens, y, static_cast<uint8_t *>(workspace));
+}
+
+lbh_status lbh_gemm_q8_k_noalloc(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t n_tokens, float *y,
+                                 lbh_error *err) {
+    if (!ctx || !m || !q8 || !y) return fail(err, LBH_NULL_ARGUMENT);
+    if (!m->gemm_a) return fail(err, LBH_INVALID_PARAMETER, m->type);   // lbh_matrix_prepare_gemm first
+    if (!ctx->scratch) return fail(err, LBH_HIP_ERROR);
+    if (n_tokens == 0 || n_tokens > (size_t)1 << 20) return fail(err, LBH_UNSUPPORTED_SHAPE, m->type, 0, 1, n_tokens);
+    const size_t need = gemm_b_bytes((int)n_tokens, (int)m->nb);
+    if (need > LBH_NOALLOC_SCRATCH_BYTES)
+        return fail(err, LBH_SCRATCH_TOO_SMALL, LBH_Q8_K, n_tokens, need, LBH_NOALLOC_SCRATCH_BYTES);
+    const lbh_status st = gemm_q8_k_into(ctx, m, q8, n_tokens, y, ctx->scratch);
+    return st == LBH_OK ? ok(err) : fail(err, st);
 }
 
 }  // extern "C"

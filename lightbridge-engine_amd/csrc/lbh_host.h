@@ -18,6 +18,7 @@ struct lbh_ctx {
     lbh::DevStatus *status_host;   // pinned mirror
     lbh::GemvTuning tuning;
     int gemm_shape;           // K-quant GEMM staging (0: registers, two blocks ahead; 1: direct to LDS)
+    uint8_t *scratch;         // this device's copy of the library's static scratch array (lbh_api.hip)
 };
 
 struct lbh_matrix {

@@ -125,6 +125,7 @@ def lib() -> C.CDLL:
             "lbh_matrix_prepare_gemm": ([p, p, E], i32),
             "lbh_gemm_workspace_bytes": ([sz, sz], sz),
             "lbh_gemm_q8_k": ([p, p, p, sz, p, p, sz], i32),
+            "lbh_gemm_q8_k_noalloc": ([p, p, p, sz, p, E], i32),
             "lbh_moe_set_batch_tiles": ([p, i32, i32, i32, i32, i32], i32),
             "lbh_moe_set_batch_engine": ([p, i32, i32, i32], i32),
             "lbh_moe_forward_batch": ([p, p, p, p, sz, sz, p, p], i32),
@@ -312,6 +313,13 @@ class HipBackend:
                                  workspace.numel() * workspace.element_size())
         if st:
             raise KernelError(LbhError(status=st))
+
+    def gemm_q8_k_noalloc(self, m: "DeviceMatrix", q8, n_tokens: int, y) -> None:
+        """gemm_q8_k staging its activation tiles in the library's static per-GPU
+        scratch (no workspace, no allocation); calls on one GPU must not overlap."""
+        _call(lib().lbh_gemm_q8_k_noalloc, self.ctx, m.handle, _dev_ptr(q8), n_tokens, _dev_ptr(y))
+
+    NOALLOC_SCRATCH_BYTES = 8 << 20
 
     @staticmethod
     def gemm_workspace_bytes(n_tokens: int, k: int) -> int:
