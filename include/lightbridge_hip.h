@@ -305,6 +305,16 @@ lbh_status lbh_moe_destroy(lbh_moe *moe);
 /* Launch-shape knob: workgroups of the routed and shared gate/up streams
  * (1..65536 each) and output rows per down workgroup (1..256). */
 lbh_status lbh_moe_set_tiles(lbh_moe *moe, int32_t wg_routed, int32_t wg_shared, int32_t tile_d);
+/* Schedule of the asynchronous single-token forwards of a layer with a shared
+ * expert: 1 runs the shared expert's gate/up and down on a second stream of
+ * the layer beside the routed experts (and beside the router chains of
+ * lbh_moe_block_forward), forked from and joined back to the context's stream;
+ * 0 (default) runs the routed and shared experts in the same two launches on
+ * the context's stream, which measured faster on MI355X (38.7 vs 50.9 us per
+ * token at the configs[2] shapes in HIP-graph replay).  Same bits either way.
+ * The layer's second stream and shared-output buffer are per layer: forwards
+ * on one layer must be ordered (one caller stream). */
+lbh_status lbh_moe_set_streams(lbh_moe *moe, int32_t two_streams);
 
 /* [sync] moe_routed_by_id_into (crates/bridge-kernels-reference/src/moe.rs:64-147):
  * ids ascending with no duplicates, coefs finite (host arrays); output[hidden] =

@@ -727,6 +727,13 @@ struct lbh_moe {
     hipEvent_t ev[4];
     uint8_t *shared_gemm_mem; // MFMA-ready copies of a K-quant shared expert (batched calls)
     size_t gemm_off[3];       // A offsets of gate, up, down in shared_gemm_mem
+    // Single-token decode with a shared expert: its gate/up and down run on
+    // side1 beside the routed experts (fork / join events); d_shared holds its
+    // raw down rows for the routed launch's combine.
+    hipStream_t side1;
+    hipEvent_t sev[2];
+    float *d_shared;
+    int two_stream;           // 1: the async forwards use side1 (default), 0: one stream
 };
 
 namespace {
@@ -753,6 +760,10 @@ void free_moe(lbh_moe *m) {
     for (int i = 0; i < 4; ++i)
         if (m->ev[i]) (void)hipEventDestroy(m->ev[i]);
     if (m->side) (void)hipStreamDestroy(m->side);
+    for (int i = 0; i < 2; ++i)
+        if (m->sev[i]) (void)hipEventDestroy(m->sev[i]);
+    if (m->side1) (void)hipStreamDestroy(m->side1);
+    if (m->d_shared) (void)hipFree(m->d_shared);
     if (m->h) (void)hipFree(m->h);
     if (m->status) (void)hipFree(m->status);
     if (m->status_host) (void)hipHostFree(m->status_host);
@@ -785,7 +796,33 @@ MoeArgs moe_args(const lbh_moe *m, const float *x, float *y) {
     a.type_gate_r = m->type_gate_r;
     a.type_down_r = m->type_down_r;
     a.routed_shape = m->experts_host[0];
+    a.d_shared = m->d_shared;
     return a;
+}
+
+// The shared expert's gate/up and down on the layer's second stream (forked
+// from and joined back to `s`) beside the routed launches `routed` enqueues on
+// s; the routed down's combine adds d_shared last, the reference's order.
+// Captured into a graph, the fork and join become graph edges.
+hipError_t forward_two_streams(lbh_moe *m, const MoeArgs &a, hipStream_t s,
+                               hipError_t (*routed_gate_up)(const MoeArgs &, hipStream_t)) {
+    MoeArgs sh = a;
+    sh.gate_part = 2, sh.down_part = 2;
+    sh.route_dev = nullptr;            // the shared stream never reads the routing
+    sh.select_in_kernel = 0;
+    sh.skip_shared_gate_up = 0;
+    MoeArgs rt = a;
+    rt.gate_part = 1, rt.down_part = 1;
+    rt.skip_shared_gate_up = 0;
+    hipError_t e = hipEventRecord(m->sev[0], s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(m->side1, m->sev[0], 0);
+    if (e == hipSuccess) e = launch_moe_gate_up(sh, m->side1);
+    if (e == hipSuccess) e = launch_moe_down(sh, m->side1);
+    if (e == hipSuccess) e = hipEventRecord(m->sev[1], m->side1);
+    if (e == hipSuccess) e = routed_gate_up(rt, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, m->sev[1], 0);
+    if (e == hipSuccess) e = launch_moe_down(rt, s);
+    return e;
 }
 
 // Host-given routing: the routed experts' planes go into the arguments.
@@ -879,6 +916,12 @@ lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_exper
         if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
     }
     if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
+    if (e == hipSuccess && has_shared) {
+        m->two_stream = 0;   // measured slower on MI355X (see lbh_moe_set_streams)
+        e = hipMalloc(&m->d_shared, hidden * sizeof(float));
+        if (e == hipSuccess) e = hipStreamCreateWithFlags(&m->side1, hipStreamNonBlocking);
+        for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipEventCreateWithFlags(&m->sev[i], hipEventDisableTiming);
+    }
     if (e == hipSuccess) e = hipMalloc(&m->status, sizeof(MoeStatus));
     if (e == hipSuccess) e = hipHostMalloc(&m->status_host, sizeof(MoeStatus), hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -933,6 +976,13 @@ lbh_status lbh_moe_destroy(lbh_moe *m) {
     return LBH_OK;
 }
 
+lbh_status lbh_moe_set_streams(lbh_moe *m, int32_t two_streams) {
+    if (!m) return LBH_NULL_ARGUMENT;
+    if (two_streams && !m->side1) return LBH_INVALID_PARAMETER;   // no shared expert
+    m->two_stream = two_streams ? 1 : 0;
+    return LBH_OK;
+}
+
 lbh_status lbh_moe_set_tiles(lbh_moe *m, int32_t wg_routed, int32_t wg_shared, int32_t tile_d) {
     if (!m) return LBH_NULL_ARGUMENT;
     if (wg_routed < 1 || wg_routed > 65536 || wg_shared < 1 || wg_shared > 65536 || tile_d < 1 || tile_d > 256)
@@ -960,6 +1010,8 @@ lbh_status lbh_moe_forward(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const 
     a.n_launch = (int32_t)n_routed;
     set_routed_planes(a, m, ids, n_routed);
     DeviceGuard g(ctx->device);
+    if (m->has_shared && m->two_stream)
+        return forward_two_streams(m, a, ctx->stream, launch_moe_gate_up) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
     return LBH_OK;
@@ -1697,6 +1749,16 @@ static lbh_status block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const f
     a.route.n = (int32_t)top_k;
     a.n_launch = (int32_t)top_k;
     a.select_in_kernel = 1;
+    if (m->has_shared && m->two_stream) {
+        // The router chains, then the routed gate/up (selecting from the
+        // logits) and down + combine on the caller's stream; the shared
+        // expert's whole FFN beside them on the second stream.
+        hipError_t e = forward_two_streams(m, a, ctx->stream, [](const MoeArgs &rt, hipStream_t s) {
+            hipError_t e2 = launch_router_logits(rt.router, s);
+            return e2 == hipSuccess ? launch_moe_gate_up(rt, s) : e2;
+        });
+        return e == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+    }
     if (m->has_shared) {
         // Router chains beside the shared gate/up, then the routed gate/up
         // (selecting from the logits), then down + combine.

@@ -126,6 +126,13 @@ struct MoeArgs {
     // y[r] = y[r] + delta[r] (residual_add_in_place, crates/bridge-kernels-
     // reference/src/norm.rs:83-98, as hy3_block_forward_token ends, layer.rs:464).
     int32_t residual;
+    // Two-stream decode: the shared expert's FFN on a second stream beside the
+    // routed experts.  gate_part: 0 both streams in one launch, 1 routed only,
+    // 2 shared only.  down_part: 0 both and the combine, 1 routed downs and the
+    // combine adding d_shared (written by part 2) last, 2 the shared down only,
+    // its raw rows to d_shared.
+    int32_t gate_part, down_part;
+    float *d_shared;            // [hidden]
     ExpertDev routed_shape;
     const uint8_t *routed_planes[MOE_MAX_ROUTED][3];   // gate, up, down
 };

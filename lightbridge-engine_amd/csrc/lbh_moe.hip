@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
     __shared__ uint32_t s_ids[MOE_MAX_ROUTED];
     __shared__ ExpertDev s_views[MOE_MAX_ROUTED];
     if (a.status && a.status->first_bad_input != ~0ull) return;
-    const int wg_s = a.has_shared && !a.skip_shared_gate_up ? a.tiles_s : 0;
+    const int wg_s = a.has_shared && !a.skip_shared_gate_up && a.gate_part != 1 ? a.tiles_s : 0;
     if ((int)blockIdx.x < wg_s) {
         const int n = a.route_dev && !a.select_in_kernel ? a.route_dev->n : a.route.n;
         gate_up_stream<TYS, LPUS>(a, SharedSlot{a, n}, 1, a.ffn_s, blockIdx.x * MOE_WAVES, wg_s * MOE_WAVES, smem);
@@ -330,7 +330,9 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     // Wave index and route count through readfirstlane: the task choice below
     // (and every descriptor derived from it) is wave-uniform.
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = __builtin_amdgcn_readfirstlane(route_n(a));
+    const int n = a.down_part == 2 ? 0 : __builtin_amdgcn_readfirstlane(route_n(a));
+    // The shared expert's down runs here unless another launch writes it to d_shared (part 1).
+    const bool shared_here = a.has_shared && a.down_part != 1;
     const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
     const int r0 = blockIdx.x * a.tile_d;
     const int r1 = r0 + a.tile_d < a.hidden ? r0 + a.tile_d : a.hidden;
@@ -344,7 +346,7 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     // Each wave's first task (routed expert `wid`, or its part of the shared
     // expert) issues its first weight loads now: their HBM latency overlaps
     // the h quantization below.
-    const int tasks = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
+    const int tasks = n + (shared_here ? DOWN_SHARED_WAVES : 0);
     const bool first_routed = wid < n, first_shared = !first_routed && wid < tasks;
     DownStream<TYR, LPUR> d_r;
     DownStream<TYS, LPUS> d_s;
@@ -363,7 +365,7 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
         const GridIn<TYR> gin_r = grid_load<TYR>();
         const GridIn<TYS> gin_s = grid_load<TYS>();
         const int cr = (nbr + 3) / 4, cs = (nbs + 3) / 4;
-        const int chunks = n * cr + (a.has_shared ? cs : 0);
+        const int chunks = n * cr + (shared_here ? cs : 0);
         auto chunk = [&](int c, const float *&x, uint8_t *&out, int &b0, int &nbl) {
             if (c < n * cr) {
                 const int m = c / cr;
@@ -428,6 +430,11 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     }
     __syncthreads();
 
+    // The shared expert's raw down rows for the combine of another launch.
+    if (a.down_part == 2) {
+        for (int t = threadIdx.x; t < r1 - r0; t += blockDim.x) a.d_shared[r0 + t] = s_y[t];
+        return;
+    }
     // Ordered combine: output.fill(0), then dest += coef * dot per expert in
     // ascending id order, then the shared expert at 1.0 (moe.rs:141-146).
     const int last = a.has_shared ? n : n - 1;
@@ -438,7 +445,8 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
             acc = __fadd_rn(acc, __fmul_rn(route_coef(a, s), s_y[s * ystride + t]));
             if (bad < 0 && !isfinite(acc)) bad = s;
         }
-        if (a.has_shared && n <= a.stop_step) acc = __fadd_rn(acc, __fmul_rn(1.0f, s_y[n * ystride + t]));
+        if (a.has_shared && n <= a.stop_step)
+            acc = __fadd_rn(acc, __fmul_rn(1.0f, shared_here ? s_y[n * ystride + t] : a.d_shared[r0 + t]));
         a.y[r0 + t] = a.residual ? __fadd_rn(a.y[r0 + t], acc) : acc;
         // A later accumulation call rejects a non-finite destination
         // (gemv.rs:126-127): record the step after which it first appeared.
@@ -480,9 +488,10 @@ static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
     const int lds = gate_up_lds<TYR>(nb) > gate_up_lds<TYS>(nb) ? gate_up_lds<TYR>(nb) : gate_up_lds<TYS>(nb);
     // tiles_s / tiles_r: workgroups of the shared / routed streams; when the
     // shared expert already ran (block decode) the routed stream takes both.
-    const bool shared_here = a.has_shared && !a.skip_shared_gate_up;
+    const bool shared_here = a.has_shared && !a.skip_shared_gate_up && a.gate_part != 1;
+    const bool routed_here = a.n_launch > 0 && a.gate_part != 2;
     const int grid = (shared_here ? a.tiles_s : 0) +
-                     (a.n_launch > 0 ? a.tiles_r + (a.skip_shared_gate_up ? a.tiles_s : 0) : 0);
+                     (routed_here ? a.tiles_r + (a.skip_shared_gate_up ? a.tiles_s : 0) : 0);
     if (grid <= 0) return hipSuccess;
     hipLaunchKernelGGL((k_moe_gate_up<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>), dim3(grid), dim3(MOE_THREADS), lds, s,
                        a);
@@ -494,6 +503,7 @@ static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
 // every expert's h.
 template <int TYR, int TYS>
 static int down_lds(int n, int has_shared, int ffn_r, int ffn_s, int tile_d) {
+    // (has_shared: the shared expert's down runs in this launch)
     const int waves = n + (has_shared ? DOWN_SHARED_WAVES : 0);
     const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
     const int q8 = (n * (ffn_r / 256) + (has_shared ? ffn_s / 256 : 0)) * 292;
@@ -503,10 +513,11 @@ static int down_lds(int n, int has_shared, int ffn_r, int ffn_s, int tile_d) {
 
 template <int TYR, int TYS>
 static hipError_t down_typed(const MoeArgs &a, hipStream_t s) {
-    const int n = a.route_dev ? a.n_launch : a.route.n;
-    const int waves = n + (a.has_shared ? DOWN_SHARED_WAVES : 0);
+    const int n = a.down_part == 2 ? 0 : a.route_dev ? a.n_launch : a.route.n;
+    const int shared_here = a.has_shared && a.down_part != 1;
+    const int waves = n + (shared_here ? DOWN_SHARED_WAVES : 0);
     const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
-    const int lds = down_lds<TYR, TYS>(n, a.has_shared, a.ffn_r, a.ffn_s, a.tile_d);
+    const int lds = down_lds<TYR, TYS>(n, shared_here, a.ffn_r, a.ffn_s, a.tile_d);
     if (lds > MOE_MAX_LDS) return hipErrorInvalidValue;
     auto kernel = k_moe_down<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>;
     if (lds > 64 * 1024) {

@@ -57,7 +57,11 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
     if (tid == 0) *done = -1;
     __syncthreads();
 
+    // The chains are a latency floor of `hidden` dependent adds: their waves
+    // take issue priority over whatever else shares the CU (the shared
+    // expert's stream runs beside them), the chain above its producers.
     if (wid >= 1 && wid <= 3) {
+        __builtin_amdgcn_s_setprio(2);
         const float4 *wt = reinterpret_cast<const float4 *>(a.w);
         const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
         for (int c = wid - 1; c < nch; c += 3) {
@@ -87,6 +91,7 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
             if (lane == 0) lds_release(&ready[c % RT_SLOTS], c);
         }
     } else if (wid == 0) {
+        __builtin_amdgcn_s_setprio(3);
         const int l = lane < RT_EXPERTS ? lane : 0;
         float sum = 0.0f;
         for (int c = 0; c < nch; ++c) {

@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
             "lbh_moe_create": ([p, p, p, p, sz, p, p, p, C.POINTER(p), E], i32),
             "lbh_moe_destroy": ([p], i32),
             "lbh_moe_set_tiles": ([p, i32, i32, i32], i32),
+            "lbh_moe_set_streams": ([p, i32], i32),
             "lbh_moe_routed_by_id_into": ([p, p, p, p, sz, p, sz, p, sz, E], i32),
             "lbh_moe_forward": ([p, p, p, p, sz, p, p], i32),
             "lbh_debug_expf": ([p, p, p, sz, i32, p, E], i32),
@@ -496,6 +497,12 @@ class MoeLayer:
         rest on the VALU dot4 path (0: all on the VALU); resets the batch launch shapes
         to their defaults."""
         st = lib().lbh_moe_set_batch_engine(self.handle, mx_min_tokens, mx_rows_gate_up, mx_rows_down)
+        if st:
+            raise KernelError(LbhError(status=st))
+
+    def set_streams(self, two_streams: bool) -> None:
+        """Shared expert on a second stream beside the routed experts (default) or all on one."""
+        st = lib().lbh_moe_set_streams(self.handle, 1 if two_streams else 0)
         if st:
             raise KernelError(LbhError(status=st))
 

@@ -195,3 +195,44 @@ def test_batched_decode_with_the_residual_add(be, oracle, layer192):
     h = dev(hidden0)
     be.moe_forward_batch_residual(layer192.moe, dev(ids.astype(np.int32)), dev(coefs), dev(xs), h)
     assert _same(host(h), want)
+
+
+def test_two_stream_schedule_gives_the_same_bits(be, oracle, layer192):
+    """The shared expert on the layer's second stream (lbh_moe_set_streams(1)):
+    host-routed and device-routed forwards equal the oracle, also under graph capture."""
+    import lbhip
+    w = synth.router_weights(192, 4096, 351)
+    r = lbhip.Router(be, w)
+    rng = np.random.default_rng(352)
+    xs = rng.standard_normal((3, 4096)).astype(np.float32)
+    wants = []
+    for t in range(3):
+        ids, coefs = oracle.route_softmax_topk(oracle.router_logits_f32(w, xs[t]), 8)
+        want, _ = layer192.oracle_out(oracle, ids, coefs, xs[t])
+        wants.append((ids, coefs, want))
+    layer192.moe.set_streams(True)
+    try:
+        xd = dev(xs)
+        y = torch.zeros((3, 4096), device="cuda")
+        for t, (ids, coefs, want) in enumerate(wants):
+            be.moe_forward(layer192.moe, ids, coefs, xd[t], y[t])
+            assert _same(host(y[t]), want)
+        s = torch.cuda.Stream()
+        be.set_stream(s)
+        y2 = torch.zeros((3, 4096), device="cuda")
+        with torch.cuda.stream(s):
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for t in range(3):
+                    lbhip.moe_block_forward(be, layer192.moe, r, xd[t], y2[t], 8)
+            for rep in range(3):
+                y2.zero_()
+                g.replay()
+                s.synchronize()
+                got = y2.cpu().numpy()
+                assert all(_same(got[t], wants[t][2]) for t in range(3)), f"replay {rep}"
+    finally:
+        be.set_stream(torch.cuda.current_stream())
+        layer192.moe.set_streams(False)
+        r.close()
