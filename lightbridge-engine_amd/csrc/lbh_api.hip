@@ -685,6 +685,29 @@ lbh_status lbh_gemv_dequant_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *
                : LBH_HIP_ERROR;
 }
 
+lbh_status lbh_debug_empty_kernel(lbh_ctx *ctx) {
+    if (!ctx) return LBH_NULL_ARGUMENT;
+    DeviceGuard g(ctx->device);
+    return launch_empty(ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+}
+
+int32_t lbh_debug_read_grid(const lbh_matrix *m, const lbh_ctx *ctx) {
+    if (!m || !ctx) return 0;
+    const long long per_wg = 256LL * 16 * 4;   // four 16-byte loads per lane per step
+    long long grid = ((long long)m->bytes + per_wg - 1) / per_wg;
+    const long long cap = 8LL * ctx->cu_count;
+    return (int32_t)(grid < 1 ? 1 : grid > cap ? cap : grid);
+}
+
+lbh_status lbh_debug_read_matrix(lbh_ctx *ctx, const lbh_matrix *m, uint32_t *sink) {
+    if (!ctx || !m || !sink) return LBH_NULL_ARGUMENT;
+    DeviceGuard g(ctx->device);
+    return launch_stream_read(m->planes, (long long)m->bytes, sink, lbh_debug_read_grid(m, ctx), ctx->stream) ==
+                   hipSuccess
+               ? LBH_OK
+               : LBH_HIP_ERROR;
+}
+
 lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in, float *out, size_t n, lbh_error *err) {
     if (!ctx || !in || !out) return fail(err, LBH_NULL_ARGUMENT);
     DeviceGuard g(ctx->device);

@@ -143,10 +143,9 @@ __device__ __forceinline__ void decode(const WSlice<T_IQ3_S, LPU> &w, const void
             const int sh = 16 * (lg & 1);
             const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
             const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
-            const uint32_t s = byte_of(w.sg[g], lg);
-            const uint2 g1 = grid[i1], g2 = grid[i2];
-            o.w[8 * g + 2 * lg] = apply_signs(g1.x, g1.y, s & 15u);
-            o.w[8 * g + 2 * lg + 1] = apply_signs(g2.x, g2.y, s >> 4);
+            const uint2 g1 = grid[i1], g2 = grid[i2], sm = grid[512 + byte_of(w.sg[g], lg)];
+            o.w[8 * g + 2 * lg] = perm(g1.y, g1.x, sm.x);
+            o.w[8 * g + 2 * lg + 1] = perm(g2.y, g2.x, sm.y);
         }
         o.s[2 * g] = sc;
         o.s[2 * g + 1] = sc;

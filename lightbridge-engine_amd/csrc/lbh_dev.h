@@ -49,11 +49,6 @@ __device__ __forceinline__ uint32_t sign_sel(uint32_t nib) {
     return ((nib * 0x810204u) & 0x04040404u) | 0x03020100u;
 }
 
-// Signed grid dword from a (magnitude, negated magnitude) pair.
-__device__ __forceinline__ uint32_t apply_signs(uint32_t pos, uint32_t neg, uint32_t nib) {
-    return perm(neg, pos, sign_sel(nib));
-}
-
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -312,8 +307,10 @@ static __constant__ uint32_t c_iq3s_grid[512] = {LBH_IQ3S_GRID_VALUES};
 
 template <int TY>
 struct GridLDS {
-    // IQ2S: the 1024 code entries, then 256 sign-byte entries (sign_lut_entry).
-    static constexpr int BYTES = TY == T_IQ2_S ? (1024 + 256) * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
+    // IQ2S: the 1024 code entries, then 256 sign-byte entries (sign_lut_entry);
+    // IQ3S: the 512 (magnitude, negation) entries, then 256 sign-byte entries
+    // (iq3_sign_entry).
+    static constexpr int BYTES = TY == T_IQ2_S ? (1024 + 256) * 8 : TY == T_IQ3_S ? (512 + 256) * 8 : 0;
 };
 
 // Sign-byte table appended to the IQ2S codes: entry s = the v_perm selector
@@ -323,6 +320,12 @@ struct GridLDS {
 __device__ __forceinline__ uint2 sign_lut_entry(uint32_t s) {
     return make_uint2(((s & 15u) * 0x810204u) & 0x04040404u, ((s >> 4) * 0x810204u) & 0x04040404u);
 }
+
+// Sign-byte table appended to the IQ3S entries: entry s = the full v_perm
+// selectors applying the low and the high nibble of s to a (magnitude,
+// negation) pair, so each group of four signs costs one LDS read instead of
+// the selector arithmetic.
+__device__ __forceinline__ uint2 iq3_sign_entry(uint32_t s) { return make_uint2(sign_sel(s & 15u), sign_sel(s >> 4)); }
 
 // Fills the grid for TY into `lds` (cooperatively, all threads of the block);
 // the caller synchronises afterwards.  grid_load / grid_store split it so the
@@ -378,6 +381,7 @@ __device__ __forceinline__ void grid_store(const GridIn<TY> &g, void *lds) {
             const uint32_t v = (uint32_t)g.e[k];
             out[threadIdx.x + 256 * k] = make_uint2(v, neg_bytes(v));
         }
+        out[512 + threadIdx.x] = iq3_sign_entry(threadIdx.x);
     }
 }
 
@@ -402,6 +406,7 @@ __device__ __forceinline__ void fill_grid(void *lds) {
             const uint32_t v = c_iq3s_grid[i];
             g[i] = make_uint2(v, neg_bytes(v));
         }
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) g[512 + i] = iq3_sign_entry(i);
     }
 }
 
@@ -571,10 +576,9 @@ __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, cons
             const int sh = 16 * (lg & 1);
             const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
             const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
-            const uint32_t s = byte_of(w.sg[g], lg);
-            const uint2 g1 = grid[i1], g2 = grid[i2];
-            gs = dot4(apply_signs(g1.x, g1.y, s & 15u), a.q[8 * g + 2 * lg], gs);
-            gs = dot4(apply_signs(g2.x, g2.y, s >> 4), a.q[8 * g + 2 * lg + 1], gs);
+            const uint2 g1 = grid[i1], g2 = grid[i2], sm = grid[512 + byte_of(w.sg[g], lg)];
+            gs = dot4(perm(g1.y, g1.x, sm.x), a.q[8 * g + 2 * lg], gs);
+            gs = dot4(perm(g2.y, g2.x, sm.y), a.q[8 * g + 2 * lg + 1], gs);
         }
         bsum += mul24(gs, (int32_t)(2 * ps + 1));
     }

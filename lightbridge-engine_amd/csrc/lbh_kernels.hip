@@ -111,6 +111,41 @@ __global__ void k_f16_to_f32(const uint16_t *in, float *out, long long n) {
         out[i] = f16_to_f32(in[i]);
 }
 
+// ------------------------------------------------------- floor measurement
+
+// Reference points for the matvecs' roofline: an empty kernel (the launch
+// floor) and a plain read of a byte range with one 16-byte load per lane per
+// step (the memory floor of reading a matrix's planes); the loaded words are
+// XOR-folded and one word per wave is stored so no load can be dropped.
+__global__ void k_empty() {}
+
+__global__ void __launch_bounds__(256) k_stream_read(const uint4 *__restrict__ src, long long n16, uint32_t *sink) {
+    uint32_t acc = 0;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n16; i += 4 * stride) {
+        const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    }
+    for (; i < n16; i += stride) {
+        const uint4 a = src[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    for (int off = 32; off >= 1; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63) == 0) sink[(blockIdx.x * blockDim.x + threadIdx.x) >> 6] = acc;
+}
+
+hipError_t launch_empty(hipStream_t s) {
+    hipLaunchKernelGGL(k_empty, dim3(1), dim3(64), 0, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_read(const void *src, long long bytes, uint32_t *sink, int grid, hipStream_t s) {
+    if (bytes < 16 || grid < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_stream_read, dim3(grid), dim3(256), 0, s, static_cast<const uint4 *>(src), bytes / 16, sink);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- launchers
 
 static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }

@@ -73,10 +73,36 @@ __device__ __forceinline__ float route_coef(const MoeArgs &a, int s) {
     return a.route_dev ? a.route_dev->coefs[s] : a.route.coefs[s];
 }
 
+// Rows whose gate and up dots a wave has finished, waiting for SwiGLU: the
+// exponential runs once per 64 rows with every lane busy instead of once per
+// row step in the step's few leader lanes.
+constexpr int SWIGLU_BATCH = 64;
+struct PendingRows {
+    float g[SWIGLU_BATCH], u[SWIGLU_BATCH];
+    int32_t row[SWIGLU_BATCH];
+    int32_t tag[SWIGLU_BATCH];   // scratch slot | (expert order << 8)
+};
+
 // LDS bytes of one gate/up workgroup of type TY.
 template <int TY>
 __host__ __device__ constexpr int gate_up_lds(int nb) {
-    return align16(GridLDS<TY>::BYTES) + align16(nb * 292) + MOE_WAVES * (int)sizeof(FoldLDS<TY>);
+    return align16(GridLDS<TY>::BYTES) + align16(nb * 292) + MOE_WAVES * (int)sizeof(FoldLDS<TY>) +
+           MOE_WAVES * (int)sizeof(PendingRows);
+}
+
+// h = SwiGLU(gate, up) (activation.rs:170-178) of a wave's n pending rows, one
+// lane per row; a non-finite h is recorded (first by expert order, then lane).
+__device__ __forceinline__ void flush_swiglu(const MoeArgs &a, PendingRows &pr, int n) {
+    wave_sync();
+    const int lane = threadIdx.x & 63;
+    if (lane < n && pr.row[lane] >= 0) {
+        const int tag = pr.tag[lane], r = pr.row[lane];
+        const float hv = swiglu_ref(pr.g[lane], pr.u[lane]);
+        a.h[(long long)(tag & 0xff) * a.h_stride + r] = hv;
+        if (a.check && !isfinite(hv))
+            atomicMin(&a.status->first_bad_swiglu, ((unsigned long long)(tag >> 8) << 32) | (unsigned)r);
+    }
+    wave_sync();
 }
 
 // Gate and up rows of `count` experts of one type, SwiGLU into h.  The
@@ -92,15 +118,22 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
     uint8_t *s_grid = smem;
     uint8_t *s_q8 = smem + align16(GridLDS<TY>::BYTES);
     FoldLDS<TY> *s_fold = reinterpret_cast<FoldLDS<TY> *>(s_q8 + align16(NB * 292));
+    PendingRows &pend = reinterpret_cast<PendingRows *>(s_fold + MOE_WAVES)[wid];
 
     const LaneMap<LPU> L(lane, NB);
     const int per = (rows + L.rpw - 1) / L.rpw;
     const int items = count * per;
     using W = WOf<TY, LPU>;
-    // item -> (slot index, expert views, row)
-    auto issue = [&](int it, W &wg, W &wu) {
+    // Items walk with a stride of nwaves: (m, j) = (it / per, it % per) is
+    // advanced by adding the stride's quotient and remainder (no division per item).
+    const int dq = nwaves / per, dr = nwaves - dq * per;
+    auto advance = [&](int &m, int &j) {
+        m += dq, j += dr;
+        if (j >= per) j -= per, m += 1;
+    };
+    // item (m, j) -> (slot index, expert views, row)
+    auto issue = [&](int it, int m, int j, W &wg, W &wu) {
         if (it >= items) return;
-        const int m = it / per, j = it - m * per;
         const int r = j * L.rpw + L.slot;
         if (!(L.lane_on && r < rows)) return;
         const MatView VG = uniform_view(slot_of(m).gate), VU = uniform_view(slot_of(m).up);
@@ -117,6 +150,7 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
     // range) so the wait before the prologue's stores counts exactly the
     // weight loads issued after it.
     int it = first_wave + wid;
+    int im = it / per, ij = it - im * per;   // the wave's current item as (m, j)
     const GridIn<TY> gin = grid_load<TY>();
     const QuantIn qin = quantize_load(a.x, 4 * wid, NB);
     W ga, ua, gb, ub;
@@ -141,29 +175,37 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
     ActOf<TY, LPU> act;
     load_act(s_q8 + L.b * 292, L.part, act);
 
-    auto process = [&](int it, const W &wg, const W &wu) {
-        const int m = it / per, j = it - m * per;
+    int npend = 0;   // wave-uniform count of pending rows
+    auto process = [&](int m, int j, const W &wg, const W &wu) {
         const int r = j * L.rpw + L.slot;
         const bool on = L.lane_on && r < rows;
         const float gv = row_dot<TY, LPU>(wg, act, on, L, s_grid, s_fold[wid], nullptr, 0);
         const float uv = row_dot<TY, LPU>(wu, act, on, L, s_grid, s_fold[wid], nullptr, 0);
-        if (on && L.leader()) {
-            const int slot = slot_of.slot(m), order = slot_of.order(m);
-            const float hv = swiglu_ref(gv, uv);
-            a.h[(long long)slot * a.h_stride + r] = hv;
-            if (a.check && !isfinite(hv))
-                atomicMin(&a.status->first_bad_swiglu, ((unsigned long long)order << 32) | (unsigned)r);
+        if (npend + L.rpw > SWIGLU_BATCH) {
+            flush_swiglu(a, pend, npend);
+            npend = 0;
         }
+        if (L.lane_on && L.leader()) {
+            const int k = npend + L.slot;
+            pend.g[k] = gv, pend.u[k] = uv;
+            pend.row[k] = on ? r : -1;   // -1: a row past the matrix, nothing to store
+            pend.tag[k] = slot_of.slot(m) | (slot_of.order(m) << 8);
+        }
+        npend += L.rpw;
     };
     while (it < items) {
-        issue(it + nwaves, gb, ub);
-        process(it, ga, ua);
-        it += nwaves;
+        int m2 = im, j2 = ij;
+        advance(m2, j2);
+        issue(it + nwaves, m2, j2, gb, ub);
+        process(im, ij, ga, ua);
+        it += nwaves, im = m2, ij = j2;
         if (it >= items) break;
-        issue(it + nwaves, ga, ua);
-        process(it, gb, ub);
-        it += nwaves;
+        advance(m2, j2);
+        issue(it + nwaves, m2, j2, ga, ua);
+        process(im, ij, gb, ub);
+        it += nwaves, im = m2, ij = j2;
     }
+    if (npend > 0) flush_swiglu(a, pend, npend);
 }
 
 // Routed experts of one launch: their gate/up views staged in LDS by the
@@ -343,24 +385,19 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     float *s_y = reinterpret_cast<float *>(s_foldp + nw * down_fold_bytes<TYR, TYS>());
     uint8_t *s_q8 = reinterpret_cast<uint8_t *>(s_y + (MOE_MAX_ROUTED + 1) * a.tile_d);   // [n * nbr + nbs] blocks
 
-    // Each wave's first task (routed expert `wid`, or its part of the shared
-    // expert) issues its first weight loads now: their HBM latency overlaps
-    // the h quantization below.
+    // Q8_K of every expert's h into LDS (quantize_row_q8_k_into of the down
+    // projection's input, gemv.rs:161-163): chunks of up to four blocks of one
+    // slot.  Load order: the codebooks and the h of the wave's first two
+    // chunks, then the first weight step of the wave's first task (routed
+    // expert `wid`, or its part of the shared expert), then the LDS stores.
+    // Vector loads retire in order, so the quantization waits only for the
+    // small h and codebook loads, and the weights' HBM round trip overlaps it.
+    // The second chunk's index is clamped (an in-range reload) so the loads
+    // are unconditional.
     const int tasks = n + (shared_here ? DOWN_SHARED_WAVES : 0);
     const bool first_routed = wid < n, first_shared = !first_routed && wid < tasks;
     DownStream<TYR, LPUR> d_r;
     DownStream<TYS, LPUS> d_s;
-    if (first_routed)
-        d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
-    else if (first_shared)
-        d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
-
-    // Q8_K of every expert's h into LDS (quantize_row_q8_k_into of the down
-    // projection's input, gemv.rs:161-163): chunks of up to four blocks of one
-    // slot.  Each wave loads the h of two chunks (and the codebook loads go
-    // out first) before quantizing either, so the prologue waits for one
-    // round trip instead of one per chunk; the second chunk's index is
-    // clamped (an in-range reload) so the loads are unconditional.
     {
         const GridIn<TYR> gin_r = grid_load<TYR>();
         const GridIn<TYS> gin_s = grid_load<TYS>();
@@ -381,24 +418,32 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
             }
         };
         bool first = true;
-        for (int c = wid; c < chunks; c += 2 * nw) {
+        for (int c = wid; chunks > 0 && (c < chunks || first); c += 2 * nw) {
+            const int cc = c < chunks ? c : chunks - 1, c1 = c + nw;
             const float *x0, *x1;
             uint8_t *o0, *o1;
             int b0, b1, n0, n1;
-            const int c1 = c + nw;
-            chunk(c, x0, o0, b0, n0);
-            chunk(c1 < chunks ? c1 : c, x1, o1, b1, n1);
+            chunk(cc, x0, o0, b0, n0);
+            chunk(c1 < chunks ? c1 : cc, x1, o1, b1, n1);
             const QuantIn q0 = quantize_load(x0, b0, n0);
             const QuantIn q1 = quantize_load(x1, b1, n1);
             if (first) {
+                if (first_routed)
+                    d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
+                else if (first_shared)
+                    d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
                 grid_store<TYR>(gin_r, s_grid_r);
                 if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
                 first = false;
             }
-            quantize_store(q0, o0);
+            if (c < chunks) quantize_store(q0, o0);
             if (c1 < chunks) quantize_store(q1, o1);
         }
-        if (first) {   // a wave without chunks still stores its share of the codebooks
+        if (first) {   // no h to quantize (never at the supported shapes)
+            if (first_routed)
+                d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
+            else if (first_shared)
+                d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
             grid_store<TYR>(gin_r, s_grid_r);
             if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
         }

@@ -64,62 +64,126 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
         __builtin_amdgcn_s_setprio(2);
         const float4 *wt = reinterpret_cast<const float4 *>(a.w);
         const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-        for (int c = wid - 1; c < nch; c += 3) {
+        constexpr int PER = RT_STEPS * RT_EXPERTS / 64;
+        struct ChunkRegs {
+            float4 v[PER], xv[PER];
+        };
+        auto load = [&](int c, ChunkRegs &r) {
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int idx = lane + 64 * k;
+                const int step = idx / RT_EXPERTS, e = e0 + idx % RT_EXPERTS;
+                r.v[k] = e < n ? wt[(long long)(c * RT_STEPS + step) * n + e] : make_float4(0.f, 0.f, 0.f, 0.f);
+                r.xv[k] = x4[c * RT_STEPS + step];
+            }
+        };
+        // Chunk c waits for its ring slot, then its products go to LDS.  The
+        // wave's next chunk is loaded before that wait, so two chunks per
+        // producer are in flight (the loads' latency, not the adds, set the
+        // pace with one).  false: the wait gave up.
+        auto publish = [&](int c, const ChunkRegs &r) {
             for (long long k = 0; k < SPIN && lds_acquire(done) < c - RT_SLOTS; ++k) __builtin_amdgcn_s_sleep(1);
             if (force || lds_acquire(done) < c - RT_SLOTS) {
                 gave_up();
-                break;
-            }
-            float4 v[RT_STEPS * RT_EXPERTS / 64], xv[RT_STEPS * RT_EXPERTS / 64];
-#pragma unroll
-            for (int k = 0; k < RT_STEPS * RT_EXPERTS / 64; ++k) {
-                const int idx = lane + 64 * k;
-                const int step = idx / RT_EXPERTS, e = e0 + idx % RT_EXPERTS;
-                v[k] = e < n ? wt[(long long)(c * RT_STEPS + step) * n + e] : make_float4(0.f, 0.f, 0.f, 0.f);
-                xv[k] = x4[c * RT_STEPS + step];
+                return false;
             }
             // The ring holds the products w[i] * x[i] (each rounded once, as the
             // reference's `weight * input_value`), so the chain only adds.
             float4 *slot = ring + (c % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
 #pragma unroll
-            for (int k = 0; k < RT_STEPS * RT_EXPERTS / 64; ++k) {
+            for (int k = 0; k < PER; ++k) {
                 float4 p;
-                p.x = __fmul_rn(v[k].x, xv[k].x), p.y = __fmul_rn(v[k].y, xv[k].y);
-                p.z = __fmul_rn(v[k].z, xv[k].z), p.w = __fmul_rn(v[k].w, xv[k].w);
+                p.x = __fmul_rn(r.v[k].x, r.xv[k].x), p.y = __fmul_rn(r.v[k].y, r.xv[k].y);
+                p.z = __fmul_rn(r.v[k].z, r.xv[k].z), p.w = __fmul_rn(r.v[k].w, r.xv[k].w);
                 slot[lane + 64 * k] = p;
             }
             if (lane == 0) lds_release(&ready[c % RT_SLOTS], c);
+            return true;
+        };
+        ChunkRegs ra, rb;
+        int c = wid - 1;
+        if (c < nch) load(c, ra);
+        while (c < nch) {
+            if (c + 3 < nch) load(c + 3, rb);
+            if (!publish(c, ra)) break;
+            c += 3;
+            if (c >= nch) break;
+            if (c + 3 < nch) load(c + 3, ra);
+            if (!publish(c, rb)) break;
+            c += 3;
         }
     } else if (wid == 0) {
         __builtin_amdgcn_s_setprio(3);
         const int l = lane < RT_EXPERTS ? lane : 0;
         float sum = 0.0f;
-        for (int c = 0; c < nch; ++c) {
+        // Chunk c's slot holds it once ready[c % RT_SLOTS] == c.  false: the wait gave up.
+        auto wait_ready = [&](int c) {
             for (long long k = 0; k < SPIN && lds_acquire(&ready[c % RT_SLOTS]) != c; ++k) __builtin_amdgcn_s_sleep(1);
             if (force || lds_acquire(&ready[c % RT_SLOTS]) != c) {
                 gave_up();
-                sum = __int_as_float(0x7fc00000);
                 if (lane == 0) lds_release(done, 0x7fffffff);
-                break;
+                return false;
             }
-            const float4 *slot = ring + (c % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
-            // Rolling eight-step read-ahead over the fully unrolled chunk: every
-            // index is a compile-time constant, so reads stay in registers.
-            constexpr int P = 8;
-            float4 buf[P];
+            return true;
+        };
+        // The chain reads the ring in batches of B steps, double-buffered: the
+        // reads of batch g + 1 are issued before the adds of batch g, and one
+        // explicit wait for all but the newest B reads (LDS reads complete in
+        // order) covers the whole batch, so the adds run back to back.  The
+        // next chunk's slot is awaited before its first batch is issued.  The
+        // empty asm statement closing each batch keeps its adds ahead of the
+        // next issue (the compiler would otherwise sink them past it, and past
+        // the wait for the next chunk).  Only the expert lanes run the chain.
+        constexpr int B = 8, NB = RT_STEPS / B;
+        float4 bufs[2][B];
+        auto issue = [&](float4 (&dst)[B], const float4 *src) {
 #pragma unroll
-            for (int k = 0; k < P; ++k) buf[k] = slot[k * RT_EXPERTS + l];
+            for (int k = 0; k < B; ++k) dst[k] = src[k * RT_EXPERTS + l];
+        };
+        auto adds = [&](const float4 (&src)[B]) {
 #pragma unroll
-            for (int j = 0; j < RT_STEPS; ++j) {
-                const float4 p = buf[j % P];
-                if (j + P < RT_STEPS) buf[j % P] = slot[(j + P) * RT_EXPERTS + l];
-                sum = __fadd_rn(sum, p.x);
-                sum = __fadd_rn(sum, p.y);
-                sum = __fadd_rn(sum, p.z);
-                sum = __fadd_rn(sum, p.w);
+            for (int k = 0; k < B; ++k) {
+                sum = __fadd_rn(sum, src[k].x);
+                sum = __fadd_rn(sum, src[k].y);
+                sum = __fadd_rn(sum, src[k].z);
+                sum = __fadd_rn(sum, src[k].w);
             }
-            if (lane == 0) lds_release(done, c);
+            asm volatile("" : "+v"(sum)::"memory");
+        };
+        // s_waitcnt lgkmcnt(B) (vmcnt and expcnt left at their maxima), fenced
+        // by scheduling barriers so that the reads just issued stay ahead of it.
+        constexpr int WAIT_NEWEST_B = 0xC07F | (B << 8);
+        auto wait_lds = [](auto cnt) {
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(decltype(cnt)::value);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        bool ok = nch > 0;
+        if (lane < RT_EXPERTS) {
+            ok = ok && wait_ready(0);
+            if (ok) issue(bufs[0], ring);
+            for (int c = 0; ok && c < nch; ++c) {
+                const float4 *cur = ring + (c % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
+                const float4 *nxt = ring + ((c + 1) % RT_SLOTS) * RT_STEPS * RT_EXPERTS;
+#pragma unroll
+                for (int b = 0; b < NB - 1; ++b) {
+                    issue(bufs[(b + 1) & 1], cur + (b + 1) * B * RT_EXPERTS);
+                    wait_lds(std::integral_constant<int, WAIT_NEWEST_B>());
+                    adds(bufs[b & 1]);
+                }
+                const bool more = c + 1 < nch;
+                if (more && !wait_ready(c + 1)) ok = false;
+                if (ok && more) {
+                    issue(bufs[0], nxt);
+                    wait_lds(std::integral_constant<int, WAIT_NEWEST_B>());
+                } else {
+                    wait_lds(std::integral_constant<int, 0xC07F>());
+                }
+                adds(bufs[(NB - 1) & 1]);
+                if (ok && lane == 0) lds_release(done, c);
+            }
         }
+        if (!ok) sum = __int_as_float(0x7fc00000);
         if (lane < RT_EXPERTS && e0 + lane < n) a.logits[e0 + lane] = sum;
     }
 }

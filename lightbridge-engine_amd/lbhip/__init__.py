@@ -107,6 +107,9 @@ def lib() -> C.CDLL:
             "lbh_gemv_dequant_accumulate_scaled_into": ([p, p, p, sz, p, sz, C.c_float, E], i32),
             "lbh_gemv_dequant_f32": ([p, p, p, p, C.c_float, i32], i32),
             "lbh_debug_f16_to_f32": ([p, p, p, sz, E], i32),
+            "lbh_debug_empty_kernel": ([p], i32),
+            "lbh_debug_read_grid": ([p, p], i32),
+            "lbh_debug_read_matrix": ([p, p, p], i32),
             "lbh_moe_create": ([p, p, p, p, sz, p, p, p, C.POINTER(p), E], i32),
             "lbh_moe_destroy": ([p], i32),
             "lbh_moe_set_tiles": ([p, i32, i32, i32], i32),
@@ -330,6 +333,18 @@ class HipBackend:
         st = lib().lbh_gemv_block_sums(self.ctx, m.handle, _dev_ptr(q8), _dev_ptr(out))
         if st:
             raise KernelError(LbhError(status=st))
+
+    def empty_kernel(self) -> None:
+        """One empty kernel launch (the launch floor of a matvec)."""
+        lib().lbh_debug_empty_kernel(self.ctx)
+
+    def read_matrix(self, m: "DeviceMatrix", sink) -> None:
+        """A plain 16-byte-per-lane read of the matrix's device bytes (its matvec's memory floor);
+        sink: int32 device tensor of read_sink_words(m) words."""
+        lib().lbh_debug_read_matrix(self.ctx, m.handle, _dev_ptr(sink))
+
+    def read_sink_words(self, m: "DeviceMatrix") -> int:
+        return 4 * lib().lbh_debug_read_grid(m.handle, self.ctx)
 
     def f16_to_f32(self, src, dst) -> None:
         _call(lib().lbh_debug_f16_to_f32, self.ctx, _dev_ptr(src), _dev_ptr(dst), src.numel())
