@@ -226,6 +226,43 @@ def cpu_moe(experts_np, shared_np, router_w, xs, seconds):
                       f"{threads} threads; value is the faster (single-pass) variant"}
 
 
+def empty_kernel_us(be, timer):
+    """Launch floor: one empty kernel per graph node, averaged over 400 nodes."""
+    g = timer.graph(lambda: [be.empty_kernel() for _ in range(400)])
+    timer.time(g, 2)
+    return timer.time(g, 20) / (20 * 400) * 1e6
+
+
+def read_floor_us(be, timer, torch, mats, nbytes):
+    """Memory floor of a matvec: the fastest plain read of its weight bytes (16-byte non-temporal
+    loads, every lane's loads issued before any is used) over a sweep of launch shapes, each
+    timed in the same rotation of weight copies as the matvec.  Returns (us, shape)."""
+    cus = be.cu_count()
+    sink = torch.zeros(4 * be.READ_MAX_GRID, dtype=torch.int32, device="cuda")
+    best = (float("inf"), None)
+    copies = len(mats)
+    reps = max(2, min(100, int(0.05 / (copies * nbytes / 5e12))))
+    for unroll in (1, 4, 8):
+        fit = max(1, min(be.READ_MAX_GRID, math.ceil(nbytes / (4096 * unroll))))
+        for grid in sorted({fit, cus, 2 * cus, 4 * cus, 8 * cus}):
+            if grid > fit:
+                continue
+            for slab in (False, True):
+                g = timer.graph(lambda: [be.read_matrix(m, sink, grid, unroll, slab) for m in mats])
+                timer.time(g, 1)
+                us = timer.time(g, reps) / (reps * copies) * 1e6
+                if us < best[0]:
+                    best = (us, {"grid": grid, "loads_per_lane_in_flight": unroll, "slab": slab})
+                del g
+    return best
+
+
+def floor_fields(kernel_us, empty_us, read):
+    """Floors beside a kernel time: frac_of_floor = best plain read / kernel time."""
+    return {"empty_kernel_us": round(empty_us, 3), "read_floor_us": round(read[0], 3),
+            "read_floor_shape": read[1], "frac_of_floor": round(read[0] / kernel_us, 4)}
+
+
 def bench_matvec_step(args, be, timer, torch, np, synth):
     w_gate = synth.random_matrix(synth.IQ2_S, FFN, HIDDEN, seed=101)
     w_down = synth.random_matrix(synth.IQ3_S, HIDDEN, FFN, seed=102)
@@ -258,6 +295,10 @@ def bench_matvec_step(args, be, timer, torch, np, synth):
     n_k = max(1, 2000 // copies)
     gate_us = timer.time(g_gate, n_k) / (n_k * copies) * 1e6
     down_us = timer.time(g_down, n_k) / (n_k * copies) * 1e6
+    del g, g_gate, g_down
+    empty_us = empty_kernel_us(be, timer)
+    gate_floor = read_floor_us(be, timer, torch, gates, w_gate.nbytes)
+    down_floor = read_floor_us(be, timer, torch, downs, w_down.nbytes)
 
     c = (steps - 1) % copies
     torch.cuda.synchronize()
@@ -265,7 +306,8 @@ def bench_matvec_step(args, be, timer, torch, np, synth):
     for m in gates + downs:
         m.close()
     return dict(w_gate=w_gate, w_down=w_down, copies=copies, steps=steps, warmup=reps_w * copies,
-                ms_per_step=ms_per_step, gate_us=gate_us, down_us=down_us, check=check)
+                ms_per_step=ms_per_step, gate_us=gate_us, down_us=down_us, check=check, empty_us=empty_us,
+                gate_floor=gate_floor, down_floor=down_floor)
 
 
 def bench_q4k(args, be, timer, torch, np, synth):
@@ -280,11 +322,13 @@ def bench_q4k(args, be, timer, torch, np, synth):
     timer.time(g, 3)
     reps = max(3, 1000 // copies)
     us = timer.time(g, reps) / (reps * copies) * 1e6
+    del g
+    floors = floor_fields(us, empty_kernel_us(be, timer), read_floor_us(be, timer, torch, ms, w.nbytes))
     for m in ms:
         m.close()
     return w, {"workload": "configs[0]: Q4_K x Q8_K matvec 4096x4096, batch 1 (fused Q8_K + matvec kernel)",
                "us_per_matvec": round(us, 3), "GB/s": round(Q4K_BYTES / us / 1e3, 2),
-               "roofline_frac": round(Q4K_BYTES / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies}
+               "roofline_frac": round(Q4K_BYTES / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies, **floors}
 
 
 # Decode matvecs of the Hy3 model's own tensors (crates/bridge-model-hy3/src/schema.rs:96-201,
@@ -298,6 +342,7 @@ MODEL_SHAPES = [("attn_q IQ2_S 8192x4096", 22, 8192, 4096), ("attn_k IQ2_S 1024x
 def bench_model_shapes(args, be, timer, torch, np, synth):
     """One fused Q8_K + matvec launch per shape, > 600 MB of weight copies in rotation."""
     out = {}
+    empty_us = empty_kernel_us(be, timer)
     for name, ty, rows, k in MODEL_SHAPES:
         w = synth.random_matrix(ty, rows, k, seed=rows + k)
         copies = max(2, math.ceil(600e6 / w.nbytes))
@@ -310,12 +355,14 @@ def bench_model_shapes(args, be, timer, torch, np, synth):
         reps = max(3, min(400, int(0.25 / (copies * w.nbytes / 5e12))))
         timer.time(g, 2)
         us = timer.time(g, reps) / (reps * copies) * 1e6
+        del g
         alg = w.nbytes + Q8(k) + 4 * rows
         out[name] = {"us": round(us, 3), "algorithmic_bytes": alg, "GB/s": round(alg / us / 1e3, 1),
-                     "roofline_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies}
+                     "roofline_frac": round(alg / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies,
+                     **floor_fields(us, empty_us, read_floor_us(be, timer, torch, ms, w.nbytes))}
         for m in ms:
             m.close()
-        del ms, xs, ys, g
+        del ms, xs, ys
         torch.cuda.empty_cache()
     return out
 
@@ -576,6 +623,7 @@ PF_TOKENS, PF_ROWS = 512, 12288
 PF_OPS = 2 * PF_TOKENS * PF_ROWS * HIDDEN                                 # 51,539,607,552
 PF_BYTES = PF_ROWS * 16 * 176 + PF_TOKENS * Q8(HIDDEN) + PF_TOKENS * PF_ROWS * 4   # 62,160,896
 MFMA_F16_PEAK_TFLOPS = 2500.0   # MI355X dense f16 matrix-core peak (the GEMM's instruction)
+MFMA_I8_PEAK_TOPS = 5000.0      # MI355X dense int8 matrix-core peak (the roofline the i8 path is priced on)
 
 
 def bench_prefill(args, be, timer, torch, np, synth):
@@ -604,8 +652,12 @@ def bench_prefill(args, be, timer, torch, np, synth):
                        "[512 x 12288], f16 MFMA (v_mfma_f32_32x32x16_f16) on integer operands: exact "
                        "per-(block, lane residue) sums",
            "us_per_step": round(us, 2), "dot_TOPS": round(tops, 2),
-           "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TOP/s",
-                        "frac": round(tops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": MEASURED_TRAFFIC["prefill"]},
+           "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
+                        "frac": round(tops / MFMA_I8_PEAK_TOPS, 4), "traffic": MEASURED_TRAFFIC["prefill"],
+                        "peak_note": "priced on the dense int8 peak (5.0 POP/s) of the integer contraction; the "
+                                     "kernel issues f16 MFMA on exact small-integer operands (measured faster than "
+                                     "the i8 instruction at this shape), whose own peak is 2.5 PFLOP/s",
+                        "frac_of_f16_instruction_peak": round(tops / MFMA_F16_PEAK_TFLOPS, 4)},
            "hbm_GB/s_algorithmic": round(PF_BYTES / us / 1e3, 1),
            "note": "the exact per-block f32 folds (9 chains x 16 blocks per output, separately rounded) run on the "
                    "VALU at ~19 ops per (row, token, block); they and the tile staging bound the kernel, not the "
@@ -753,9 +805,12 @@ def main():
 
     value = STEP_BYTES / (mv["ms_per_step"] * 1e-3) / 1e9
     if mv["down_us"] >= mv["gate_us"]:
-        dom = ("k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)", mv["down_us"], DOWN_BYTES, MEASURED_TRAFFIC["down"])
+        dom = ("k_gemv<IQ3_S, fused Q8_K> (down 4096x1536)", mv["down_us"], DOWN_BYTES, MEASURED_TRAFFIC["down"],
+               mv["down_floor"])
     else:
-        dom = ("k_gemv<IQ2_S, fused Q8_K> (gate 1536x4096)", mv["gate_us"], GATE_BYTES, MEASURED_TRAFFIC["gate"])
+        dom = ("k_gemv<IQ2_S, fused Q8_K> (gate 1536x4096)", mv["gate_us"], GATE_BYTES, MEASURED_TRAFFIC["gate"],
+               mv["gate_floor"])
+    step_floor_us = mv["gate_floor"][0] + mv["down_floor"][0]
     achieved = dom[2] / (dom[1] * 1e-6) / 1e9
     line = {
         "metric": "quant matvec HBM GB/s (% of MI355X peak); MoE-block decode tokens/s",
@@ -780,8 +835,16 @@ def main():
                    "algorithmic_bytes_per_step": STEP_BYTES, "lpu": args.lpu},
         "roofline": {"bound": "hbm", "kernel": dom[0], "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": dom[3],
-                     "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2]},
+                     "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2],
+                     **floor_fields(dom[1], mv["empty_us"], dom[4])},
         "kernels_us": {"iq2s_gate": round(mv["gate_us"], 3), "iq3s_down": round(mv["down_us"], 3)},
+        "floors": {"what": "launch floor (an empty kernel) and memory floor (the fastest plain read of the same "
+                           "weight bytes over a sweep of launch shapes, same rotation of copies) per kernel of the "
+                           "step; frac_of_floor = floor / measured",
+                   "gate": floor_fields(mv["gate_us"], mv["empty_us"], mv["gate_floor"]),
+                   "down": floor_fields(mv["down_us"], mv["empty_us"], mv["down_floor"]),
+                   "step_read_floor_us": round(step_floor_us, 3),
+                   "step_frac_of_floor": round(step_floor_us / (mv["ms_per_step"] * 1e3), 4)},
         "q4k_matvec": q4k,
         "model_matvecs": {"workload": "decode matvecs (fused Q8_K + matvec, batch 1) at the Hy3 model's tensor shapes "
                                       "and types (schema.rs:96-201)", "shapes": model_mv},

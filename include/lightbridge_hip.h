@@ -545,13 +545,17 @@ lbh_status lbh_debug_expf(lbh_ctx *ctx, const float *in_dev, float *out_dev, siz
  * the device arithmetic against the C library on any machine. */
 void lbh_debug_expf_host(const float *in, float *out, size_t n, int32_t swiglu, const float *up);
 
-/* [async] Floor references for the matvec rooflines: an empty kernel (the launch
- * floor), and a plain read of a matrix's device bytes with 16-byte loads (the
- * memory floor of a matvec over it), one word per wave XOR-folded into sink_dev
- * (lbh_debug_read_grid(m, ctx) * 4 words). */
+/* [async] Floor references for the matvec rooflines (no counterpart in the
+ * reference): an empty kernel (the launch floor), and a plain read of a
+ * matrix's device bytes with 16-byte non-temporal loads (the memory floor of a
+ * matvec over it) in one of several launch shapes: `grid` workgroups of 256
+ * lanes (1..LBH_DEBUG_READ_MAX_GRID), `unroll` loads in flight per lane (1, 2,
+ * 4 or 8), grid-strided (slab == 0) or one contiguous slab per workgroup.
+ * One word per wave is XOR-folded into sink_dev, which holds 4 * grid words. */
+#define LBH_DEBUG_READ_MAX_GRID 65536
 lbh_status lbh_debug_empty_kernel(lbh_ctx *ctx);
-int32_t lbh_debug_read_grid(const lbh_matrix *m, const lbh_ctx *ctx);
-lbh_status lbh_debug_read_matrix(lbh_ctx *ctx, const lbh_matrix *m, uint32_t *sink_dev);
+lbh_status lbh_debug_read_matrix(lbh_ctx *ctx, const lbh_matrix *m, uint32_t *sink_dev, int32_t grid, int32_t unroll,
+                                 int32_t slab);
 
 /* [sync] Converts n binary16 values with the device conversion the kernels use. */
 lbh_status lbh_debug_f16_to_f32(lbh_ctx *ctx, const uint16_t *in_dev, float *out_dev, size_t n,

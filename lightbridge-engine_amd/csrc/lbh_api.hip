@@ -691,19 +691,13 @@ lbh_status lbh_debug_empty_kernel(lbh_ctx *ctx) {
     return launch_empty(ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
 
-int32_t lbh_debug_read_grid(const lbh_matrix *m, const lbh_ctx *ctx) {
-    if (!m || !ctx) return 0;
-    const long long per_wg = 256LL * 16 * 4;   // four 16-byte loads per lane per step
-    long long grid = ((long long)m->bytes + per_wg - 1) / per_wg;
-    const long long cap = 8LL * ctx->cu_count;
-    return (int32_t)(grid < 1 ? 1 : grid > cap ? cap : grid);
-}
-
-lbh_status lbh_debug_read_matrix(lbh_ctx *ctx, const lbh_matrix *m, uint32_t *sink) {
+lbh_status lbh_debug_read_matrix(lbh_ctx *ctx, const lbh_matrix *m, uint32_t *sink, int32_t grid, int32_t unroll,
+                                 int32_t slab) {
     if (!ctx || !m || !sink) return LBH_NULL_ARGUMENT;
+    if (grid < 1 || grid > LBH_DEBUG_READ_MAX_GRID || (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8))
+        return LBH_INVALID_PARAMETER;
     DeviceGuard g(ctx->device);
-    return launch_stream_read(m->planes, (long long)m->bytes, sink, lbh_debug_read_grid(m, ctx), ctx->stream) ==
-                   hipSuccess
+    return launch_stream_read(m->planes, (long long)m->bytes, sink, grid, unroll, slab != 0, ctx->stream) == hipSuccess
                ? LBH_OK
                : LBH_HIP_ERROR;
 }

@@ -20,6 +20,10 @@
 //                 y = ((0 + c_0 d_0) + c_1 d_1) + ... + 1.0 * d_shared.
 //
 // The shared expert is one more "expert" that every token selects.
+//
+// Several workgroups read the same expert rows (one per chunk of its tokens),
+// so the weight loads keep the default cache policy here.
+#define LBH_WEIGHT_CPOL 0
 #include "lbh_internal.h"
 #include "lbh_math.h"
 #include "lbh_router.h"

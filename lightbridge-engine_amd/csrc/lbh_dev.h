@@ -83,20 +83,33 @@ __device__ __forceinline__ Planes make_planes(const uint8_t *base, long long uni
     return p;
 }
 
+// Cache policy of the weight loads.  A matvec streams each weight byte once
+// per launch: there the loads are nt (non-temporal, cache-policy bit 1 of the
+// gfx950 buffer loads), which measured 12-16% faster on MI355X for every
+// matvec shape (IQ2_S 1536x4096 5.48 -> 4.82 us, Q4_K 4096x4096 6.05 -> 5.17
+// us, Q5_K 120832x4096 5.2 -> 5.6 TB/s).  A translation unit whose kernels
+// read the same weights from several workgroups (the batched decode, where
+// each chunk of an expert's tokens re-reads its rows) defines
+// LBH_WEIGHT_CPOL 0 before including this header: there the nt policy
+// measured 13% slower (450 -> 510 us per 64-token step).
+#ifndef LBH_WEIGHT_CPOL
+#define LBH_WEIGHT_CPOL 2
+#endif
+constexpr int WEIGHT_CPOL = LBH_WEIGHT_CPOL;
 __device__ __forceinline__ uint4 bld128(const Planes &P, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(P.rsrc, voff, soff, 0));
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(P.rsrc, voff, soff, WEIGHT_CPOL));
 }
 __device__ __forceinline__ uint2 bld64(const Planes &P, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(P.rsrc, voff, soff, 0));
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(P.rsrc, voff, soff, WEIGHT_CPOL));
 }
 __device__ __forceinline__ uint32_t bld32(const Planes &P, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b32(P.rsrc, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(P.rsrc, voff, soff, WEIGHT_CPOL);
 }
 __device__ __forceinline__ uint32_t bld16(const Planes &P, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b16(P.rsrc, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b16(P.rsrc, voff, soff, WEIGHT_CPOL);
 }
 __device__ __forceinline__ uint32_t bld8(const Planes &P, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b8(P.rsrc, voff, soff, 0);
+    return __builtin_amdgcn_raw_buffer_load_b8(P.rsrc, voff, soff, WEIGHT_CPOL);
 }
 
 // 24-bit signed multiply (full rate): every integer product in the dots has

@@ -264,7 +264,8 @@ hipError_t launch_validate_scales(int ty, const uint8_t *ggml, long long units,
 hipError_t launch_f16_to_f32(const uint16_t *in, float *out, long long n, hipStream_t s);
 hipError_t launch_empty(hipStream_t s);
 // sink holds grid * 4 words (one per wave).
-hipError_t launch_stream_read(const void *src, long long bytes, uint32_t *sink, int grid, hipStream_t s);
+hipError_t launch_stream_read(const void *src, long long bytes, uint32_t *sink, int grid, int unroll, int slab,
+                              hipStream_t s);
 
 // Raw GGML row dots (vec_dot_q8_k per row; 1 <= nb <= 64), the Q8_K scale scan
 // and the DequantF32 matvec (lbh_dot.hip).  `st` words set -> no writes.

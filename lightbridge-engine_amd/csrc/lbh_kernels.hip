@@ -114,22 +114,41 @@ __global__ void k_f16_to_f32(const uint16_t *in, float *out, long long n) {
 // ------------------------------------------------------- floor measurement
 
 // Reference points for the matvecs' roofline: an empty kernel (the launch
-// floor) and a plain read of a byte range with one 16-byte load per lane per
-// step (the memory floor of reading a matrix's planes); the loaded words are
-// XOR-folded and one word per wave is stored so no load can be dropped.
+// floor) and plain reads of a byte range with 16-byte non-temporal loads (the
+// memory floor of reading a matrix's planes), in one of several launch shapes
+// so that a caller can take the fastest: U loads per lane in flight, either
+// grid-strided over the whole range or over one contiguous slab per
+// workgroup.  The loaded words are XOR-folded and one word per wave is stored
+// so no load can be dropped.
 __global__ void k_empty() {}
 
-__global__ void __launch_bounds__(256) k_stream_read(const uint4 *__restrict__ src, long long n16, uint32_t *sink) {
+typedef unsigned v4u32 __attribute__((ext_vector_type(4)));
+
+template <int U>
+__global__ void __launch_bounds__(256) k_stream_read(const uint4 *__restrict__ src, long long n16, uint32_t *sink,
+                                                     int slab) {
+    const v4u32 *p = reinterpret_cast<const v4u32 *>(src);
     uint32_t acc = 0;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; i + 3 * stride < n16; i += 4 * stride) {
-        const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    long long i0, end, stride;
+    if (slab) {
+        const long long per = (n16 + gridDim.x - 1) / gridDim.x;
+        i0 = (long long)blockIdx.x * per + threadIdx.x;
+        end = min((long long)(blockIdx.x + 1) * per, n16);
+        stride = blockDim.x;
+    } else {
+        i0 = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+        end = n16;
+        stride = (long long)gridDim.x * blockDim.x;
     }
-    for (; i < n16; i += stride) {
-        const uint4 a = src[i];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    for (long long i = i0; i < end; i += U * stride) {
+        v4u32 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long long j = i + u * stride;
+            v[u] = j < end ? __builtin_nontemporal_load(p + j) : v4u32{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     for (int off = 32; off >= 1; off >>= 1) acc ^= __shfl_xor(acc, off, 64);
     if ((threadIdx.x & 63) == 0) sink[(blockIdx.x * blockDim.x + threadIdx.x) >> 6] = acc;
@@ -140,9 +159,17 @@ hipError_t launch_empty(hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_stream_read(const void *src, long long bytes, uint32_t *sink, int grid, hipStream_t s) {
-    if (bytes < 16 || grid < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_stream_read, dim3(grid), dim3(256), 0, s, static_cast<const uint4 *>(src), bytes / 16, sink);
+hipError_t launch_stream_read(const void *src, long long bytes, uint32_t *sink, int grid, int unroll, int slab,
+                              hipStream_t s) {
+    if (bytes < 16 || grid < 1 || grid > 65536) return hipErrorInvalidValue;
+    const uint4 *p = static_cast<const uint4 *>(src);
+    switch (unroll) {
+    case 1: hipLaunchKernelGGL(k_stream_read<1>, dim3(grid), dim3(256), 0, s, p, bytes / 16, sink, slab); break;
+    case 2: hipLaunchKernelGGL(k_stream_read<2>, dim3(grid), dim3(256), 0, s, p, bytes / 16, sink, slab); break;
+    case 4: hipLaunchKernelGGL(k_stream_read<4>, dim3(grid), dim3(256), 0, s, p, bytes / 16, sink, slab); break;
+    case 8: hipLaunchKernelGGL(k_stream_read<8>, dim3(grid), dim3(256), 0, s, p, bytes / 16, sink, slab); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

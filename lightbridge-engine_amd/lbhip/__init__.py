@@ -108,8 +108,7 @@ def lib() -> C.CDLL:
             "lbh_gemv_dequant_f32": ([p, p, p, p, C.c_float, i32], i32),
             "lbh_debug_f16_to_f32": ([p, p, p, sz, E], i32),
             "lbh_debug_empty_kernel": ([p], i32),
-            "lbh_debug_read_grid": ([p, p], i32),
-            "lbh_debug_read_matrix": ([p, p, p], i32),
+            "lbh_debug_read_matrix": ([p, p, p, i32, i32, i32], i32),
             "lbh_moe_create": ([p, p, p, p, sz, p, p, p, C.POINTER(p), E], i32),
             "lbh_moe_destroy": ([p], i32),
             "lbh_moe_set_tiles": ([p, i32, i32, i32], i32),
@@ -338,13 +337,14 @@ class HipBackend:
         """One empty kernel launch (the launch floor of a matvec)."""
         lib().lbh_debug_empty_kernel(self.ctx)
 
-    def read_matrix(self, m: "DeviceMatrix", sink) -> None:
-        """A plain 16-byte-per-lane read of the matrix's device bytes (its matvec's memory floor);
-        sink: int32 device tensor of read_sink_words(m) words."""
-        lib().lbh_debug_read_matrix(self.ctx, m.handle, _dev_ptr(sink))
+    READ_MAX_GRID = 65536
 
-    def read_sink_words(self, m: "DeviceMatrix") -> int:
-        return 4 * lib().lbh_debug_read_grid(m.handle, self.ctx)
+    def read_matrix(self, m: "DeviceMatrix", sink, grid: int, unroll: int = 4, slab: bool = False) -> None:
+        """A plain read of the matrix's device bytes with 16-byte non-temporal loads (its matvec's memory
+        floor) in one launch shape; sink: int32 device tensor of at least 4 * grid words."""
+        st = lib().lbh_debug_read_matrix(self.ctx, m.handle, _dev_ptr(sink), grid, unroll, int(slab))
+        if st:
+            raise KernelError(LbhError(status=st))
 
     def f16_to_f32(self, src, dst) -> None:
         _call(lib().lbh_debug_f16_to_f32, self.ctx, _dev_ptr(src), _dev_ptr(dst), src.numel())
@@ -516,7 +516,7 @@ class MoeLayer:
             raise KernelError(LbhError(status=st))
 
     def set_streams(self, two_streams: bool) -> None:
-        """Shared expert on a second stream beside the routed experts (default) or all on one."""
+        """Shared expert on a second stream beside the routed experts, or (default) all on one."""
         st = lib().lbh_moe_set_streams(self.handle, 1 if two_streams else 0)
         if st:
             raise KernelError(LbhError(status=st))
