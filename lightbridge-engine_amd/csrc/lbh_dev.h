@@ -165,27 +165,55 @@ __device__ __forceinline__ QuantIn quantize_load(const float *__restrict__ x, lo
     return q;
 }
 
+// Row (16-lane) reductions through DPP, every lane of the row receiving the
+// result: quad butterflies, then the half-row and row mirrors.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_row(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t row16_max(uint32_t v) {
+    uint32_t o = dpp_row<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v = o > v ? o : v;
+    o = dpp_row<0x4E>(v);            // quad_perm [2, 3, 0, 1]
+    v = o > v ? o : v;
+    o = dpp_row<0x141>(v);           // row_half_mirror
+    v = o > v ? o : v;
+    o = dpp_row<0x140>(v);           // row_mirror
+    return o > v ? o : v;
+}
+__device__ __forceinline__ uint32_t row16_or(uint32_t v) {
+    v |= dpp_row<0xB1>(v);
+    v |= dpp_row<0x4E>(v);
+    v |= dpp_row<0x141>(v);
+    return v | dpp_row<0x140>(v);
+}
+
 __device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out) {
     const int lane = threadIdx.x & 63;
     const int li = lane & 15;
     const float *v = q.v;
-    uint32_t amax_l = __float_as_uint(fabsf(v[0]));
-    float max_l = v[0];
+    // The lane's largest |x| and the value at its first index: a pairwise
+    // tree whose strict compare keeps the lower index on ties.
+    uint32_t a[16];
+    float mv[16];
 #pragma unroll
-    for (int i = 1; i < 16; ++i) {
-        const uint32_t a = __float_as_uint(fabsf(v[i]));
-        if (a > amax_l) amax_l = a, max_l = v[i];
-    }
-    uint32_t amax = amax_l;
+    for (int i = 0; i < 16; ++i) a[i] = __float_as_uint(fabsf(v[i])), mv[i] = v[i];
 #pragma unroll
-    for (int off = 8; off >= 1; off >>= 1) {
-        const uint32_t o = __shfl_xor(amax, off, 16);
-        amax = o > amax ? o : amax;
+    for (int st = 1; st < 16; st *= 2) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 2 * st) {
+            if (a[i + st] > a[i]) a[i] = a[i + st], mv[i] = mv[i + st];
+        }
     }
+    const uint32_t amax_l = a[0];
+    const uint32_t amax = row16_max(amax_l);
+    // The lowest lane of the row holding the row maximum owns the first index
+    // (lane order is element order); its value reaches the row by an OR of
+    // the owner's bits with zeros.
     const unsigned long long hit = __ballot(amax_l == amax);
     const int row0 = lane & 48;
     const int owner = row0 + __builtin_ctzll((hit >> row0) & 0xffffull);
-    const float maxv = __shfl(max_l, owner, 64);
+    const float maxv = __uint_as_float(row16_or(lane == owner ? __float_as_uint(mv[0]) : 0u));
     uint32_t packed[4] = {0, 0, 0, 0};
     int32_t qsum = 0;
     float d = 0.0f;
@@ -200,7 +228,9 @@ __device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out) {
         }
         d = 1.0f / iscale;
     }
-    const int32_t next = __shfl_down(qsum, 1, 64);
+    // bsums pair: this lane's sum and the next lane's (row_shl:1; only even
+    // lanes of a row use it, so the source stays inside the row).
+    const int32_t next = __builtin_amdgcn_update_dpp(0, qsum, 0x101, 0xf, 0xf, false);
     if (q.valid) {
         uint8_t *ob = out + q.blk * 292;
         uint32_t *qs = reinterpret_cast<uint32_t *>(ob + 4 + 16 * li);
