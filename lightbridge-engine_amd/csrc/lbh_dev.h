@@ -523,30 +523,68 @@ __device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t
 constexpr uint32_t IQ2S_POS = 0x002b1908u;
 constexpr uint32_t IQ2S_NEG = 0x00d5e7f8u;
 
-// IQ2_S integer block sum over the slice's groups (q8_k.rs:337-364).
-template <int LPU>
+// IQ2_S integer block sum over the slice's groups (q8_k.rs:337-364).  With
+// GB > 0 the codebook and sign-table reads of GB groups at a time are issued
+// before any of them is used (one LDS round trip per GB groups instead of
+// one per pair of lookups, at the cost of the registers that hold them: a
+// latency-bound matvec with one wave per SIMD gains, kernels that rely on
+// occupancy keep GB = 0, the compiler's interleaved schedule).
+template <int LPU, int GB = 0>
 __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, const ActIQ<8 / LPU> &a,
                                              const uint2 *grid) {
     constexpr int G = 8 / LPU;
     int32_t bsum = 0;
+    if constexpr (GB == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
-        const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
-        int32_t part[2] = {0, 0};
+        for (int g = 0; g < G; ++g) {
+            const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+            const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
+            int32_t part[2] = {0, 0};
 #pragma unroll
-        for (int lg = 0; lg < 4; ++lg) {
-            const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
-            const uint2 code = grid[idx];
-            // selector bits of the eight sign bits: byte i takes the negated
-            // source (selector 4 + code) when sign bit i is set
-            const uint2 sm = grid[1024 + byte_of(w.sg[g], lg)];
-            const uint32_t sel_lo = sm.x | code.x;
-            const uint32_t sel_hi = sm.y | code.y;
-            part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
-            part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
+            for (int lg = 0; lg < 4; ++lg) {
+                const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
+                const uint2 code = grid[idx];
+                // selector bits of the eight sign bits: byte i takes the
+                // negated source (selector 4 + code) when sign bit i is set
+                const uint2 sm = grid[1024 + byte_of(w.sg[g], lg)];
+                const uint32_t sel_lo = sm.x | code.x;
+                const uint32_t sel_hi = sm.y | code.y;
+                part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
+                part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
+            }
+            bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
         }
-        bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
+    } else {
+        constexpr int GC = G < GB ? G : GB;
+#pragma unroll
+        for (int g0 = 0; g0 < G; g0 += GC) {
+            uint2 code[GC][4], sm[GC][4];
+#pragma unroll
+            for (int k = 0; k < GC; ++k) {
+                const int g = g0 + k;
+                const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+#pragma unroll
+                for (int lg = 0; lg < 4; ++lg) {
+                    code[k][lg] = grid[byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u)];
+                    sm[k][lg] = grid[1024 + byte_of(w.sg[g], lg)];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < GC; ++k) {
+                const int g = g0 + k;
+                const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
+                int32_t part[2] = {0, 0};
+#pragma unroll
+                for (int lg = 0; lg < 4; ++lg) {
+                    const uint32_t sel_lo = sm[k][lg].x | code[k][lg].x;
+                    const uint32_t sel_hi = sm[k][lg].y | code[k][lg].y;
+                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
+                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
+                }
+                bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
+            }
+        }
     }
     return bsum;
 }
@@ -599,31 +637,68 @@ __device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t
     }
 }
 
-// IQ3_S integer block sum over the slice's groups (q8_k.rs:380-428).
-template <int LPU>
+// IQ3_S integer block sum over the slice's groups (q8_k.rs:380-428); GB as
+// for IQ2_S.
+template <int LPU, int GB = 0>
 __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, const ActIQ<8 / LPU> &a,
                                              const uint2 *grid) {
     constexpr int G = 8 / LPU;
     int32_t bsum = 0;
+    if constexpr (GB == 0) {
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
-        // local group g is global group gg = G*p + g; its scale nibble is
-        // nibble (gg & 1) of scale byte gg / 2, i.e. nibble g of w.sc (G <= 4)
-        // or nibble g of the 32-bit word holding all four scale bytes (G == 8).
-        const uint32_t ps = (w.sc >> (4 * g)) & 15u;
-        int32_t gs = 0;
+        for (int g = 0; g < G; ++g) {
+            const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+            // local group g is global group gg = G*p + g; its scale nibble is
+            // nibble (gg & 1) of scale byte gg / 2, i.e. nibble g of w.sc (G <= 4)
+            // or nibble g of the 32-bit word holding all four scale bytes (G == 8).
+            const uint32_t ps = (w.sc >> (4 * g)) & 15u;
+            int32_t gs = 0;
 #pragma unroll
-        for (int lg = 0; lg < 4; ++lg) {
-            const uint32_t qq = w.qs[2 * g + (lg >> 1)];
-            const int sh = 16 * (lg & 1);
-            const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
-            const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
-            const uint2 g1 = grid[i1], g2 = grid[i2], sm = grid[512 + byte_of(w.sg[g], lg)];
-            gs = dot4(perm(g1.y, g1.x, sm.x), a.q[8 * g + 2 * lg], gs);
-            gs = dot4(perm(g2.y, g2.x, sm.y), a.q[8 * g + 2 * lg + 1], gs);
+            for (int lg = 0; lg < 4; ++lg) {
+                const uint32_t qq = w.qs[2 * g + (lg >> 1)];
+                const int sh = 16 * (lg & 1);
+                const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
+                const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
+                const uint2 g1 = grid[i1], g2 = grid[i2], sm = grid[512 + byte_of(w.sg[g], lg)];
+                gs = dot4(perm(g1.y, g1.x, sm.x), a.q[8 * g + 2 * lg], gs);
+                gs = dot4(perm(g2.y, g2.x, sm.y), a.q[8 * g + 2 * lg + 1], gs);
+            }
+            bsum += mul24(gs, (int32_t)(2 * ps + 1));
         }
-        bsum += mul24(gs, (int32_t)(2 * ps + 1));
+        return bsum;
+    }
+    constexpr int GC = GB == 0 ? 1 : G < GB ? G : GB;
+#pragma unroll
+    for (int g0 = 0; g0 < G; g0 += GC) {
+        uint2 g1[GC][4], g2[GC][4], sm[GC][4];
+#pragma unroll
+        for (int k = 0; k < GC; ++k) {
+            const int g = g0 + k;
+            const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+#pragma unroll
+            for (int lg = 0; lg < 4; ++lg) {
+                const uint32_t qq = w.qs[2 * g + (lg >> 1)];
+                const int sh = 16 * (lg & 1);
+                const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
+                const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
+                g1[k][lg] = grid[i1];
+                g2[k][lg] = grid[i2];
+                sm[k][lg] = grid[512 + byte_of(w.sg[g], lg)];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < GC; ++k) {
+            const int g = g0 + k;
+            const uint32_t ps = (w.sc >> (4 * g)) & 15u;
+            int32_t gs = 0;
+#pragma unroll
+            for (int lg = 0; lg < 4; ++lg) {
+                gs = dot4(perm(g1[k][lg].y, g1[k][lg].x, sm[k][lg].x), a.q[8 * g + 2 * lg], gs);
+                gs = dot4(perm(g2[k][lg].y, g2[k][lg].x, sm[k][lg].y), a.q[8 * g + 2 * lg + 1], gs);
+            }
+            bsum += mul24(gs, (int32_t)(2 * ps + 1));
+        }
     }
     return bsum;
 }

@@ -95,7 +95,11 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
     auto process = [&](int it, const W &w) {
         const int r = it * L.rpw + L.slot;
         const bool on = L.lane_on && r < rows;
-        const float v = row_dot<TY, LPU>(w, act, on, L, s_grid, s_fold[wid], p.block_sums, (long long)r * NB + L.b);
+        // One wave per SIMD: the codebook reads are gathered (the latency of a
+        // single wave's LDS round trips is the dot's critical path).
+        constexpr int GB = TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
+        const float v =
+            row_dot<TY, LPU, GB>(w, act, on, L, s_grid, s_fold[wid], p.block_sums, (long long)r * NB + L.b);
         if (on && L.leader()) store_y(p, r, v);
     };
 

@@ -68,9 +68,10 @@ using WOf = typename std::conditional<Traits<TY>::KQ, WSliceKQ<TY, LPU>, WSlice<
 
 // Integer stage + fold of one wave step.  `on` marks lanes whose row exists;
 // the row value is returned in the row's leader lane (part 0, block 0).
-// block_sums (optional) receives the integer stage of unit u.  Contains wave
-// barriers: every lane of the wave must call it.
-template <int TY, int LPU>
+// block_sums (optional) receives the integer stage of unit u.  GB: codebook
+// lookups gathered per GB groups (slice_sum).  Contains wave barriers: every
+// lane of the wave must call it.
+template <int TY, int LPU, int GB = 0>
 __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, LPU> &act, bool on,
                                          const LaneMap<LPU> &L, const void *grid, FoldLDS<TY> &f,
                                          int32_t *block_sums, long long u) {
@@ -115,7 +116,7 @@ __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, 
         int32_t bs = 0;
         uint32_t dbits = 0;
         if (on) {
-            bs = slice_sum(w, act, reinterpret_cast<const uint2 *>(grid));
+            bs = slice_sum<LPU, GB>(w, act, reinterpret_cast<const uint2 *>(grid));
             dbits = w.d;
         }
         bs = unit_reduce<LPU>(bs);
