@@ -188,7 +188,15 @@ __device__ __forceinline__ uint32_t row16_or(uint32_t v) {
     return v | dpp_row<0x140>(v);
 }
 
-__device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out) {
+// out_r (optional): a residue-major copy of the block's quants for the
+// K-quant dots, 256 bytes per block at out_r + RES_STRIDE * block (the 16
+// bytes of padding keep the 16-byte reads of consecutive blocks by
+// consecutive lanes in distinct LDS banks): dword t of
+// 32-byte group j holds the quants 32j + t + 8k, k = 0..3 (the ActKQ layout).
+// Lane li holds group li / 2's quants 16 (li & 1) .. + 15, i.e. bytes k = 2
+// (li & 1) and 2 (li & 1) + 1 of each of the group's eight dwords.
+constexpr int RES_STRIDE = 272;
+__device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out, uint8_t *out_r = nullptr) {
     const int lane = threadIdx.x & 63;
     const int li = lane & 15;
     const float *v = q.v;
@@ -240,12 +248,24 @@ __device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out) {
             *reinterpret_cast<uint32_t *>(ob + 260 + 2 * li) =
                 (uint32_t)(uint16_t)(int16_t)qsum | ((uint32_t)(uint16_t)(int16_t)next << 16);
         if (li == 0) *reinterpret_cast<uint32_t *>(ob) = __float_as_uint(d);
+        if (out_r) {
+            // half-dword t = quants t and t + 8 of this lane's 16
+            const uint32_t h01 = perm(packed[2], packed[0], 0x05010400u);   // t = 0, 1
+            const uint32_t h23 = perm(packed[2], packed[0], 0x07030602u);   // t = 2, 3
+            const uint32_t h45 = perm(packed[3], packed[1], 0x05010400u);   // t = 4, 5
+            const uint32_t h67 = perm(packed[3], packed[1], 0x07030602u);   // t = 6, 7
+            uint16_t *o = reinterpret_cast<uint16_t *>(out_r + q.blk * RES_STRIDE + 32 * (li >> 1) + 2 * (li & 1));
+            o[0] = (uint16_t)h01, o[2] = (uint16_t)(h01 >> 16);
+            o[4] = (uint16_t)h23, o[6] = (uint16_t)(h23 >> 16);
+            o[8] = (uint16_t)h45, o[10] = (uint16_t)(h45 >> 16);
+            o[12] = (uint16_t)h67, o[14] = (uint16_t)(h67 >> 16);
+        }
     }
 }
 
 __device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x, uint8_t *out, long long first,
-                                                     long long nblocks) {
-    quantize_store(quantize_load(x, first, nblocks), out);
+                                                     long long nblocks, uint8_t *out_r = nullptr) {
+    quantize_store(quantize_load(x, first, nblocks), out, out_r);
 }
 
 // ------------------------------------------------------------ type traits
@@ -326,6 +346,27 @@ __device__ __forceinline__ void load_act(const uint8_t *blk, int p, ActKQ<G> &a)
             for (int k = 0; k < 4; ++k) v |= byte_of(n[2 * k + t / 4], t % 4) << (8 * k);
             a.t[j][t] = v;
         }
+    }
+    const uint8_t *bs = blk + 260 + 8 * G * p;
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+        const uint32_t w = ld_u32(bs + 4 * j);
+        a.bsp[j] = (int32_t)(int16_t)(w & 0xffff) + (int32_t)(int16_t)(w >> 16);
+    }
+}
+
+// The same K-quant slice from a residue-major copy of the block's quants
+// (quantize_store's out_r): `res` is the block's 256 bytes, `blk` its Q8_K
+// block (scale and bsums).
+template <int G>
+__device__ __forceinline__ void load_act_res(const uint8_t *blk, const uint8_t *res, int p, ActKQ<G> &a) {
+    a.d8 = __uint_as_float(ld_u32(blk));
+    const uint4 *q = reinterpret_cast<const uint4 *>(res + 64 * G * p);
+#pragma unroll
+    for (int j = 0; j < 2 * G; ++j) {
+        const uint4 v0 = q[2 * j], v1 = q[2 * j + 1];
+        a.t[j][0] = v0.x, a.t[j][1] = v0.y, a.t[j][2] = v0.z, a.t[j][3] = v0.w;
+        a.t[j][4] = v1.x, a.t[j][5] = v1.y, a.t[j][6] = v1.z, a.t[j][7] = v1.w;
     }
     const uint8_t *bs = blk + 260 + 8 * G * p;
 #pragma unroll

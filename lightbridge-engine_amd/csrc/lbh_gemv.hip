@@ -38,6 +38,10 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
     constexpr int GB = GridLDS<TY>::BYTES > 0 ? GridLDS<TY>::BYTES : 16;
     __shared__ __align__(16) uint8_t s_grid[GB];
     __shared__ __align__(16) uint8_t s_q8[FUSEQ ? MAX_NB * 292 : 16];
+    // K-quant dots read the quants residue-major: quantized once per workgroup
+    // into that layout too, instead of a byte transpose in every lane.
+    constexpr bool RES = FUSEQ && Traits<TY>::KQ;
+    __shared__ __align__(16) uint8_t s_q8r[RES ? MAX_NB * RES_STRIDE : 16];
     __shared__ FoldLDS<TY> s_fold[GEMV_WAVES];
 
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -76,8 +80,9 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
 
     grid_store<TY>(gin, s_grid);
     if constexpr (FUSEQ) {
-        quantize_store(qin, s_q8);
-        for (int b0 = 4 * wid + 4 * GEMV_WAVES; b0 < NB; b0 += 4 * GEMV_WAVES) quantize_blocks_wave(p.x, s_q8, b0, NB);
+        quantize_store(qin, s_q8, RES ? s_q8r : nullptr);
+        for (int b0 = 4 * wid + 4 * GEMV_WAVES; b0 < NB; b0 += 4 * GEMV_WAVES)
+            quantize_blocks_wave(p.x, s_q8, b0, NB, RES ? s_q8r : nullptr);
     }
     __syncthreads();
 #pragma unroll
@@ -90,7 +95,10 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
     }
 
     ActOf<TY, LPU> act;
-    load_act(FUSEQ ? s_q8 + L.b * 292 : p.q8 + (long long)L.b * 292, L.part, act);
+    if constexpr (RES)
+        load_act_res(s_q8 + L.b * 292, s_q8r + L.b * RES_STRIDE, L.part, act);
+    else
+        load_act(FUSEQ ? s_q8 + L.b * 292 : p.q8 + (long long)L.b * 292, L.part, act);
 
     auto process = [&](int it, const W &w) {
         const int r = it * L.rpw + L.slot;
