@@ -18,8 +18,12 @@
 
 namespace lbh {
 
+// Workgroups of 256 threads, or 512 for matrices large enough to give every
+// CU several such workgroups' worth of wave steps: every workgroup pays the
+// prologue (codebook and activation staging), so fewer, larger workgroups
+// pay it fewer times.
 constexpr int GEMV_THREADS = 256;
-constexpr int GEMV_WAVES = GEMV_THREADS / 64;
+constexpr int GEMV_THREADS_LARGE = 512;
 constexpr int MAX_NB = 64;
 
 __device__ __forceinline__ bool status_set(const DevStatus *st) {
@@ -33,8 +37,9 @@ __device__ __forceinline__ void store_y(const GemvArgs &p, int r, float v) {
         p.y[r] = v;
 }
 
-template <int TY, int LPU, bool FUSEQ, int D>
-__global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
+template <int TY, int LPU, bool FUSEQ, int D, int NT>
+__global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
+    constexpr int GEMV_WAVES = NT / 64;
     constexpr int GB = GridLDS<TY>::BYTES > 0 ? GridLDS<TY>::BYTES : 16;
     __shared__ __align__(16) uint8_t s_grid[GB];
     __shared__ __align__(16) uint8_t s_q8[FUSEQ ? MAX_NB * 292 : 16];
@@ -90,7 +95,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) k_gemv(GemvArgs p) {
     if (status_set(p.status)) return;
     if constexpr (FUSEQ) {
         if (p.q8_out && blockIdx.x == 0)
-            for (int i = threadIdx.x; i < NB * 73; i += GEMV_THREADS)
+            for (int i = threadIdx.x; i < NB * 73; i += NT)
                 reinterpret_cast<uint32_t *>(p.q8_out)[i] = reinterpret_cast<const uint32_t *>(s_q8)[i];
     }
 
@@ -130,32 +135,44 @@ static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b)
 
 // Workgroups of one kernel instance that fit on a CU at once (register and LDS
 // limited), queried once per instance.
-template <int TY, int LPU, bool FUSEQ, int D>
+template <int TY, int LPU, bool FUSEQ, int D, int NT>
 static int resident_per_cu() {
     static std::atomic<int> cached{0};
     int n = cached.load(std::memory_order_relaxed);
     if (n == 0) {
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv<TY, LPU, FUSEQ, D>, GEMV_THREADS, 0) != hipSuccess ||
-            n < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_gemv<TY, LPU, FUSEQ, D, NT>, NT, 0) != hipSuccess || n < 1)
             n = 1;
         cached.store(n, std::memory_order_relaxed);
     }
     return n;
 }
 
-// Grid: one workgroup per GEMV_WAVES wave steps, capped at `max_blocks`, or,
+// Grid: one workgroup per NT / 64 wave steps, capped at `max_blocks`, or,
 // when that is 0, at the workgroups resident on the device at once: a
 // persistent grid pays the prologue (codebook and activation staging) once per
 // resident workgroup instead of once per later wave of workgroups.
-template <int TY, int LPU, bool FUSEQ, int D>
-static hipError_t launch_inst(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
+template <int TY, int LPU, bool FUSEQ, int D, int NT>
+static hipError_t launch_nt(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
     const int rpw = (64 / LPU) / a.m.nb;
     const int items = cdiv(a.m.rows, rpw);
-    int grid = cdiv(items, GEMV_WAVES);
-    const int cap = t.max_blocks > 0 ? t.max_blocks : resident_per_cu<TY, LPU, FUSEQ, D>() * t.cu_count;
+    int grid = cdiv(items, NT / 64);
+    const int cap = t.max_blocks > 0 ? t.max_blocks : resident_per_cu<TY, LPU, FUSEQ, D, NT>() * t.cu_count;
     if (cap > 0 && grid > cap) grid = cap;
-    hipLaunchKernelGGL((k_gemv<TY, LPU, FUSEQ, D>), dim3(grid), dim3(GEMV_THREADS), 0, s, a);
+    hipLaunchKernelGGL((k_gemv<TY, LPU, FUSEQ, D, NT>), dim3(grid), dim3(NT), 0, s, a);
     return hipGetLastError();
+}
+
+// 512-thread workgroups for one lane per unit once the matrix has at least
+// 2 * 64 * 4 units per CU (measured on MI355X: IQ2_S 8192x4096 7.2 -> 6.0 us,
+// IQ3_S 4096x13312 14.5 -> 12.7 us; Q4_K 4096x4096 stays faster at 256).
+template <int TY, int LPU, bool FUSEQ, int D>
+static hipError_t launch_inst(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
+    if constexpr (LPU == 1) {
+        const long long units = (long long)a.m.rows * a.m.nb;
+        if (units >= 2LL * 64 * 4 * (t.cu_count > 0 ? t.cu_count : 256))
+            return launch_nt<TY, LPU, FUSEQ, D, GEMV_THREADS_LARGE>(a, t, s);
+    }
+    return launch_nt<TY, LPU, FUSEQ, D, GEMV_THREADS>(a, t, s);
 }
 
 template <int TY, int LPU, int D>
@@ -185,14 +202,16 @@ static hipError_t launch_lpu(const GemvArgs &a, const GemvTuning &t, int lpu, in
 
 // Built-in lanes-per-unit choice.  One lane per (row, block) unit reads each
 // block once with the fewest instructions, but holds a whole block of
-// activations in registers (two or three waves per SIMD); it is the faster
-// choice once the matrix gives every CU at least four such waves.  Smaller
-// matrices are latency-bound and gain from the shorter per-lane work of two
-// lanes per unit (measured on MI355X: Q4_K 4096x4096 6.0 vs 6.9 us at one and
-// two lanes; IQ2_S 1536x4096 5.4 vs 5.8 us at two and one).
+// activations in registers; it is the faster choice once the matrix gives
+// every CU at least four such waves.  Smaller matrices are latency-bound and
+// gain from the shorter per-lane work of more lanes per unit (measured on
+// MI355X: Q4_K 4096x4096 4.5 vs 5.5 us at one and two lanes; IQ2_S 1536x4096
+// 4.6 vs 5.2 us at two and one; IQ2_S 1024x4096 4.3 vs 4.6 us at four and
+// two).
 static int default_lpu(const GemvArgs &a, int cu_count) {
     const long long units = (long long)a.m.rows * a.m.nb;
-    return units >= 64LL * 4 * (cu_count > 0 ? cu_count : 256) ? 1 : 2;
+    const long long cus = cu_count > 0 ? cu_count : 256;
+    return units >= 64LL * 4 * cus ? 1 : units >= 80LL * cus ? 2 : 4;
 }
 
 hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
