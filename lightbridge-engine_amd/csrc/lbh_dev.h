@@ -411,86 +411,86 @@ __device__ __forceinline__ uint2 sign_lut_entry(uint32_t s) {
 // the selector arithmetic.
 __device__ __forceinline__ uint2 iq3_sign_entry(uint32_t s) { return make_uint2(sign_sel(s & 15u), sign_sel(s >> 4)); }
 
+// The LDS images of both tables (GridLDS layout), built at compile time from
+// the codebooks: a workgroup's fill is a plain copy with 16-byte loads.
+struct GridImages {
+    uint32_t iq2s[2 * (1024 + 256)];
+    uint32_t iq3s[2 * (512 + 256)];
+    constexpr GridImages() : iq2s{}, iq3s{} {
+        const uint64_t g2[1024] = {LBH_IQ2S_GRID_VALUES};
+        for (int i = 0; i < 1024; ++i) {
+            uint32_t c[2] = {0, 0};
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t m = (uint32_t)(g2[i] >> (8 * e)) & 0xffu;
+                c[e >> 2] |= (m == 8 ? 0u : m == 25 ? 1u : 2u) << (8 * (e & 3));
+            }
+            iq2s[2 * i] = c[0], iq2s[2 * i + 1] = c[1];
+        }
+        // sign_lut_entry: nib * 0x810204 moves bit i to bit 8i + 2 with no carries.
+        for (uint32_t sb = 0; sb < 256; ++sb) {
+            iq2s[2 * (1024 + sb)] = ((sb & 15u) * 0x810204u) & 0x04040404u;
+            iq2s[2 * (1024 + sb) + 1] = ((sb >> 4) * 0x810204u) & 0x04040404u;
+        }
+        const uint32_t g3[512] = {LBH_IQ3S_GRID_VALUES};
+        for (int i = 0; i < 512; ++i) iq3s[2 * i] = g3[i], iq3s[2 * i + 1] = (g3[i] ^ 0xffffffffu) + 0x01010101u;
+        // iq3_sign_entry: sign_sel of each nibble.
+        for (uint32_t sb = 0; sb < 256; ++sb) {
+            iq3s[2 * (512 + sb)] = (((sb & 15u) * 0x810204u) & 0x04040404u) | 0x03020100u;
+            iq3s[2 * (512 + sb) + 1] = (((sb >> 4) * 0x810204u) & 0x04040404u) | 0x03020100u;
+        }
+    }
+};
+static __constant__ GridImages c_grid_images = GridImages();
+
+template <int TY>
+__device__ __forceinline__ const uint4 *grid_image() {
+    return reinterpret_cast<const uint4 *>(TY == T_IQ2_S ? c_grid_images.iq2s : c_grid_images.iq3s);
+}
+
 // Fills the grid for TY into `lds` (cooperatively, all threads of the block);
 // the caller synchronises afterwards.  grid_load / grid_store split it so the
-// table reads can be issued ahead of a kernel's weight loads (blocks of up to
-// 256 threads: four IQ2S entries or two IQ3S entries per thread).
+// table reads can be issued ahead of a kernel's weight loads (the first 256
+// threads of the block: three IQ2S or two IQ3S 16-byte pieces per thread).
 template <int TY>
 struct GridIn {
-    uint64_t e[TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 1];
+    static constexpr int PIECES = GridLDS<TY>::BYTES / 16;
+    static constexpr int N = PIECES == 0 ? 1 : (PIECES + 255) / 256;
+    uint4 e[N];
 };
 
 template <int TY>
 __device__ __forceinline__ GridIn<TY> grid_load() {
     GridIn<TY> g;
-    if constexpr (TY == T_IQ2_S) {
+    if constexpr (GridIn<TY>::PIECES > 0) {
+        const uint4 *img = grid_image<TY>();
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < GridIn<TY>::N; ++k) {
             const int i = threadIdx.x + 256 * k;
-            g.e[k] = threadIdx.x < 256 ? c_iq2s_grid[i] : 0;
+            g.e[k] = threadIdx.x < 256 && i < GridIn<TY>::PIECES ? img[i] : make_uint4(0u, 0u, 0u, 0u);
         }
-    } else if constexpr (TY == T_IQ3_S) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            g.e[k] = threadIdx.x < 256 ? c_iq3s_grid[i] : 0;
-        }
-    } else {
-        g.e[0] = 0;
     }
     return g;
 }
 
 template <int TY>
 __device__ __forceinline__ void grid_store(const GridIn<TY> &g, void *lds) {
-    if (threadIdx.x >= 256) return;
-    if constexpr (TY == T_IQ2_S) {
-        uint2 *out = reinterpret_cast<uint2 *>(lds);
+    if constexpr (GridIn<TY>::PIECES > 0) {
+        if (threadIdx.x >= 256) return;
+        uint4 *out = reinterpret_cast<uint4 *>(lds);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint64_t v = g.e[k];
-            uint32_t c[2] = {0, 0};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t m = (uint32_t)(v >> (8 * e)) & 0xffu;
-                c[e >> 2] |= (m == 8 ? 0u : m == 25 ? 1u : 2u) << (8 * (e & 3));
-            }
-            out[threadIdx.x + 256 * k] = make_uint2(c[0], c[1]);
+        for (int k = 0; k < GridIn<TY>::N; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < GridIn<TY>::PIECES) out[i] = g.e[k];
         }
-        out[1024 + threadIdx.x] = sign_lut_entry(threadIdx.x);
-    } else if constexpr (TY == T_IQ3_S) {
-        uint2 *out = reinterpret_cast<uint2 *>(lds);
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const uint32_t v = (uint32_t)g.e[k];
-            out[threadIdx.x + 256 * k] = make_uint2(v, neg_bytes(v));
-        }
-        out[512 + threadIdx.x] = iq3_sign_entry(threadIdx.x);
     }
 }
 
 template <int TY>
 __device__ __forceinline__ void fill_grid(void *lds) {
-    if constexpr (TY == T_IQ2_S) {
-        uint2 *g = reinterpret_cast<uint2 *>(lds);
-        for (int i = threadIdx.x; i < 1024; i += blockDim.x) {
-            const uint64_t v = c_iq2s_grid[i];
-            uint32_t c[2] = {0, 0};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t m = (uint32_t)(v >> (8 * e)) & 0xffu;
-                c[e >> 2] |= (m == 8 ? 0u : m == 25 ? 1u : 2u) << (8 * (e & 3));
-            }
-            g[i] = make_uint2(c[0], c[1]);
-        }
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) g[1024 + i] = sign_lut_entry(i);
-    } else if constexpr (TY == T_IQ3_S) {
-        uint2 *g = reinterpret_cast<uint2 *>(lds);
-        for (int i = threadIdx.x; i < 512; i += blockDim.x) {
-            const uint32_t v = c_iq3s_grid[i];
-            g[i] = make_uint2(v, neg_bytes(v));
-        }
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) g[512 + i] = iq3_sign_entry(i);
+    if constexpr (GridIn<TY>::PIECES > 0) {
+        const uint4 *img = grid_image<TY>();
+        uint4 *out = reinterpret_cast<uint4 *>(lds);
+        for (int i = threadIdx.x; i < GridIn<TY>::PIECES; i += blockDim.x) out[i] = img[i];
     }
 }
 
