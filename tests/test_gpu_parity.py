@@ -267,3 +267,55 @@ def test_fused_quantize_gemv_matches_quantize_then_dot(be, oracle, ty, rows, k):
     d = dev(dest0)
     be.gemv_f32(m, dev(x), d, None, coef=-0.75, accumulate=True)
     assert np.array_equal(host(d).view(np.uint32), want_acc.view(np.uint32))
+
+
+@pytest.mark.parametrize("ty,rows,k", [(Q4_K, 37, 256), (Q5_K, 129, 768), (Q4_K, 9, 16384), (Q5_K, 700, 4096),
+                                       (IQ2_S, 70, 16384), (IQ3_S, 513, 2304), (Q4_K, 8192, 4096),
+                                       (Q5_K, 8192, 4096), (IQ2_S, 9000, 4096), (IQ3_S, 4096, 8192)])
+def test_fused_quantize_gemv_every_launch_shape(be, oracle, ty, rows, k):
+    """The fused kernel quantizes x in every workgroup (K-quant types also into a
+    residue-major copy) and picks its workgroup size and lanes per unit from the
+    shape (512 threads at >= 2 * 64 * 4 units per CU): every choice, and a
+    workgroup cap that makes each wave walk many rows, gives the bits of
+    quantize_row_q8_k_into followed by the reference row dots."""
+    w = synth.random_matrix(ty, rows, k, 3 * rows + k + ty)
+    x = synth.random_activations(k, rows + k)
+    x[:256] *= 1e-3                       # a block with a different scale
+    q8_ref = oracle.quantize_q8_k(x)
+    want = oracle.gemv_prequantized(oracle.make_exec(oracle.MODE_CPU_PARALLEL_Q8K, 8, True),
+                                    oracle.make_matrix(ty, rows, k, w), q8_ref)
+    m = be.upload(ty, rows, k, w)
+    xd = dev(x)
+    try:
+        for lpu in (0, 1, 2, 4):
+            for cap in (0, 3):
+                be.set_tuning(be.TUNE_GEMV_LPU, lpu)
+                be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
+                y = torch.full((rows,), float("nan"), device="cuda")
+                q8 = torch.zeros(q8_ref.size, dtype=torch.uint8, device="cuda")
+                be.gemv_f32(m, xd, y, q8)
+                assert np.array_equal(host(q8), q8_ref), (lpu, cap)
+                got = host(y)
+                bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
+                assert bad.size == 0, (lpu, cap, bad.size, bad[:5])
+    finally:
+        be.set_tuning(be.TUNE_GEMV_LPU, 0)
+        be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, 0)
+
+
+def test_floor_reference_kernels(be):
+    """The roofline floor kernels (no reference counterpart): an empty launch and
+    plain reads of a matrix in every launch shape the bench sweeps; bad shapes
+    are refused with InvalidParameter."""
+    import lbhip
+    m = be.upload(IQ2_S, 1536, 4096, synth.random_matrix(IQ2_S, 1536, 4096, 5))
+    sink = torch.zeros(4 * 4096, dtype=torch.int32, device="cuda")
+    be.empty_kernel()
+    for unroll in (1, 2, 4, 8):
+        for grid in (1, 7, 492, 4096):
+            for slab in (False, True):
+                be.read_matrix(m, sink, grid, unroll, slab)
+    torch.cuda.synchronize()
+    for grid, unroll in ((0, 1), (be.READ_MAX_GRID + 1, 1), (4, 3), (4, 16)):
+        with pytest.raises(lbhip.KernelError, match="InvalidParameter"):
+            be.read_matrix(m, sink, grid, unroll)
