@@ -112,7 +112,8 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
         // single wave's LDS round trips is the dot's critical path).
         constexpr int GB = TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
         const float v =
-            row_dot<TY, LPU, GB>(w, act, on, L, s_grid, s_fold[wid], p.block_sums, (long long)r * NB + L.b);
+            row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8>(w, act, on, L, s_grid, s_fold[wid], p.block_sums,
+                                                          (long long)r * NB + L.b);
         if (on && L.leader()) store_y(p, r, v);
     };
 

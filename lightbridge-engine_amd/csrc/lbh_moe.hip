@@ -332,7 +332,7 @@ struct DownStream {
         auto process = [&](int i, const W &w) {
             const int r = r0 + i * L.rpw + L.slot;
             const bool on = L.lane_on && r < r1;
-            const float v = row_dot<TY, LPU>(w, act, on, L, s_grid, fold, nullptr, 0);
+            const float v = row_dot<TY, LPU, 0, Traits<TY>::KQ ? 16 : 8>(w, act, on, L, s_grid, fold, nullptr, 0);
             if (on && L.leader()) s_y[r - r0] = v;
         };
         while (it < items) {

@@ -18,29 +18,39 @@ struct FoldLDS {
     float chain[Traits<TY>::KQ ? 64 : 1][9];
 };
 
+// Chain of n <= W terms with every read issued first (clamped in-bounds
+// index), padded to W with +0.0 terms, which leave every partial sum
+// unchanged: a chain that starts at +0.0 never holds -0.0, and s - 0.0 == s
+// for all s.
+template <int W>
+__device__ __forceinline__ float fold_padded(const float *t, int n, bool subtract) {
+    float v[W], s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < W; ++i) {
+        const float x = t[i < n ? i : 0];
+        v[i] = i < n ? x : 0.0f;
+    }
+    if (subtract) {
+#pragma unroll
+        for (int i = 0; i < W; ++i) s = __fsub_rn(s, v[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < W; ++i) s = __fadd_rn(s, v[i]);
+    }
+    return s;
+}
+
 // Sequential f32 fold of n per-block terms, s = ((0 + t0) + t1) + ... (or
 // 0 - t0 - t1 ... for the minimum chain): the reference's block loop order.
-// For n <= 16 every read is issued first (clamped in-bounds index) and the
-// chain is padded with +0.0 terms, which leave every partial sum unchanged:
-// a chain that starts at +0.0 never holds -0.0, and s - 0.0 == s for all s.
+// Rows of up to 16 blocks use a padded chain; with FW = 8 rows of up to 8
+// blocks (K = 1536 rows have 6) take a chain of 8 (a shorter dependent-add
+// chain, at the registers of a second unrolled copy: kernels whose
+// occupancy sits at a register limit keep FW = 16).
+template <int FW = 16>
 __device__ __forceinline__ float fold_terms(const float *t, int n, bool subtract) {
+    if (FW == 8 && n <= 8) return fold_padded<8>(t, n, subtract);
+    if (n <= 16) return fold_padded<16>(t, n, subtract);
     float s = 0.0f;
-    if (n <= 16) {
-        float v[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float x = t[i < n ? i : 0];
-            v[i] = i < n ? x : 0.0f;
-        }
-        if (subtract) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s = __fsub_rn(s, v[i]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s = __fadd_rn(s, v[i]);
-        }
-        return s;
-    }
     for (int i = 0; i < n; ++i) s = subtract ? __fsub_rn(s, t[i]) : __fadd_rn(s, t[i]);
     return s;
 }
@@ -69,9 +79,9 @@ using WOf = typename std::conditional<Traits<TY>::KQ, WSliceKQ<TY, LPU>, WSlice<
 // Integer stage + fold of one wave step.  `on` marks lanes whose row exists;
 // the row value is returned in the row's leader lane (part 0, block 0).
 // block_sums (optional) receives the integer stage of unit u.  GB: codebook
-// lookups gathered per GB groups (slice_sum).  Contains wave barriers: every
-// lane of the wave must call it.
-template <int TY, int LPU, int GB = 0>
+// lookups gathered per GB groups (slice_sum); FW: fold_terms.  Contains wave
+// barriers: every lane of the wave must call it.
+template <int TY, int LPU, int GB = 0, int FW = 16>
 __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, LPU> &act, bool on,
                                          const LaneMap<LPU> &L, const void *grid, FoldLDS<TY> &f,
                                          int32_t *block_sums, long long u) {
@@ -104,7 +114,7 @@ __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, 
         wave_sync();
         // Chains 0..7: sums[l] += term (q8_k.rs:316-318); chain 8: sum -= term (:319-320).
         if (on && L.part == 0)
-            for (int c = L.b; c < 9; c += L.nb) f.chain[L.slot][c] = fold_terms(&f.terms[c][L.slot * L.nb], L.nb, c == 8);
+            for (int c = L.b; c < 9; c += L.nb) f.chain[L.slot][c] = fold_terms<FW>(&f.terms[c][L.slot * L.nb], L.nb, c == 8);
         wave_sync();
         if (on && L.leader()) {
             float s = f.chain[L.slot][8];
@@ -126,7 +136,7 @@ __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, 
         }
         wave_sync();
         if (on && L.leader()) {
-            float s = fold_terms(&f.terms[0][L.slot * L.nb], L.nb, false);
+            float s = fold_terms<FW>(&f.terms[0][L.slot * L.nb], L.nb, false);
             if (TY == T_IQ2_S) s = __fmul_rn(0.125f, s);  // q8_k.rs:369
             result = s;
         }
