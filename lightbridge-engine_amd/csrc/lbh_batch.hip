@@ -850,24 +850,28 @@ struct MxStep {
     float d8;
 };
 
-// LDS of a matrix-core stream workgroup: the tables, then per tile the
-// per-block f32 terms [matrix][block][token][row].
+// LDS of a matrix-core stream workgroup: the tables, then (split > 1) per
+// tile the per-block f32 terms [matrix][block][token][row].
 __host__ __device__ constexpr int mx_lds_bytes(int ty, int nm, int split, int nb) {
-    return (ty == T_IQ2_S ? MxTab<T_IQ2_S>::BYTES : MxTab<T_IQ3_S>::BYTES) + (MX_WAVES / split) * nm * nb * 256 * 4;
+    return (ty == T_IQ2_S ? MxTab<T_IQ2_S>::BYTES : MxTab<T_IQ3_S>::BYTES) +
+           (split > 1 ? (MX_WAVES / split) * nm * nb * 256 * 4 : 0);
 }
 
 // Rows [r0, r1) (r1 - r0 <= 16 * MX_WAVES / S) of NM matrices (K = 256 nb)
 // against the chunk's tokens.  The workgroup holds MX_WAVES / S tiles of 16
 // rows; the S waves of a tile take its blocks j, j + S, ...: together they
 // read S consecutive blocks of each row (adjacent 16-byte pieces of the same
-// lines) per step.  Each wave writes the f32 term (d * d8) * (float)bsum of
-// each (row, token, block) it computes to LDS; after a workgroup barrier one
-// thread per (tile, token, row) folds its terms in block order (lbh_rows.h:
-// chain = 0 + t_0 + t_1 + ...; IQ2_S result = 0.125 * chain) and calls
-// out(token column, row, values).  Lane l's token column holds the operand
-// row bq / bd.  The first step's loads are issued before `prologue` (table
-// fill, ended by a workgroup barrier); then each step's loads are in flight
-// while the one before is computed.
+// lines) per step.  With S > 1 each wave writes the f32 term
+// (d * d8) * (float)bsum of each (row, token, block) it computes to LDS;
+// after a workgroup barrier one thread per (tile, token, row) folds its terms
+// in block order (lbh_rows.h: chain = 0 + t_0 + t_1 + ...; IQ2_S result =
+// 0.125 * chain) and calls out(token column, row, values).  With S = 1 the
+// wave computes every block of its tile in order and each lane keeps the
+// chains of its four (row, token) results in registers (no term table, so
+// the workgroup's LDS is the tables alone).  Lane l's token column holds the
+// operand row bq / bd.  The first step's loads are issued before `prologue`
+// (table fill, ended by a workgroup barrier); then each step's loads are in
+// flight while the one before is computed.
 template <int TY, int NM, int S, class Prologue, class Out>
 __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1, int nb, const uint8_t *bq,
                                          const float *bd, const uint8_t *tab, float *terms, Prologue prologue, Out out) {
@@ -901,6 +905,11 @@ __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1
         st.d8 = bd[b];
     };
     float *tt = terms + tl * NM * nb * 256;
+    float chain[NM][4];   // S == 1: result i of the lane is (row 4q + i, token c)
+#pragma unroll
+    for (int t = 0; t < NM; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) chain[t][i] = 0.0f;
     auto process = [&](int s, const MxStep<TY, NM> &st) {
         constexpr int CH = mx_chain<TY>();
         const int b = j + S * s;
@@ -933,7 +942,11 @@ __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float dr = __shfl(da, 4 * q + i, 64);
-                o[i] = __fmul_rn(__fmul_rn(dr, st.d8), (float)bs[t][i]);
+                const float term = __fmul_rn(__fmul_rn(dr, st.d8), (float)bs[t][i]);
+                if constexpr (S == 1)
+                    chain[t][i] = __fadd_rn(chain[t][i], term);   // blocks in order
+                else
+                    o[i] = term;
             }
         }
     };
@@ -946,6 +959,17 @@ __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1
         if (s + 1 >= steps) break;
         issue(s + 2, sa);
         process(s + 1, sb);
+    }
+    if constexpr (S == 1) {
+        if (rt0 >= r1) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float res[NM];
+#pragma unroll
+            for (int t = 0; t < NM; ++t) res[t] = TY == T_IQ2_S ? __fmul_rn(0.125f, chain[t][i]) : chain[t][i];  // q8_k.rs:369
+            out(c, rt0 + 4 * q + i, res);
+        }
+        return;
     }
     __syncthreads();
     for (int p = threadIdx.x; p < (MX_WAVES / S) * 256; p += MX_THREADS) {
