@@ -904,7 +904,7 @@ __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1
         for (int k = 0; k < 4; ++k) st.bq[k] = src[k];
         st.d8 = bd[b];
     };
-    float *tt = terms + tl * NM * nb * 256;
+    float *tt = S > 1 ? terms + tl * NM * nb * 256 : terms;   // S == 1: no term table
     float chain[NM][4];   // S == 1: result i of the lane is (row 4q + i, token c)
 #pragma unroll
     for (int t = 0; t < NM; ++t)
