@@ -107,6 +107,25 @@ class Timer:
             e1.synchronize()
         return e0.elapsed_time(e1) * 1e-3   # seconds
 
+    def spread(self, g, replays, per):
+        """Median, p10 and p90 in us per unit over `replays` replays, each bracketed by its own
+        event pair on the stream (one replay = `per` units: steps, launches or tokens)."""
+        torch, s = self.torch, self.stream
+        with torch.cuda.stream(s):
+            g.replay()
+            s.synchronize()
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(replays)]
+            for a, b in ev:
+                a.record(s)
+                g.replay()
+                b.record(s)
+            ev[-1][1].synchronize()
+        us = sorted(a.elapsed_time(b) * 1e3 / per for a, b in ev)
+        q = lambda f: us[min(len(us) - 1, int(round(f * (len(us) - 1))))]  # noqa: E731
+        return {"median_us": round(q(0.5), 3), "p10_us": round(q(0.1), 3), "p90_us": round(q(0.9), 3),
+                "replays": replays, "units_per_replay": per}
+
 
 def logical_cpus():
     """Logical CPUs this process may run on (the box's share, not the machine's count)."""
@@ -290,11 +309,13 @@ def bench_matvec_step(args, be, timer, torch, np, synth):
     t = timer.time(g, reps)
     steps = reps * copies
     ms_per_step = t / steps * 1e3
+    step_spread = timer.spread(g, 100, copies)
     g_gate = timer.graph(lambda: [be.gemv_f32(gates[c], xs[c], hs[c]) for c in range(copies)])
     g_down = timer.graph(lambda: [be.gemv_f32(downs[c], hs[c], ys[c]) for c in range(copies)])
     n_k = max(1, 2000 // copies)
     gate_us = timer.time(g_gate, n_k) / (n_k * copies) * 1e6
     down_us = timer.time(g_down, n_k) / (n_k * copies) * 1e6
+    kernel_spread = {"iq2s_gate": timer.spread(g_gate, 100, copies), "iq3s_down": timer.spread(g_down, 100, copies)}
     del g, g_gate, g_down
     empty_us = empty_kernel_us(be, timer)
     gate_floor = read_floor_us(be, timer, torch, gates, w_gate.nbytes)
@@ -307,7 +328,7 @@ def bench_matvec_step(args, be, timer, torch, np, synth):
         m.close()
     return dict(w_gate=w_gate, w_down=w_down, copies=copies, steps=steps, warmup=reps_w * copies,
                 ms_per_step=ms_per_step, gate_us=gate_us, down_us=down_us, check=check, empty_us=empty_us,
-                gate_floor=gate_floor, down_floor=down_floor)
+                gate_floor=gate_floor, down_floor=down_floor, step_spread=step_spread, kernel_spread=kernel_spread)
 
 
 def bench_q4k(args, be, timer, torch, np, synth):
@@ -322,13 +343,15 @@ def bench_q4k(args, be, timer, torch, np, synth):
     timer.time(g, 3)
     reps = max(3, 1000 // copies)
     us = timer.time(g, reps) / (reps * copies) * 1e6
+    spread = timer.spread(g, 100, copies)
     del g
     floors = floor_fields(us, empty_kernel_us(be, timer), read_floor_us(be, timer, torch, ms, w.nbytes))
     for m in ms:
         m.close()
     return w, {"workload": "configs[0]: Q4_K x Q8_K matvec 4096x4096, batch 1 (fused Q8_K + matvec kernel)",
                "us_per_matvec": round(us, 3), "GB/s": round(Q4K_BYTES / us / 1e3, 2),
-               "roofline_frac": round(Q4K_BYTES / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies, **floors}
+               "roofline_frac": round(Q4K_BYTES / us / 1e3 / HBM_PEAK_GBS, 4), "weight_copies": copies,
+               "per_replay_spread": spread, **floors}
 
 
 # Decode matvecs of the Hy3 model's own tensors (crates/bridge-model-hy3/src/schema.rs:96-201,
@@ -395,6 +418,7 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
     g_dev = timer.graph(lambda: [lbhip.moe_block_forward(be, moe, router, xs[i], ys[i], TOP_K) for i in range(T)])
     timer.time(g_dev, 1)
     us_dev = timer.time(g_dev, reps) / (reps * T) * 1e6
+    spread_host, spread_dev = timer.spread(g_host, 11, T), timer.spread(g_dev, 11, T)
 
     torch.cuda.synchronize()
     host = lambda t: t.cpu().numpy()  # noqa: E731
@@ -402,9 +426,11 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
                        "4096x1536), top-8 softmax of an F32 4096x192 router, Q4_K/Q5_K shared expert ffn 4096",
            "tokens_timed": T * reps, "distinct_experts_hit": hit,
            "routing_given": {"us_per_token": round(us_host, 2), "tokens_per_s": round(1e6 / us_host, 1),
-                             "GB/s": round((MOE_WEIGHT_BYTES - N_EXPERTS * HIDDEN * 4) / us_host / 1e3, 1)},
+                             "GB/s": round((MOE_WEIGHT_BYTES - N_EXPERTS * HIDDEN * 4) / us_host / 1e3, 1),
+                             "per_replay_spread": spread_host},
            "with_device_router": {"us_per_token": round(us_dev, 2), "tokens_per_s": round(1e6 / us_dev, 1),
-                                  "GB/s": round(MOE_WEIGHT_BYTES / us_dev / 1e3, 1)},
+                                  "GB/s": round(MOE_WEIGHT_BYTES / us_dev / 1e3, 1),
+                                  "per_replay_spread": spread_dev},
            "algorithmic_weight_bytes_per_token": MOE_WEIGHT_BYTES}
     state = dict(experts_np=experts_np, shared_np=shared_np, router_w=router_w, xs_np=xs_np,
                  last_y=host(ys[T - 1]), moe=moe, router=router, experts=experts, shared=shared)
@@ -434,6 +460,7 @@ def bench_batch(args, be, timer, torch, np, synth, state):
     timer.time(g, 2)
     reps = max(2, args.batch_reps)
     us = timer.time(g, reps) / (reps * R) * 1e6
+    spread = timer.spread(g, 20, R)
     torch.cuda.synchronize()
     ids_h = ids.cpu().numpy().view(np.uint32)
     hits = [len(np.unique(ids_h[r])) for r in range(R)]
@@ -442,7 +469,7 @@ def bench_batch(args, be, timer, torch, np, synth, state):
     res = {"workload": "configs[3]: batched decode, 64 tokens: the configs[2] MoE block, per-token top-8 of seeded "
                        "Zipf(s=1.1) router logits (softmax top-8 on the device), token-by-expert sort, grouped "
                        "per-expert gate/up + SwiGLU + down, ordered combine",
-           "tokens_per_step": T, "steps_timed": reps * R, "us_per_step": round(us, 2),
+           "tokens_per_step": T, "steps_timed": reps * R, "us_per_step": round(us, 2), "per_replay_spread": spread,
            "tokens_per_s": round(T / us * 1e6, 1),
            "distinct_experts_hit_per_step": hits,
            "algorithmic_bytes_per_step": int(bytes_step),
@@ -646,12 +673,13 @@ def bench_prefill(args, be, timer, torch, np, synth):
     timer.time(g, 2)
     reps = 10
     us = timer.time(g, reps) / (reps * copies) * 1e6
+    spread = timer.spread(g, 50, copies)
     torch.cuda.synchronize()
     tops = PF_OPS / us / 1e6
     res = {"workload": "configs[4]: prefill 512 tokens, Q8_K activations [512 x 4096] x Q5_K [12288 x 4096] -> f32 "
                        "[512 x 12288], f16 MFMA (v_mfma_f32_32x32x16_f16) on integer operands: exact "
                        "per-(block, lane residue) sums",
-           "us_per_step": round(us, 2), "dot_TOPS": round(tops, 2),
+           "us_per_step": round(us, 2), "per_replay_spread": spread, "dot_TOPS": round(tops, 2),
            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": MFMA_I8_PEAK_TOPS, "unit": "TOP/s",
                         "frac": round(tops / MFMA_I8_PEAK_TOPS, 4), "traffic": MEASURED_TRAFFIC["prefill"],
                         "peak_note": "priced on the dense int8 peak (5.0 POP/s) of the integer contraction; the "
@@ -838,6 +866,10 @@ def main():
                      "avg_launch_us": round(dom[1], 3), "algorithmic_bytes_per_launch": dom[2],
                      **floor_fields(dom[1], mv["empty_us"], dom[4])},
         "kernels_us": {"iq2s_gate": round(mv["gate_us"], 3), "iq3s_down": round(mv["down_us"], 3)},
+        "timing": {"what": "value, ms_per_step and kernels_us are totals over back-to-back HIP-graph replays "
+                           "(one event pair around all of them); the spreads time each replay with its own "
+                           "event pair and give median / p10 / p90 per step or per launch",
+                   "step": mv["step_spread"], **mv["kernel_spread"]},
         "floors": {"what": "launch floor (an empty kernel) and memory floor (the fastest plain read of the same "
                            "weight bytes over a sweep of launch shapes, same rotation of copies) per kernel of the "
                            "step; frac_of_floor = floor / measured",
