@@ -386,7 +386,8 @@ __device__ __forceinline__ void stage_q8(uint8_t *s_act, int n, int nb, Src src_
     }
 }
 
-// LDS layout of a stream workgroup: [staged activations][codebook][fold tables].
+// LDS of a stream workgroup: the codebook (a static array, static_grid), then,
+// dynamic, [staged activations][fold tables].
 template <int TY, int NM>
 __host__ __device__ constexpr int stream_lds(int tc, int nb, int lpu) {
     return al16(tc * nb * Q8L) + al16(GridLDS<TY>::BYTES) + MB_WAVES * 4 * wave_fold_floats<TY, NM>(rows_per_step(lpu, nb), nb);
@@ -555,8 +556,8 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
     const int nb = a.hidden / 256;
     constexpr int LPU = mb_lpu<TY>();
     uint8_t *s_act = smem;
-    uint8_t *grid = smem + al16(valu_cap(a, TY) * nb * Q8L);
-    float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
+    uint8_t *grid = static_grid<TY>();
+    float *fold = reinterpret_cast<float *>(smem + al16(valu_cap(a, TY) * nb * Q8L));
     if constexpr (SHARED) {
         const int tiles = (a.ffn_s + a.rt_gu_s - 1) / a.rt_gu_s;
         const int c = blockIdx.x / tiles, tile = blockIdx.x - c * tiles;
@@ -657,8 +658,8 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
         const int n = a.n_tokens - t0 < a.tc ? a.n_tokens - t0 : a.tc;
         if (mx_takes<TY>(a, n)) return;
         const int r0 = tile * a.rt_d_s, r1 = r0 + a.rt_d_s < a.hidden ? r0 + a.rt_d_s : a.hidden;
-        uint8_t *grid = smem + al16(valu_cap(a, TY) * nb * Q8L);
-        float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
+        uint8_t *grid = static_grid<TY>();
+        float *fold = reinterpret_cast<float *>(smem + al16(valu_cap(a, TY) * nb * Q8L));
         const MatView mv[1] = {a.shared.down};
         batch_rows<TY, LPU, 1>(
             mv, r0, r1, s_act, n, grid, fold,
@@ -676,8 +677,8 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
         const int e = a.chunk_expert[c], p0 = a.chunk_p0[c], n = a.chunk_n[c];
         if (mx_takes<TY>(a, n)) return;
         const int r0 = tile * a.rt_d_r, r1 = r0 + a.rt_d_r < a.hidden ? r0 + a.rt_d_r : a.hidden;
-        uint8_t *grid = smem + al16(valu_cap(a, TY) * nb * Q8L);
-        float *fold = reinterpret_cast<float *>(grid + al16(GridLDS<TY>::BYTES));
+        uint8_t *grid = static_grid<TY>();
+        float *fold = reinterpret_cast<float *>(smem + al16(valu_cap(a, TY) * nb * Q8L));
         const MatView mv[1] = {a.experts[e].down};
         batch_rows<TY, LPU, 1>(
             mv, r0, r1, s_act, n, grid, fold,
@@ -1152,8 +1153,11 @@ static hipError_t allow_lds(K kernel, int lds) {
     return hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
 }
 
+// lds: the stage's LDS footprint; the VALU kernels hold the codebook
+// statically, the rest is dynamic.
 template <int TY, bool SHARED>
 static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
+    lds -= al16(GridLDS<TY>::BYTES);
     hipError_t e = allow_lds(k_mb_gate_up<TY, SHARED>, lds);
     if (e != hipSuccess) return e;
     const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.ffn_s, a.rt_gu_s) : a.max_chunks * cdiv(a.ffn_r, a.rt_gu_r);
@@ -1163,6 +1167,7 @@ static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
 
 template <int TY, bool SHARED>
 static hipError_t down_typed(const BatchArgs &a, int lds, hipStream_t s) {
+    lds -= al16(GridLDS<TY>::BYTES);
     hipError_t e = allow_lds(k_mb_down<TY, SHARED>, lds);
     if (e != hipSuccess) return e;
     const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.hidden, a.rt_d_s) : a.max_chunks * cdiv(a.hidden, a.rt_d_r);

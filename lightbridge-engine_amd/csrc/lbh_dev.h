@@ -494,6 +494,16 @@ __device__ __forceinline__ void fill_grid(void *lds) {
     }
 }
 
+// The LDS codebook of TY as a static array of the kernel that inlines this:
+// its address is fixed when the kernel is compiled, so every lookup folds it
+// into the ds_read offset field (a table in dynamic LDS costs an address add
+// per lookup).  Kernels that also use dynamic LDS get it after this array.
+template <int TY>
+__device__ __forceinline__ uint8_t *static_grid() {
+    __shared__ __align__(16) uint8_t g[GridLDS<TY>::BYTES > 0 ? GridLDS<TY>::BYTES : 16];
+    return g;
+}
+
 // ------------------------------------------------------------ weight slices
 //
 // The bytes one lane needs from its unit, loaded from the device layout

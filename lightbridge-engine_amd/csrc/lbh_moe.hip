@@ -83,11 +83,11 @@ struct PendingRows {
     int32_t tag[SWIGLU_BATCH];   // scratch slot | (expert order << 8)
 };
 
-// LDS bytes of one gate/up workgroup of type TY.
+// Dynamic LDS bytes of one gate/up workgroup of type TY (the codebook is a
+// static array, static_grid).
 template <int TY>
 __host__ __device__ constexpr int gate_up_lds(int nb) {
-    return align16(GridLDS<TY>::BYTES) + align16(nb * 292) + MOE_WAVES * (int)sizeof(FoldLDS<TY>) +
-           MOE_WAVES * (int)sizeof(PendingRows);
+    return align16(nb * 292) + MOE_WAVES * (int)sizeof(FoldLDS<TY>) + MOE_WAVES * (int)sizeof(PendingRows);
 }
 
 // h = SwiGLU(gate, up) (activation.rs:170-178) of a wave's n pending rows, one
@@ -115,8 +115,8 @@ __device__ __forceinline__ void gate_up_stream(const MoeArgs &a, const SlotOf &s
                                                int first_wave, int nwaves, uint8_t *smem) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
     const int NB = a.hidden / 256;
-    uint8_t *s_grid = smem;
-    uint8_t *s_q8 = smem + align16(GridLDS<TY>::BYTES);
+    uint8_t *s_grid = static_grid<TY>();
+    uint8_t *s_q8 = smem;
     FoldLDS<TY> *s_fold = reinterpret_cast<FoldLDS<TY> *>(s_q8 + align16(NB * 292));
     PendingRows &pend = reinterpret_cast<PendingRows *>(s_fold + MOE_WAVES)[wid];
 
@@ -378,9 +378,9 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
     const int r0 = blockIdx.x * a.tile_d;
     const int r1 = r0 + a.tile_d < a.hidden ? r0 + a.tile_d : a.hidden;
-    uint8_t *s_grid_r = smem;
-    uint8_t *s_grid_s = smem + align16(GridLDS<TYR>::BYTES);
-    uint8_t *s_foldp = s_grid_s + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES);
+    uint8_t *s_grid_r = static_grid<TYR>();
+    uint8_t *s_grid_s = static_grid<TYS>();
+    uint8_t *s_foldp = smem;
     const int nw = blockDim.x >> 6;
     float *s_y = reinterpret_cast<float *>(s_foldp + nw * down_fold_bytes<TYR, TYS>());
     uint8_t *s_q8 = reinterpret_cast<uint8_t *>(s_y + (MOE_MAX_ROUTED + 1) * a.tile_d);   // [n * nbr + nbs] blocks
@@ -543,17 +543,22 @@ static hipError_t gate_up_typed(const MoeArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Dynamic LDS of a down launch over n routed experts: the codebooks, one fold
-// table per wave, the per-row down outputs of every expert and the Q8_K of
-// every expert's h.
+// Static LDS of a down launch: the codebooks (static_grid).
+template <int TYR, int TYS>
+constexpr int down_grid_lds() {
+    return align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES);
+}
+
+// LDS of a down launch over n routed experts: the codebooks (static), then,
+// dynamic, one fold table per wave, the per-row down outputs of every expert
+// and the Q8_K of every expert's h.
 template <int TYR, int TYS>
 static int down_lds(int n, int has_shared, int ffn_r, int ffn_s, int tile_d) {
     // (has_shared: the shared expert's down runs in this launch)
     const int waves = n + (has_shared ? DOWN_SHARED_WAVES : 0);
     const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
     const int q8 = (n * (ffn_r / 256) + (has_shared ? ffn_s / 256 : 0)) * 292;
-    return align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES) +
-           nw * down_fold_bytes<TYR, TYS>() + (MOE_MAX_ROUTED + 1) * tile_d * 4 + align16(q8);
+    return down_grid_lds<TYR, TYS>() + nw * down_fold_bytes<TYR, TYS>() + (MOE_MAX_ROUTED + 1) * tile_d * 4 + align16(q8);
 }
 
 template <int TYR, int TYS>
@@ -564,13 +569,14 @@ static hipError_t down_typed(const MoeArgs &a, hipStream_t s) {
     const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
     const int lds = down_lds<TYR, TYS>(n, shared_here, a.ffn_r, a.ffn_s, a.tile_d);
     if (lds > MOE_MAX_LDS) return hipErrorInvalidValue;
+    const int dyn = lds - down_grid_lds<TYR, TYS>();
     auto kernel = k_moe_down<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>;
-    if (lds > 64 * 1024) {
+    if (dyn > 64 * 1024) {
         const hipError_t e =
-            hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+            hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kernel, dim3(cdiv(a.hidden, a.tile_d)), dim3(64 * nw), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(cdiv(a.hidden, a.tile_d)), dim3(64 * nw), dyn, s, a);
     return hipGetLastError();
 }
 
