@@ -30,6 +30,22 @@ constexpr int MOE_WAVES = MOE_THREADS / 64;
 __host__ __device__ constexpr int align16(int v) { return (v + 15) & ~15; }
 
 __device__ __forceinline__ int route_n(const MoeArgs &a) { return a.route_dev ? a.route_dev->n : a.route.n; }
+// A wave-uniform read of memory that no wave of the running kernel writes,
+// through the constant address space: a scalar load.  (Through a generic
+// pointer it is a vector load, and the wait for it drains every load the
+// wave has in flight.)
+template <class T>
+__device__ __forceinline__ T scalar_read(const T *p) {
+    static_assert(sizeof(T) % 4 == 0, "whole words");
+    T v;
+    uint32_t *d = reinterpret_cast<uint32_t *>(&v);
+    const __attribute__((address_space(4))) uint32_t *w = (const __attribute__((address_space(4))) uint32_t *)p;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(T) / 4); ++i) d[i] = w[i];
+    return v;
+}
+// Stands in for absent status words (no non-finite value recorded).
+__device__ const unsigned long long k_no_status[2] = {~0ull, ~0ull};
 __device__ __forceinline__ uint32_t route_id(const MoeArgs &a, int s) {
     return a.route_dev ? a.route_dev->ids[s] : a.route.ids[s];
 }
@@ -62,7 +78,12 @@ __device__ __forceinline__ MatView uniform_view(const MatView &v) {
 // segment), else from the device table.
 __device__ __forceinline__ ExpertDev routed_view(const MoeArgs &a, int s) {
     const int su = __builtin_amdgcn_readfirstlane(s);
-    if (!a.routed_given) return a.experts[__builtin_amdgcn_readfirstlane((int)route_id(a, su))];
+    if (!a.routed_given) {
+        // Device route (read only by launches that do not write it) and the
+        // expert table: scalar loads.
+        const uint32_t id = a.route_dev ? scalar_read(&a.route_dev->ids[su]) : a.route.ids[su];
+        return scalar_read(&a.experts[__builtin_amdgcn_readfirstlane((int)id)]);
+    }
     ExpertDev v = a.routed_shape;
     v.gate.planes = a.routed_planes[su][0];
     v.up.planes = a.routed_planes[su][1];
@@ -367,12 +388,16 @@ constexpr int DOWN_MAX_WAVES = 12;
 template <int TYR, int LPUR, int TYS, int LPUS>
 __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    if (a.status && (a.status->first_bad_input != ~0ull || a.status->first_bad_swiglu != ~0ull)) return;
-    if (a.route_dev && a.route_dev->n < 0) return;   // invalid device route: y unchanged
+    // The device route count is a scalar read (an unconditional load from a
+    // selected address: a load inside a branch is waited for inside it); the
+    // status words are read once the prologue's loads are out and acted on
+    // after it (a non-finite input or SwiGLU, or an invalid device route,
+    // leaves y unchanged), so no wait for them holds back a prologue load.
+    const int route_count = scalar_read(a.route_dev ? &a.route_dev->n : &a.route.n);
     // Wave index and route count through readfirstlane: the task choice below
     // (and every descriptor derived from it) is wave-uniform.
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n = a.down_part == 2 ? 0 : __builtin_amdgcn_readfirstlane(route_n(a));
+    const int n = a.down_part == 2 || route_count < 0 ? 0 : __builtin_amdgcn_readfirstlane(route_count);
     // The shared expert's down runs here unless another launch writes it to d_shared (part 1).
     const bool shared_here = a.has_shared && a.down_part != 1;
     const int nbr = a.ffn_r / 256, nbs = a.ffn_s / 256;
@@ -387,17 +412,18 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
 
     // Q8_K of every expert's h into LDS (quantize_row_q8_k_into of the down
     // projection's input, gemv.rs:161-163): chunks of up to four blocks of one
-    // slot.  Load order: the codebooks and the h of the wave's first two
-    // chunks, then the first weight step of the wave's first task (routed
-    // expert `wid`, or its part of the shared expert), then the LDS stores.
-    // Vector loads retire in order, so the quantization waits only for the
-    // small h and codebook loads, and the weights' HBM round trip overlaps it.
-    // The second chunk's index is clamped (an in-range reload) so the loads
-    // are unconditional.
+    // slot.  Order: the codebooks and the h of the wave's first two chunks,
+    // a wait for them, the first weight step of the wave's first task
+    // (routed expert `wid`, or its part of the shared expert), then the LDS
+    // stores and the quantization, which overlap that step's HBM round trip.
+    // A wave's first two chunks (wid, wid + nw) are straight-line code, their
+    // indices clamped (an in-range reload), so no wait separates their loads;
+    // chunks past 2 nw (more than eight routed experts) follow one at a time.
     const int tasks = n + (shared_here ? DOWN_SHARED_WAVES : 0);
     const bool first_routed = wid < n, first_shared = !first_routed && wid < tasks;
     DownStream<TYR, LPUR> d_r;
     DownStream<TYS, LPUS> d_s;
+    unsigned long long bad_input, bad_swiglu;
     {
         const GridIn<TYR> gin_r = grid_load<TYR>();
         const GridIn<TYS> gin_s = grid_load<TYS>();
@@ -417,38 +443,39 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
                 nbl = nbs;
             }
         };
-        bool first = true;
-        for (int c = wid; chunks > 0 && (c < chunks || first); c += 2 * nw) {
-            const int cc = c < chunks ? c : chunks - 1, c1 = c + nw;
-            const float *x0, *x1;
-            uint8_t *o0, *o1;
-            int b0, b1, n0, n1;
-            chunk(cc, x0, o0, b0, n0);
-            chunk(c1 < chunks ? c1 : cc, x1, o1, b1, n1);
-            const QuantIn q0 = quantize_load(x0, b0, n0);
-            const QuantIn q1 = quantize_load(x1, b1, n1);
-            if (first) {
-                if (first_routed)
-                    d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
-                else if (first_shared)
-                    d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
-                grid_store<TYR>(gin_r, s_grid_r);
-                if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
-                first = false;
-            }
-            if (c < chunks) quantize_store(q0, o0);
-            if (c1 < chunks) quantize_store(q1, o1);
-        }
-        if (first) {   // no h to quantize (never at the supported shapes)
-            if (first_routed)
-                d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
-            else if (first_shared)
-                d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
-            grid_store<TYR>(gin_r, s_grid_r);
-            if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
+        const int last = chunks > 0 ? chunks - 1 : 0;
+        const float *x0, *x1;
+        uint8_t *o0, *o1;
+        int b0, b1, n0, n1;
+        chunk(wid < last ? wid : last, x0, o0, b0, n0);
+        chunk(wid + nw < last ? wid + nw : last, x1, o1, b1, n1);
+        const QuantIn q0 = quantize_load(x0, b0, chunks > 0 ? n0 : 0);
+        const QuantIn q1 = quantize_load(x1, b1, chunks > 0 ? n1 : 0);
+        // vmcnt(0): the codebook and h land before the first weight step goes
+        // out.  The weight loads differ by wave role, so a store that waited
+        // for an older load behind them would wait for all of them; this way
+        // the quantization runs while the weights are in flight.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        if (first_routed)
+            d_r.start(routed_view(a, wid).down, nbr, r0, r1, 0, 1);
+        else if (first_shared)
+            d_s.start(a.shared.down, nbs, r0, r1, wid - n, DOWN_SHARED_WAVES);
+        bad_input = scalar_read(a.status ? &a.status->first_bad_input : &k_no_status[0]);
+        bad_swiglu = scalar_read(a.status ? &a.status->first_bad_swiglu : &k_no_status[1]);
+        grid_store<TYR>(gin_r, s_grid_r);
+        if (TYS != TYR) grid_store<TYS>(gin_s, s_grid_s);
+        if (wid < chunks) quantize_store(q0, o0);
+        if (wid + nw < chunks) quantize_store(q1, o1);
+        for (int c = wid + 2 * nw; c < chunks; c += nw) {
+            const float *x;
+            uint8_t *o;
+            int b, nbl;
+            chunk(c, x, o, b, nbl);
+            quantize_store(quantize_load(x, b, nbl), o);
         }
     }
     __syncthreads();
+    if (bad_input != ~0ull || bad_swiglu != ~0ull || (a.route_dev && route_count < 0)) return;
 
     // Tasks: routed experts 0..n-1, then DOWN_SHARED_WAVES interleaved parts of
     // the shared expert; wave w takes tasks w, w + nw, ... (the first one
