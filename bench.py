@@ -57,7 +57,7 @@ BATCH_TOKENS = 64
 # HBM bytes per launch (read + write) measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain copy of
 # known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2384065 + 6144, "down": 2988466 + 19648, "prefill": 325221276 + 25165824}
+MEASURED_TRAFFIC = {"gate": 2384009 + 6144, "down": 2988392 + 19648, "prefill": 325213737 + 25165824}
 
 
 def parse():
