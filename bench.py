@@ -545,7 +545,8 @@ def bench_streaming(args, be, torch, np, synth, lbhip, state):
 
 
 def bench_ingest(args, be, torch, np, synth, lbhip):
-    """GGUF payload ingestion straight to HBM (SURVEY 8(f) row 4's path): the
+    """GGUF payload ingestion straight to HBM (crates/bridge-gguf/src/reader.rs:194-341 locates the
+    tensor; the bytes go to the device without a whole-file host copy): the
     Hy3 output head (Q5_K 120832x4096, 340 MB) in a GGUF file (page cache),
     located by the directory reader and streamed through pinned 32 MiB chunks
     with lbh_matrix_create_streamed, against lbh_matrix_create from host memory."""
