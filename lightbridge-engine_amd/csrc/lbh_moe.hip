@@ -576,14 +576,23 @@ constexpr int down_grid_lds() {
     return align16(GridLDS<TYR>::BYTES) + align16(TYS == TYR ? 0 : GridLDS<TYS>::BYTES);
 }
 
+// Waves of a down workgroup: one per routed expert, DOWN_SHARED_WAVES for the
+// shared expert when its down runs in the launch, at most DOWN_MAX_WAVES and
+// at least four, because grid_load spreads a codebook over the first 256
+// threads of the workgroup (waves past the task count take part in the
+// prologue only).
+static int down_waves(int n, int has_shared) {
+    const int waves = n + (has_shared ? DOWN_SHARED_WAVES : 0);
+    return waves < 4 ? 4 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
+}
+
 // LDS of a down launch over n routed experts: the codebooks (static), then,
 // dynamic, one fold table per wave, the per-row down outputs of every expert
 // and the Q8_K of every expert's h.
 template <int TYR, int TYS>
 static int down_lds(int n, int has_shared, int ffn_r, int ffn_s, int tile_d) {
     // (has_shared: the shared expert's down runs in this launch)
-    const int waves = n + (has_shared ? DOWN_SHARED_WAVES : 0);
-    const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
+    const int nw = down_waves(n, has_shared);
     const int q8 = (n * (ffn_r / 256) + (has_shared ? ffn_s / 256 : 0)) * 292;
     return down_grid_lds<TYR, TYS>() + nw * down_fold_bytes<TYR, TYS>() + (MOE_MAX_ROUTED + 1) * tile_d * 4 + align16(q8);
 }
@@ -592,8 +601,7 @@ template <int TYR, int TYS>
 static hipError_t down_typed(const MoeArgs &a, hipStream_t s) {
     const int n = a.down_part == 2 ? 0 : a.route_dev ? a.n_launch : a.route.n;
     const int shared_here = a.has_shared && a.down_part != 1;
-    const int waves = n + (shared_here ? DOWN_SHARED_WAVES : 0);
-    const int nw = waves < 1 ? 1 : waves > DOWN_MAX_WAVES ? DOWN_MAX_WAVES : waves;
+    const int nw = down_waves(n, shared_here);
     const int lds = down_lds<TYR, TYS>(n, shared_here, a.ffn_r, a.ffn_s, a.tile_d);
     if (lds > MOE_MAX_LDS) return hipErrorInvalidValue;
     const int dyn = lds - down_grid_lds<TYR, TYS>();

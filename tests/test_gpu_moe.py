@@ -97,6 +97,45 @@ def test_moe_config3_shapes_bit_exact_and_repeatable(be, oracle, config3):
         assert _same(host(y), want)
 
 
+@pytest.mark.parametrize("top_k", [1, 2, 3])
+def test_down_launches_of_fewer_than_four_routed_experts(be, oracle, small, top_k):
+    """A down launch whose workgroup would hold fewer than four waves (top-1..3 without
+    the shared expert's down in it: the routed launch of the two-stream schedule, or a
+    layer without a shared expert) still fills its whole codebook: the device codebook
+    loader spreads it over 256 threads.  The layer without a shared expert shares the
+    small layer's routed matrices and is checked against the oracle with an all-zero
+    shared expert (its down rows are +0.0, which leaves every accumulation unchanged)."""
+    rng = np.random.default_rng(40 + top_k)
+    ids = np.sort(rng.choice(6, size=top_k, replace=False)).astype(np.uint32)
+    coefs = rng.random(top_k).astype(np.float32)
+    x = rng.standard_normal(512).astype(np.float32)
+    want, err = small.oracle_out(oracle, ids, coefs, x)
+    assert err.status == 0
+    small.moe.set_streams(True)
+    try:
+        y = dev(np.zeros(512, np.float32))
+        be.moe_forward(small.moe, ids, coefs, dev(x), y)
+        assert _same(host(y), want), "two-stream schedule"
+    finally:
+        small.moe.set_streams(False)
+
+    zero = [np.zeros_like(m) for m in small.shared_np]
+    orc_zero = oracle.make_expert(oracle.make_matrix(Q4_K, 512, 512, zero[0]),
+                                  oracle.make_matrix(Q4_K, 512, 512, zero[1]),
+                                  oracle.make_matrix(Q5_K, 512, 512, zero[2]))
+    want0 = np.full(512, np.nan, np.float32)
+    ex = oracle.make_exec(oracle.MODE_CPU_PARALLEL_Q8K, 8, True)
+    err = oracle.moe_routed_by_id_status(ex, ids, coefs, small.orc_experts, orc_zero, x, want0)
+    assert err.status == 0
+    plain = be.moe_create(small._keep[0], None)
+    try:
+        y = dev(np.zeros(512, np.float32))
+        be.moe_forward(plain, ids, coefs, dev(x), y)
+        assert _same(host(y), want0), "no shared expert"
+    finally:
+        plain.close()
+
+
 @pytest.mark.parametrize("tiles", [(1, 1, 1), (7, 3, 7), (512, 512, 256), (300, 200, 20)])
 def test_moe_launch_shapes_give_the_same_bits(be, oracle, config3, tiles):
     rng = np.random.default_rng(sum(tiles))
