@@ -730,6 +730,7 @@ struct lbh_moe {
     MoeStatus *status;
     MoeStatus *status_host;
     int wg_r, wg_s, tile_d;   // gate/up workgroups (routed, shared stream); down rows per workgroup
+    int wg_s_given;           // shared-stream workgroups of the routing-given gate/up launch
     // Batched decode scratch (lbh_moe_reserve_batch): capacity and one allocation.
     size_t cap_tokens, cap_k;
     uint8_t *batch_mem;
@@ -807,7 +808,7 @@ MoeArgs moe_args(const lbh_moe *m, const float *x, float *y) {
     a.h = m->h;
     a.h_stride = m->h_stride;
     a.tiles_r = m->wg_r;
-    a.tiles_s = m->has_shared ? m->wg_s : 0;
+    a.tiles_s = m->has_shared ? m->wg_s_given : 0;
     a.tile_d = m->tile_d;
     a.stop_step = 0x7fffffff;
     a.type_gate_r = m->type_gate_r;
@@ -899,10 +900,14 @@ lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_exper
         m->shared.down = view_of(shared_down);
     }
     // Gate/up workgroups (measured on the configs[2] shapes): two per CU for
-    // the routed stream, and for the shared stream its byte share of two per
-    // CU (the top-8 routed gate/up against the shared gate/up).  More routed
-    // workgroups slow the device-router path, where every routed workgroup
-    // selects the route from the logits in its prologue.
+    // the routed stream.  The shared stream of the routing-given launch takes
+    // the rest of one round of resident workgroups (512 + 256 at three per
+    // CU: 34.1 us per token, against 35.4 with its byte share of two per CU
+    // and 37.5-38.0 once the grid spills into a second round).  Beside the
+    // router chains, and in the device-router path's selecting launch, which
+    // runs the routed stream on wg_r + wg_s workgroups, the byte share stays
+    // (55.7 us per token, 56.3 with a full round): every routed workgroup
+    // there selects the route from the logits in its prologue.
     {
         const double br = 8.0 * 2.0 * (double)gate_bytes;
         const double bs = has_shared ? 2.0 * (double)shared_gate->bytes : 0.0;
@@ -910,6 +915,11 @@ lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_exper
         m->wg_s = has_shared ? (int)(total * bs / (br + bs) + 0.5) : 0;
         if (has_shared && m->wg_s < 1) m->wg_s = 1;
         m->wg_r = total;
+        m->wg_s_given = m->wg_s;
+        if (has_shared) {
+            const int round = moe_gate_up_resident_per_cu(tg, shared_gate->type, (int)hidden) * ctx->cu_count;
+            if (round - m->wg_r > m->wg_s) m->wg_s_given = round - m->wg_r;
+        }
     }
     m->tile_d = 16;
     // The down kernel stages the Q8_K of every routed expert's h (up to
@@ -1009,6 +1019,7 @@ lbh_status lbh_moe_set_tiles(lbh_moe *m, int32_t wg_routed, int32_t wg_shared, i
         return LBH_UNSUPPORTED_SHAPE;
     m->wg_r = wg_routed;
     m->wg_s = wg_shared;
+    m->wg_s_given = wg_shared;
     m->tile_d = tile_d;
     return LBH_OK;
 }
@@ -1760,6 +1771,7 @@ static lbh_status block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const f
     if (mode != 0 && (mode != 1 || !r->bias)) return LBH_INVALID_PARAMETER;
     DeviceGuard g(ctx->device);
     MoeArgs a = moe_args(m, x, y);
+    a.tiles_s = m->has_shared ? m->wg_s : 0;   // the device-router launches' shared-stream share
     a.residual = residual;
     a.router = router_args(r, x, top_k, mode, weight_scale);
     a.route_dev = r->route;

@@ -246,6 +246,8 @@ hipError_t launch_moe_down(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_reset_status(MoeStatus *st, hipStream_t s);
 // LDS of one single-token MoE down launch (gfx950 gives a workgroup at most MOE_MAX_LDS).
 constexpr int MOE_MAX_LDS = 160 * 1024;
+// Gate/up workgroups of the (routed, shared) type pair resident on one CU at once.
+int moe_gate_up_resident_per_cu(int type_gate_r, int type_gate_s, int hidden);
 int moe_down_lds_bytes(int type_down_r, int type_down_s, int n_routed, int has_shared, int ffn_r, int ffn_s,
                        int tile_d);
 hipError_t launch_expf(const float *in, float *out, long long n, int swiglu, const float *up, hipStream_t s);

@@ -625,6 +625,23 @@ int moe_down_lds_bytes(int type_down_r, int type_down_s, int n_routed, int has_s
     return 0x7fffffff;
 }
 
+template <int TYR, int TYS>
+static int gate_up_resident(int hidden) {
+    const int nb = hidden / 256;
+    const int lds = gate_up_lds<TYR>(nb) > gate_up_lds<TYS>(nb) ? gate_up_lds<TYR>(nb) : gate_up_lds<TYS>(nb);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, k_moe_gate_up<TYR, moe_lpu<TYR>(), TYS, moe_lpu<TYS>()>, MOE_THREADS, lds) != hipSuccess || n < 1)
+        n = 1;
+    return n;
+}
+
+int moe_gate_up_resident_per_cu(int type_gate_r, int type_gate_s, int hidden) {
+    if (type_gate_r == T_IQ2_S && type_gate_s == T_Q4_K) return gate_up_resident<T_IQ2_S, T_Q4_K>(hidden);
+    if (type_gate_r == T_IQ2_S && type_gate_s == T_IQ2_S) return gate_up_resident<T_IQ2_S, T_IQ2_S>(hidden);
+    return 1;
+}
+
 hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s) {
     const int nb = a.hidden / 256;
     const int rw = (a.router.n_experts + RT_EXPERTS - 1) / RT_EXPERTS;
