@@ -104,7 +104,8 @@ def test_down_launches_of_fewer_than_four_routed_experts(be, oracle, small, top_
     layer without a shared expert) still fills its whole codebook: the device codebook
     loader spreads it over 256 threads.  The layer without a shared expert shares the
     small layer's routed matrices and is checked against the oracle with an all-zero
-    shared expert (its down rows are +0.0, which leaves every accumulation unchanged)."""
+    shared expert (its down rows are +0.0, which leaves every accumulation unchanged),
+    through the host-routed forward and through the device-router block decode."""
     rng = np.random.default_rng(40 + top_k)
     ids = np.sort(rng.choice(6, size=top_k, replace=False)).astype(np.uint32)
     coefs = rng.random(top_k).astype(np.float32)
@@ -128,11 +129,23 @@ def test_down_launches_of_fewer_than_four_routed_experts(be, oracle, small, top_
     err = oracle.moe_routed_by_id_status(ex, ids, coefs, small.orc_experts, orc_zero, x, want0)
     assert err.status == 0
     plain = be.moe_create(small._keep[0], None)
+    import lbhip
+    w = synth.router_weights(6, 512, 50 + top_k)
+    r = lbhip.Router(be, w)
     try:
         y = dev(np.zeros(512, np.float32))
         be.moe_forward(plain, ids, coefs, dev(x), y)
         assert _same(host(y), want0), "no shared expert"
+        # the block decode (router chains, selection, routed launches) on the same layer
+        rids, rcoefs = oracle.route_softmax_topk(oracle.router_logits_f32(w, x), top_k)
+        want_b = np.full(512, np.nan, np.float32)
+        err = oracle.moe_routed_by_id_status(ex, rids, rcoefs, small.orc_experts, orc_zero, x, want_b)
+        assert err.status == 0
+        y = dev(np.zeros(512, np.float32))
+        lbhip.moe_block_forward(be, plain, r, dev(x), y, top_k)
+        assert _same(host(y), want_b), "block decode, no shared expert"
     finally:
+        r.close()
         plain.close()
 
 
