@@ -1771,7 +1771,14 @@ static lbh_status block_forward(lbh_ctx *ctx, lbh_moe *m, lbh_router *r, const f
     if (mode != 0 && (mode != 1 || !r->bias)) return LBH_INVALID_PARAMETER;
     DeviceGuard g(ctx->device);
     MoeArgs a = moe_args(m, x, y);
-    a.tiles_s = m->has_shared ? m->wg_s : 0;   // the device-router launches' shared-stream share
+    // Beside the router chains the shared stream keeps its byte share (wg_s);
+    // the selecting routed launch, which takes tiles_r + tiles_s workgroups,
+    // fills the same round as the routing-given launch (55.2 vs 55.7 us per
+    // token at the configs[2] shapes).
+    if (m->has_shared) {
+        a.tiles_s = m->wg_s;
+        a.tiles_r = m->wg_r + m->wg_s_given - m->wg_s;
+    }
     a.residual = residual;
     a.router = router_args(r, x, top_k, mode, weight_scale);
     a.route_dev = r->route;
