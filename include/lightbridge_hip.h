@@ -303,7 +303,11 @@ lbh_status lbh_moe_create(lbh_ctx *ctx, const lbh_matrix *const *gate, const lbh
                           lbh_error *err);
 lbh_status lbh_moe_destroy(lbh_moe *moe);
 /* Launch-shape knob: workgroups of the routed and shared gate/up streams
- * (1..65536 each) and output rows per down workgroup (1..256). */
+ * (1..65536 each) and output rows per down workgroup (1..256).  Defaults:
+ * two routed workgroups per CU; for the shared stream its byte share of two
+ * per CU beside the router chains, and in the routing-given and selecting
+ * gate/up launches whatever fills one round of resident workgroups.  A set
+ * value applies to every launch. */
 lbh_status lbh_moe_set_tiles(lbh_moe *moe, int32_t wg_routed, int32_t wg_shared, int32_t tile_d);
 /* Schedule of the asynchronous single-token forwards of a layer with a shared
  * expert: 1 runs the shared expert's gate/up and down on a second stream of
