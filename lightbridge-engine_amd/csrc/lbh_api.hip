@@ -158,7 +158,7 @@ lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
         ctx->tuning.max_blocks = value;
         return LBH_OK;
     case LBH_TUNE_GEMV_DEPTH:
-        if (value < 0 || value == 1 || value > 4) return LBH_INVALID_PARAMETER;
+        if (value < 0 || value > 4) return LBH_INVALID_PARAMETER;
         ctx->tuning.depth = value;
         return LBH_OK;
     case LBH_TUNE_GEMM_SHAPE:

@@ -112,7 +112,7 @@ using DecOf = typename std::conditional<Traits<TY>::KQ, DecKQ<LPU>, DecIQ<LPU>>:
 template <int LPU>
 __device__ __forceinline__ void decode(const WSlice<T_IQ2_S, LPU> &w, const void *gridp, int, DecIQ<LPU> &o) {
     constexpr int G = 8 / LPU;
-    const uint2 *grid = reinterpret_cast<const uint2 *>(gridp);
+    const GridRef<T_IQ2_S> grid(gridp);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
@@ -120,8 +120,8 @@ __device__ __forceinline__ void decode(const WSlice<T_IQ2_S, LPU> &w, const void
 #pragma unroll
         for (int lg = 0; lg < 4; ++lg) {
             const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
-            const uint2 code = grid[idx];
-            const uint2 sm = grid[1024 + byte_of(w.sg[g], lg)];
+            const uint2 code = grid.code(idx);
+            const uint2 sm = grid.sel(byte_of(w.sg[g], lg));
             const uint32_t sel_lo = sm.x | code.x;
             const uint32_t sel_hi = sm.y | code.y;
             o.w[8 * g + 2 * lg] = perm(IQ2S_NEG, IQ2S_POS, sel_lo);
@@ -136,20 +136,17 @@ __device__ __forceinline__ void decode(const WSlice<T_IQ2_S, LPU> &w, const void
 template <int LPU>
 __device__ __forceinline__ void decode(const WSlice<T_IQ3_S, LPU> &w, const void *gridp, int, DecIQ<LPU> &o) {
     constexpr int G = 8 / LPU;
-    const uint2 *grid = reinterpret_cast<const uint2 *>(gridp);
+    const GridRef<T_IQ3_S> grid(gridp);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
         const int32_t sc = (int32_t)(2 * ((w.sc >> (4 * g)) & 15u) + 1);
+        uint32_t ad[8];
+        iq3_group_addrs(w.qs[2 * g], w.qs[2 * g + 1], byte_of(g < 4 ? w.qh : w.qh2, g & 3), ad);
 #pragma unroll
         for (int lg = 0; lg < 4; ++lg) {
-            const uint32_t qq = w.qs[2 * g + (lg >> 1)];
-            const int sh = 16 * (lg & 1);
-            const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
-            const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
-            const uint2 g1 = grid[i1], g2 = grid[i2], sm = grid[512 + byte_of(w.sg[g], lg)];
-            o.w[8 * g + 2 * lg] = perm(g1.y, g1.x, sm.x);
-            o.w[8 * g + 2 * lg + 1] = perm(g2.y, g2.x, sm.y);
+            const uint2 sm = grid.sel(byte_of(w.sg[g], lg));
+            o.w[8 * g + 2 * lg] = iq3_signed(grid.pair(ad[2 * lg]), sm.x);
+            o.w[8 * g + 2 * lg + 1] = iq3_signed(grid.pair(ad[2 * lg + 1]), sm.y);
         }
         o.s[2 * g] = sc;
         o.s[2 * g + 1] = sc;

@@ -38,8 +38,10 @@ __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel)
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t v, int i) { return (v >> (8 * i)) & 0xffu; }
 
-// Byte-wise negation of grid magnitudes (all grid bytes are in 1..63: no borrows).
-__device__ __forceinline__ uint32_t neg_bytes(uint32_t g) { return (g ^ 0xffffffffu) + 0x01010101u; }
+// Byte-wise negation of grid magnitudes: every grid byte m is in 1..63, and
+// 0x01010100 = sum over bytes i of 256 << 8i (mod 2^32), so byte i of the
+// difference is 256 - m_i, i.e. -m_i, with no borrow between bytes.
+__host__ __device__ constexpr uint32_t neg_bytes(uint32_t g) { return 0x01010100u - g; }
 
 // v_perm selector applying four sign bits to a dword of magnitudes: byte i
 // takes the negated magnitude (selector 4 + i, from the first source) when bit
@@ -195,8 +197,11 @@ __device__ __forceinline__ uint32_t row16_or(uint32_t v) {
 // 32-byte group j holds the quants 32j + t + 8k, k = 0..3 (the ActKQ layout).
 // Lane li holds group li / 2's quants 16 (li & 1) .. + 15, i.e. bytes k = 2
 // (li & 1) and 2 (li & 1) + 1 of each of the group's eight dwords.
+// out_q (optional): the block's 256 quants alone, at out_q + RES_STRIDE *
+// block, 16-byte aligned for the ActIQL reads.
 constexpr int RES_STRIDE = 272;
-__device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out, uint8_t *out_r = nullptr) {
+__device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out, uint8_t *out_r = nullptr,
+                                               uint8_t *out_q = nullptr) {
     const int lane = threadIdx.x & 63;
     const int li = lane & 15;
     const float *v = q.v;
@@ -248,6 +253,9 @@ __device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out, u
             *reinterpret_cast<uint32_t *>(ob + 260 + 2 * li) =
                 (uint32_t)(uint16_t)(int16_t)qsum | ((uint32_t)(uint16_t)(int16_t)next << 16);
         if (li == 0) *reinterpret_cast<uint32_t *>(ob) = __float_as_uint(d);
+        if (out_q)
+            *reinterpret_cast<uint4 *>(out_q + q.blk * RES_STRIDE + 16 * li) =
+                make_uint4(packed[0], packed[1], packed[2], packed[3]);
         if (out_r) {
             // half-dword t = quants t and t + 8 of this lane's 16
             const uint32_t h01 = perm(packed[2], packed[0], 0x05010400u);   // t = 0, 1
@@ -264,8 +272,9 @@ __device__ __forceinline__ void quantize_store(const QuantIn &q, uint8_t *out, u
 }
 
 __device__ __forceinline__ void quantize_blocks_wave(const float *__restrict__ x, uint8_t *out, long long first,
-                                                     long long nblocks, uint8_t *out_r = nullptr) {
-    quantize_store(quantize_load(x, first, nblocks), out, out_r);
+                                                     long long nblocks, uint8_t *out_r = nullptr,
+                                                     uint8_t *out_q = nullptr) {
+    quantize_store(quantize_load(x, first, nblocks), out, out_r, out_q);
 }
 
 // ------------------------------------------------------------ type traits
@@ -320,6 +329,28 @@ struct ActKQ {
 template <int TY, int LPU>
 using ActOf = typename std::conditional<Traits<TY>::KQ, ActKQ<Traits<TY>::NG / LPU>,
                                         ActIQ<Traits<TY>::NG / LPU>>::type;
+
+// IQ activation slice left in LDS: `q` addresses the lane's 256 quants in a
+// 16-byte aligned copy (quantize_store's out_q), read one group of 32 at a
+// time.  Holds 2 VGPRs where ActIQ<8> holds 65, for kernels whose occupancy
+// the register file limits.
+struct ActIQL {
+    const uint8_t *q;
+    float d8;
+};
+
+// The 32 quants (8 dwords) of group g of an activation slice.
+template <int G>
+__device__ __forceinline__ void act_group(const ActIQ<G> &a, int g, uint32_t (&q)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = a.q[8 * g + i];
+}
+__device__ __forceinline__ void act_group(const ActIQL &a, int g, uint32_t (&q)[8]) {
+    const uint4 *p = reinterpret_cast<const uint4 *>(a.q + 32 * g);
+    const uint4 v0 = p[0], v1 = p[1];
+    q[0] = v0.x, q[1] = v0.y, q[2] = v0.z, q[3] = v0.w;
+    q[4] = v1.x, q[5] = v1.y, q[6] = v1.z, q[7] = v1.w;
+}
 
 // `blk` is a 292-byte Q8_K block (global or LDS); part p of LPU.
 template <int G>
@@ -382,19 +413,75 @@ __device__ __forceinline__ void load_act_res(const uint8_t *blk, const uint8_t *
 //   IQ2S: uint2 x 1024 (8 KiB) of byte codes 0/1/2 for the magnitudes 8/25/43
 //         (the only values in the codebook); v_perm with selector code + 4*sign
 //         picks from the constant dwords {8,25,43} / {-8,-25,-43}.
-//   IQ3S: uint2 {pos, neg} x 512 (4 KiB): each entry next to its byte-wise negation.
+//   IQ3S: uint32 x 512 (2 KiB) magnitude words; the negation is one VALU
+//         subtraction (neg_bytes), cheaper than the 4 more LDS bytes per
+//         lookup a stored (magnitude, negation) pair costs.
 
 // Each translation unit holds its own copy (no relocatable device code).
 #include "lbh_iq_grids.inc"
 static __constant__ uint64_t c_iq2s_grid[1024] = {LBH_IQ2S_GRID_VALUES};
 static __constant__ uint32_t c_iq3s_grid[512] = {LBH_IQ3S_GRID_VALUES};
 
+// IQ3S: 512 (magnitude, negation) pairs of 8 bytes at iq3_pair_offset, then
+// the 256 sign-byte entries (iq3_sign_entry) at IQ3_SIGN_OFF.  The pair order
+// makes a lookup's LDS address one v_perm of the qs bytes (iq3_group_addrs):
+// stored magnitudes and negations cost 4 more LDS bytes per lookup than a
+// magnitude table, but LDS bandwidth is not what bounds these decodes, VALU
+// issue is.
 template <int TY>
 struct GridLDS {
-    // IQ2S: the 1024 code entries, then 256 sign-byte entries (sign_lut_entry);
-    // IQ3S: the 512 (magnitude, negation) entries, then 256 sign-byte entries
-    // (iq3_sign_entry).
-    static constexpr int BYTES = TY == T_IQ2_S ? (1024 + 256) * 8 : TY == T_IQ3_S ? (512 + 256) * 8 : 0;
+    static constexpr int MAIN = TY == T_IQ2_S ? 1024 * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
+    static constexpr int BYTES = MAIN > 0 ? MAIN + 256 * 8 : 0;
+};
+constexpr int IQ3_SIGN_OFF = 512 * 8;
+
+// Byte offset of the IQ3S pair of 9-bit index q | h << 8: (q & 15) * 256 +
+// (q & 0xf0) + 8 h, a bijection onto the 8-byte slots of 4 KiB.
+__host__ __device__ constexpr uint32_t iq3_pair_offset(uint32_t q, uint32_t h) {
+    return (q & 15u) * 256u + (q & 0xf0u) + 8u * h;
+}
+
+// The eight pair offsets of one IQ3S group: qs bytes j = 0..7 (q0 = bytes
+// 0-3, q1 = bytes 4-7) with high bit j of the group's qh byte h
+// (q8_k.rs:397-420).  Per qs dword: y = low nibbles, x = high nibbles with the
+// high bit at bit 3 of each byte, and offset j = x_j + 256 y_j, one v_perm.
+__device__ __forceinline__ void iq3_group_addrs(uint32_t q0, uint32_t q1, uint32_t h, uint32_t (&a)[8]) {
+    // bit j of a nibble to bit 0 of byte j: n * 0x204081 places bit j at
+    // 8j + (7 (j' - j)) only for j' = j inside the mask, with no carries.
+    const uint32_t b0 = __umul24(h & 15u, 0x204081u) & 0x01010101u;
+    const uint32_t b1 = __umul24((h >> 4) & 15u, 0x204081u) & 0x01010101u;
+    const uint32_t x0 = (q0 & 0xf0f0f0f0u) | (b0 << 3), y0 = q0 & 0x0f0f0f0fu;
+    const uint32_t x1 = (q1 & 0xf0f0f0f0u) | (b1 << 3), y1 = q1 & 0x0f0f0f0fu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        // byte 0 <- x byte j (selector j), byte 1 <- y byte j (4 + j), bytes 2-3 <- 0
+        const uint32_t sel = 0x0c0c0000u | ((4u + j) << 8) | (uint32_t)j;
+        a[j] = perm(y0, x0, sel);
+        a[4 + j] = perm(y1, x1, sel);
+    }
+}
+
+// A lane's view of a codebook in LDS.  VSEL computes the sign selectors in
+// VALU (three ops per nibble) instead of reading the sign table: one LDS read
+// fewer per eight weights, for kernels whose LDS issue, not VALU, is short.
+template <int TY, bool VSEL = false>
+struct GridRef {
+    const uint8_t *g;
+    __device__ __forceinline__ explicit GridRef(const void *p) : g(static_cast<const uint8_t *>(p)) {}
+    // IQ2S code entry of 10-bit index i; IQ3S pair at byte offset o
+    // (iq3_pair_offset); selectors of sign byte sb (sign_lut_entry /
+    // iq3_sign_entry).
+    __device__ __forceinline__ uint2 code(uint32_t i) const { return reinterpret_cast<const uint2 *>(g)[i]; }
+    __device__ __forceinline__ uint2 pair(uint32_t o) const { return *reinterpret_cast<const uint2 *>(g + o); }
+    __device__ __forceinline__ uint2 sel(uint32_t sb) const {
+        if constexpr (VSEL) {
+            constexpr uint32_t o = TY == T_IQ3_S ? 0x03020100u : 0u;
+            return make_uint2((__umul24(sb & 15u, 0x810204u) & 0x04040404u) | o,
+                              (__umul24((sb >> 4) & 15u, 0x810204u) & 0x04040404u) | o);
+        } else {
+            return reinterpret_cast<const uint2 *>(g + GridLDS<TY>::MAIN)[sb];
+        }
+    }
 };
 
 // Sign-byte table appended to the IQ2S codes: entry s = the v_perm selector
@@ -410,6 +497,10 @@ __device__ __forceinline__ uint2 sign_lut_entry(uint32_t s) {
 // negation) pair, so each group of four signs costs one LDS read instead of
 // the selector arithmetic.
 __device__ __forceinline__ uint2 iq3_sign_entry(uint32_t s) { return make_uint2(sign_sel(s & 15u), sign_sel(s >> 4)); }
+
+// The signed IQ3S grid dword of a (magnitude, negation) pair and its sign
+// selector (q8_k.rs:397-420).
+__device__ __forceinline__ uint32_t iq3_signed(uint2 pr, uint32_t sel) { return perm(pr.y, pr.x, sel); }
 
 // The LDS images of both tables (GridLDS layout), built at compile time from
 // the codebooks: a workgroup's fill is a plain copy with 16-byte loads.
@@ -432,11 +523,14 @@ struct GridImages {
             iq2s[2 * (1024 + sb) + 1] = ((sb >> 4) * 0x810204u) & 0x04040404u;
         }
         const uint32_t g3[512] = {LBH_IQ3S_GRID_VALUES};
-        for (int i = 0; i < 512; ++i) iq3s[2 * i] = g3[i], iq3s[2 * i + 1] = (g3[i] ^ 0xffffffffu) + 0x01010101u;
+        for (uint32_t i = 0; i < 512; ++i) {
+            const uint32_t o = iq3_pair_offset(i & 255u, i >> 8) / 4;
+            iq3s[o] = g3[i], iq3s[o + 1] = neg_bytes(g3[i]);
+        }
         // iq3_sign_entry: sign_sel of each nibble.
         for (uint32_t sb = 0; sb < 256; ++sb) {
-            iq3s[2 * (512 + sb)] = (((sb & 15u) * 0x810204u) & 0x04040404u) | 0x03020100u;
-            iq3s[2 * (512 + sb) + 1] = (((sb >> 4) * 0x810204u) & 0x04040404u) | 0x03020100u;
+            iq3s[1024 + 2 * sb] = (((sb & 15u) * 0x810204u) & 0x04040404u) | 0x03020100u;
+            iq3s[1024 + 2 * sb + 1] = (((sb >> 4) * 0x810204u) & 0x04040404u) | 0x03020100u;
         }
     }
 };
@@ -580,9 +674,8 @@ constexpr uint32_t IQ2S_NEG = 0x00d5e7f8u;
 // one per pair of lookups, at the cost of the registers that hold them: a
 // latency-bound matvec with one wave per SIMD gains, kernels that rely on
 // occupancy keep GB = 0, the compiler's interleaved schedule).
-template <int LPU, int GB = 0>
-__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, const ActIQ<8 / LPU> &a,
-                                             const uint2 *grid) {
+template <int LPU, int GB = 0, class A, bool VS>
+__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, const A &a, const GridRef<T_IQ2_S, VS> &grid) {
     constexpr int G = 8 / LPU;
     int32_t bsum = 0;
     if constexpr (GB == 0) {
@@ -590,18 +683,20 @@ __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, cons
         for (int g = 0; g < G; ++g) {
             const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
             const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
+            uint32_t aq[8];
+            act_group(a, g, aq);
             int32_t part[2] = {0, 0};
 #pragma unroll
             for (int lg = 0; lg < 4; ++lg) {
                 const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
-                const uint2 code = grid[idx];
+                const uint2 code = grid.code(idx);
                 // selector bits of the eight sign bits: byte i takes the
                 // negated source (selector 4 + code) when sign bit i is set
-                const uint2 sm = grid[1024 + byte_of(w.sg[g], lg)];
+                const uint2 sm = grid.sel(byte_of(w.sg[g], lg));
                 const uint32_t sel_lo = sm.x | code.x;
                 const uint32_t sel_hi = sm.y | code.y;
-                part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
-                part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
+                part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), aq[2 * lg], part[lg >> 1]);
+                part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), aq[2 * lg + 1], part[lg >> 1]);
             }
             bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
         }
@@ -616,8 +711,8 @@ __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, cons
                 const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
 #pragma unroll
                 for (int lg = 0; lg < 4; ++lg) {
-                    code[k][lg] = grid[byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u)];
-                    sm[k][lg] = grid[1024 + byte_of(w.sg[g], lg)];
+                    code[k][lg] = grid.code(byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u));
+                    sm[k][lg] = grid.sel(byte_of(w.sg[g], lg));
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -625,13 +720,15 @@ __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, cons
             for (int k = 0; k < GC; ++k) {
                 const int g = g0 + k;
                 const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
+                uint32_t aq[8];
+                act_group(a, g, aq);
                 int32_t part[2] = {0, 0};
 #pragma unroll
                 for (int lg = 0; lg < 4; ++lg) {
                     const uint32_t sel_lo = sm[k][lg].x | code[k][lg].x;
                     const uint32_t sel_hi = sm[k][lg].y | code[k][lg].y;
-                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), a.q[8 * g + 2 * lg], part[lg >> 1]);
-                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), a.q[8 * g + 2 * lg + 1], part[lg >> 1]);
+                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), aq[2 * lg], part[lg >> 1]);
+                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), aq[2 * lg + 1], part[lg >> 1]);
                 }
                 bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
             }
@@ -688,65 +785,40 @@ __device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t
     }
 }
 
-// IQ3_S integer block sum over the slice's groups (q8_k.rs:380-428); GB as
-// for IQ2_S.
-template <int LPU, int GB = 0>
-__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, const ActIQ<8 / LPU> &a,
-                                             const uint2 *grid) {
+// IQ3_S integer block sum over the slice's groups (q8_k.rs:380-428).  GB > 0
+// issues the LDS reads of GB groups before any of them is used (as for
+// IQ2_S).  Local group g is global group G*p + g; its scale nibble is nibble
+// g of w.sc (G <= 4: the lane's scale bits; G == 8: all four scale bytes).
+template <int LPU, int GB = 0, class A, bool VS>
+__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, const A &a, const GridRef<T_IQ3_S, VS> &grid) {
     constexpr int G = 8 / LPU;
-    int32_t bsum = 0;
-    if constexpr (GB == 0) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
-            // local group g is global group gg = G*p + g; its scale nibble is
-            // nibble (gg & 1) of scale byte gg / 2, i.e. nibble g of w.sc (G <= 4)
-            // or nibble g of the 32-bit word holding all four scale bytes (G == 8).
-            const uint32_t ps = (w.sc >> (4 * g)) & 15u;
-            int32_t gs = 0;
-#pragma unroll
-            for (int lg = 0; lg < 4; ++lg) {
-                const uint32_t qq = w.qs[2 * g + (lg >> 1)];
-                const int sh = 16 * (lg & 1);
-                const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
-                const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
-                const uint2 g1 = grid[i1], g2 = grid[i2], sm = grid[512 + byte_of(w.sg[g], lg)];
-                gs = dot4(perm(g1.y, g1.x, sm.x), a.q[8 * g + 2 * lg], gs);
-                gs = dot4(perm(g2.y, g2.x, sm.y), a.q[8 * g + 2 * lg + 1], gs);
-            }
-            bsum += mul24(gs, (int32_t)(2 * ps + 1));
-        }
-        return bsum;
-    }
     constexpr int GC = GB == 0 ? 1 : G < GB ? G : GB;
+    int32_t bsum = 0;
 #pragma unroll
     for (int g0 = 0; g0 < G; g0 += GC) {
-        uint2 g1[GC][4], g2[GC][4], sm[GC][4];
+        uint2 pr[GC][8], sm[GC][4];
 #pragma unroll
         for (int k = 0; k < GC; ++k) {
             const int g = g0 + k;
-            const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+            uint32_t ad[8];
+            iq3_group_addrs(w.qs[2 * g], w.qs[2 * g + 1], byte_of(g < 4 ? w.qh : w.qh2, g & 3), ad);
 #pragma unroll
-            for (int lg = 0; lg < 4; ++lg) {
-                const uint32_t qq = w.qs[2 * g + (lg >> 1)];
-                const int sh = 16 * (lg & 1);
-                const uint32_t i1 = ((qq >> sh) & 0xffu) | ((h << (8 - 2 * lg)) & 0x100u);
-                const uint32_t i2 = ((qq >> (sh + 8)) & 0xffu) | ((h << (7 - 2 * lg)) & 0x100u);
-                g1[k][lg] = grid[i1];
-                g2[k][lg] = grid[i2];
-                sm[k][lg] = grid[512 + byte_of(w.sg[g], lg)];
-            }
+            for (int j = 0; j < 8; ++j) pr[k][j] = grid.pair(ad[j]);
+#pragma unroll
+            for (int lg = 0; lg < 4; ++lg) sm[k][lg] = grid.sel(byte_of(w.sg[g], lg));
         }
-        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (GB > 0) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < GC; ++k) {
             const int g = g0 + k;
             const uint32_t ps = (w.sc >> (4 * g)) & 15u;
+            uint32_t aq[8];
+            act_group(a, g, aq);
             int32_t gs = 0;
 #pragma unroll
             for (int lg = 0; lg < 4; ++lg) {
-                gs = dot4(perm(g1[k][lg].y, g1[k][lg].x, sm[k][lg].x), a.q[8 * g + 2 * lg], gs);
-                gs = dot4(perm(g2[k][lg].y, g2[k][lg].x, sm[k][lg].y), a.q[8 * g + 2 * lg + 1], gs);
+                gs = dot4(iq3_signed(pr[k][2 * lg], sm[k][lg].x), aq[2 * lg], gs);
+                gs = dot4(iq3_signed(pr[k][2 * lg + 1], sm[k][lg].y), aq[2 * lg + 1], gs);
             }
             bsum += mul24(gs, (int32_t)(2 * ps + 1));
         }

@@ -24,6 +24,7 @@ namespace lbh {
 // pay it fewer times.
 constexpr int GEMV_THREADS = 256;
 constexpr int GEMV_THREADS_LARGE = 512;
+constexpr int GEMV_THREADS_XL = 1024;
 constexpr int MAX_NB = 64;
 
 __device__ __forceinline__ bool status_set(const DevStatus *st) {
@@ -47,6 +48,11 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     // into that layout too, instead of a byte transpose in every lane.
     constexpr bool RES = FUSEQ && Traits<TY>::KQ;
     __shared__ __align__(16) uint8_t s_q8r[RES ? MAX_NB * RES_STRIDE : 16];
+    // 1024-thread IQ instances read the activations from LDS one group at a
+    // time (ActIQL) instead of holding a whole block in registers, which is
+    // what fits four waves per SIMD.
+    constexpr bool AL = LPU == 1 && !Traits<TY>::KQ && NT == GEMV_THREADS_XL;
+    __shared__ __align__(16) uint8_t s_q8q[AL ? MAX_NB * RES_STRIDE : 16];
     __shared__ FoldLDS<TY> s_fold[GEMV_WAVES];
 
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -74,8 +80,26 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     // after the barrier.
     int it = blockIdx.x * GEMV_WAVES + wid;
     const GridIn<TY> gin = grid_load<TY>();
-    QuantIn qin;
-    if constexpr (FUSEQ) qin = quantize_load(p.x, 4 * wid, NB);
+    // The input blocks of the first QP quantize passes are loaded here, ahead
+    // of the weights: a pass whose loads went out after the weight loads
+    // would wait for the whole weight burst to land before the barrier.
+    constexpr int QP = FUSEQ ? (MAX_NB / (4 * GEMV_WAVES) < 2 ? MAX_NB / (4 * GEMV_WAVES) : 2) : 1;
+    QuantIn qin[QP];
+    if constexpr (FUSEQ) {
+#pragma unroll
+        for (int q = 0; q < QP; ++q) qin[q] = quantize_load(p.x, 4 * wid + 4 * GEMV_WAVES * q, NB);
+    }
+    // Caller-quantized activations of an AL instance: their quants copied to
+    // the aligned LDS copy (NB * 64 dwords, at most four per thread).
+    constexpr int CP = !FUSEQ && AL ? MAX_NB * 64 / NT : 1;
+    uint32_t cp[CP];
+    if constexpr (!FUSEQ && AL) {
+#pragma unroll
+        for (int c = 0; c < CP; ++c) {
+            const int i = threadIdx.x + NT * c;
+            cp[c] = i < NB * 64 ? ld_u32(p.q8 + (i >> 6) * 292 + 4 + 4 * (i & 63)) : 0u;
+        }
+    }
     W w[D];
     {
         int r = it * L.rpw + (L.lane_on ? L.slot : L.rpw - 1);
@@ -85,9 +109,18 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
 
     grid_store<TY>(gin, s_grid);
     if constexpr (FUSEQ) {
-        quantize_store(qin, s_q8, RES ? s_q8r : nullptr);
-        for (int b0 = 4 * wid + 4 * GEMV_WAVES; b0 < NB; b0 += 4 * GEMV_WAVES)
-            quantize_blocks_wave(p.x, s_q8, b0, NB, RES ? s_q8r : nullptr);
+#pragma unroll
+        for (int q = 0; q < QP; ++q)
+            if (4 * wid + 4 * GEMV_WAVES * q < NB)
+                quantize_store(qin[q], s_q8, RES ? s_q8r : nullptr, AL ? s_q8q : nullptr);
+        for (int b0 = 4 * wid + 4 * GEMV_WAVES * QP; b0 < NB; b0 += 4 * GEMV_WAVES)
+            quantize_blocks_wave(p.x, s_q8, b0, NB, RES ? s_q8r : nullptr, AL ? s_q8q : nullptr);
+    } else if constexpr (AL) {
+#pragma unroll
+        for (int c = 0; c < CP; ++c) {
+            const int i = threadIdx.x + NT * c;
+            if (i < NB * 64) *reinterpret_cast<uint32_t *>(s_q8q + (i >> 6) * RES_STRIDE + 4 * (i & 63)) = cp[c];
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -99,21 +132,26 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
                 reinterpret_cast<uint32_t *>(p.q8_out)[i] = reinterpret_cast<const uint32_t *>(s_q8)[i];
     }
 
-    ActOf<TY, LPU> act;
-    if constexpr (RES)
+    using A = typename std::conditional<AL, ActIQL, ActOf<TY, LPU>>::type;
+    A act;
+    if constexpr (AL) {
+        act.q = s_q8q + L.b * RES_STRIDE;
+        act.d8 = __uint_as_float(ld_u32(FUSEQ ? s_q8 + L.b * 292 : p.q8 + (long long)L.b * 292));
+    } else if constexpr (RES) {
         load_act_res(s_q8 + L.b * 292, s_q8r + L.b * RES_STRIDE, L.part, act);
-    else
+    } else {
         load_act(FUSEQ ? s_q8 + L.b * 292 : p.q8 + (long long)L.b * 292, L.part, act);
+    }
 
     auto process = [&](int it, const W &w) {
         const int r = it * L.rpw + L.slot;
         const bool on = L.lane_on && r < rows;
         // One wave per SIMD: the codebook reads are gathered (the latency of a
         // single wave's LDS round trips is the dot's critical path).
-        constexpr int GB = TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
+        constexpr int GB = D == 1 ? 0 : TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
         const float v =
-            row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8>(w, act, on, L, s_grid, s_fold[wid], p.block_sums,
-                                                          (long long)r * NB + L.b);
+            row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8, A, AL>(w, act, on, L, s_grid, s_fold[wid],
+                                                                 p.block_sums, (long long)r * NB + L.b);
         if (on && L.leader()) store_y(p, r, v);
     };
 
@@ -168,6 +206,7 @@ static hipError_t launch_nt(const GemvArgs &a, const GemvTuning &t, hipStream_t 
 // IQ3_S 4096x13312 14.5 -> 12.7 us; Q4_K 4096x4096 stays faster at 256).
 template <int TY, int LPU, bool FUSEQ, int D>
 static hipError_t launch_inst(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
+    if constexpr (LPU == 1 && D == 1 && !Traits<TY>::KQ) return launch_nt<TY, LPU, FUSEQ, D, GEMV_THREADS_XL>(a, t, s);
     if constexpr (LPU == 1) {
         const long long units = (long long)a.m.rows * a.m.nb;
         if (units >= 2LL * 64 * 4 * (t.cu_count > 0 ? t.cu_count : 256))
@@ -186,6 +225,7 @@ static hipError_t launch_typed(const GemvArgs &a, const GemvTuning &t, int depth
     switch (depth) {
     case 4: return launch_depth<TY, LPU, 4>(a, t, s);
     case 3: return launch_depth<TY, LPU, 3>(a, t, s);
+    case 1: return launch_depth<TY, LPU, 1>(a, t, s);
     default: return launch_depth<TY, LPU, 2>(a, t, s);
     }
 }
@@ -215,12 +255,23 @@ static int default_lpu(const GemvArgs &a, int cu_count) {
     return units >= 64LL * 4 * cus ? 1 : units >= 80LL * cus ? 2 : 4;
 }
 
+// Built-in depth: one row step per wave in 1024-thread workgroups (activations
+// read from LDS, four waves per SIMD) for one-lane IQ matvecs with at least 12
+// wave steps per CU, two steps in flight otherwise (measured on MI355X, fused
+// Q8_K: IQ2_S 13312x4096 8.9 -> 8.0 us, IQ3_S 4096x13312 12.3 -> 11.3 us;
+// IQ3_S 4096x8192, 8 steps per CU, 7.7 vs 9.1 us stays at two).
+static int default_depth(const GemvArgs &a, int lpu, int cu_count) {
+    const bool iq = a.m.type == T_IQ2_S || a.m.type == T_IQ3_S;
+    const long long steps = (long long)a.m.rows * a.m.nb / 64;
+    return iq && lpu == 1 && steps >= 12LL * (cu_count > 0 ? cu_count : 256) ? 1 : 2;
+}
+
 hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
     const int nb = a.m.nb;
     if (nb < 1 || nb > MAX_NB || a.m.rows < 1) return hipErrorInvalidValue;
     if (!a.q8 && !a.x) return hipErrorInvalidValue;
     const int lpu = t.lpu > 0 ? t.lpu : default_lpu(a, t.cu_count);
-    const int depth = t.depth > 0 ? t.depth : 2;
+    const int depth = t.depth > 0 ? t.depth : default_depth(a, lpu, t.cu_count);
     switch (a.m.type) {
     case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, t, lpu, depth, s);
     case T_IQ3_S: return launch_lpu<T_IQ3_S>(a, t, lpu, depth, s);

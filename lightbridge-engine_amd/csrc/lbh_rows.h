@@ -81,8 +81,8 @@ using WOf = typename std::conditional<Traits<TY>::KQ, WSliceKQ<TY, LPU>, WSlice<
 // block_sums (optional) receives the integer stage of unit u.  GB: codebook
 // lookups gathered per GB groups (slice_sum); FW: fold_terms.  Contains wave
 // barriers: every lane of the wave must call it.
-template <int TY, int LPU, int GB = 0, int FW = 16>
-__device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, LPU> &act, bool on,
+template <int TY, int LPU, int GB = 0, int FW = 16, class A = ActOf<TY, LPU>, bool VSEL = false>
+__device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const A &act, bool on,
                                          const LaneMap<LPU> &L, const void *grid, FoldLDS<TY> &f,
                                          int32_t *block_sums, long long u) {
     using Tr = Traits<TY>;
@@ -126,7 +126,7 @@ __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const ActOf<TY, 
         int32_t bs = 0;
         uint32_t dbits = 0;
         if (on) {
-            bs = slice_sum<LPU, GB>(w, act, reinterpret_cast<const uint2 *>(grid));
+            bs = slice_sum<LPU, GB>(w, act, GridRef<TY, VSEL>(grid));
             dbits = w.d;
         }
         bs = unit_reduce<LPU>(bs);

@@ -230,15 +230,20 @@ def test_upload_shape_errors(be):
 @pytest.mark.parametrize("ty,rows,k", [(Q4_K, 300, 4096), (Q5_K, 97, 2048), (IQ2_S, 515, 4096),
                                        (IQ3_S, 1029, 1536), (IQ2_S, 33, 256), (Q5_K, 17, 16384)])
 def test_gemv_every_lanes_per_unit_and_persistent_loop(be, oracle, lpu, ty, rows, k):
-    """Every launch shape gives the same bits: lanes per unit 1/2/4, and a
-    workgroup cap of 3 so each wave walks many rows of the persistent loop."""
+    """Every launch shape gives the same bits: lanes per unit 1/2/4, one or two
+    row steps in flight per wave (one lane per unit at depth 1: 1024-thread
+    workgroups reading the activations from LDS), and a workgroup cap of 3 so
+    each wave walks many rows of the persistent loop."""
     try:
-        for cap in (0, 3):
-            be.set_tuning(be.TUNE_GEMV_LPU, lpu)
-            be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
-            _check_gemv(be, oracle, ty, rows, k, seed=rows + lpu + cap)
+        for depth in (0, 1):
+            for cap in (0, 3):
+                be.set_tuning(be.TUNE_GEMV_LPU, lpu)
+                be.set_tuning(be.TUNE_GEMV_DEPTH, depth)
+                be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
+                _check_gemv(be, oracle, ty, rows, k, seed=rows + lpu + cap)
     finally:
         be.set_tuning(be.TUNE_GEMV_LPU, 0)
+        be.set_tuning(be.TUNE_GEMV_DEPTH, 0)
         be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, 0)
 
 
@@ -271,7 +276,8 @@ def test_fused_quantize_gemv_matches_quantize_then_dot(be, oracle, ty, rows, k):
 
 @pytest.mark.parametrize("ty,rows,k", [(Q4_K, 37, 256), (Q5_K, 129, 768), (Q4_K, 9, 16384), (Q5_K, 700, 4096),
                                        (IQ2_S, 70, 16384), (IQ3_S, 513, 2304), (Q4_K, 8192, 4096),
-                                       (Q5_K, 8192, 4096), (IQ2_S, 9000, 4096), (IQ3_S, 4096, 8192)])
+                                       (Q5_K, 8192, 4096), (IQ2_S, 9000, 4096), (IQ3_S, 4096, 8192),
+                                       (IQ2_S, 13312, 4096), (IQ3_S, 4096, 13312)])
 def test_fused_quantize_gemv_every_launch_shape(be, oracle, ty, rows, k):
     """The fused kernel quantizes x in every workgroup (K-quant types also into a
     residue-major copy) and picks its workgroup size and lanes per unit from the
@@ -287,19 +293,21 @@ def test_fused_quantize_gemv_every_launch_shape(be, oracle, ty, rows, k):
     m = be.upload(ty, rows, k, w)
     xd = dev(x)
     try:
-        for lpu in (0, 1, 2, 4):
+        for lpu, depth in ((0, 0), (1, 0), (2, 0), (4, 0), (1, 1), (1, 2)):
             for cap in (0, 3):
                 be.set_tuning(be.TUNE_GEMV_LPU, lpu)
+                be.set_tuning(be.TUNE_GEMV_DEPTH, depth)
                 be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
                 y = torch.full((rows,), float("nan"), device="cuda")
                 q8 = torch.zeros(q8_ref.size, dtype=torch.uint8, device="cuda")
                 be.gemv_f32(m, xd, y, q8)
-                assert np.array_equal(host(q8), q8_ref), (lpu, cap)
+                assert np.array_equal(host(q8), q8_ref), (lpu, depth, cap)
                 got = host(y)
                 bad = np.nonzero(got.view(np.uint32) != want.view(np.uint32))[0]
-                assert bad.size == 0, (lpu, cap, bad.size, bad[:5])
+                assert bad.size == 0, (lpu, depth, cap, bad.size, bad[:5])
     finally:
         be.set_tuning(be.TUNE_GEMV_LPU, 0)
+        be.set_tuning(be.TUNE_GEMV_DEPTH, 0)
         be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, 0)
 
 
