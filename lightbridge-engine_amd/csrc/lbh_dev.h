@@ -428,12 +428,52 @@ static __constant__ uint32_t c_iq3s_grid[512] = {LBH_IQ3S_GRID_VALUES};
 // stored magnitudes and negations cost 4 more LDS bytes per lookup than a
 // magnitude table, but LDS bandwidth is not what bounds these decodes, VALU
 // issue is.
+// Table tag of the signed IQ3S table below (a layout tag, not a GGML type).
+constexpr int T_IQ3S_SGN = 0x100 | T_IQ3_S;
+
 template <int TY>
 struct GridLDS {
     static constexpr int MAIN = TY == T_IQ2_S ? 1024 * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
-    static constexpr int BYTES = MAIN > 0 ? MAIN + 256 * 8 : 0;
+    static constexpr int BYTES = TY == T_IQ3S_SGN ? 8192 * 4 : MAIN > 0 ? MAIN + 256 * 8 : 0;
 };
 constexpr int IQ3_SIGN_OFF = 512 * 8;
+
+// Signed IQ3S table (32 KiB): the signed grid dword of every 9-bit index
+// q | h << 8 and four sign bits s4 (bit i negates byte i), at byte offset
+// 256 * ((q & 3) | h << 2 | s4 << 3) + (q & 0xfc).  One LDS word per four
+// weights replaces the (magnitude, negation) pair, the sign selectors and the
+// v_perm that applies them.
+__host__ __device__ constexpr uint32_t iq3_signed_offset(uint32_t q, uint32_t h, uint32_t s4) {
+    return 256u * ((q & 3u) | (h << 2) | (s4 << 3)) + (q & 0xfcu);
+}
+
+// The eight signed-table offsets of one IQ3S group: qs bytes j = 0..7 (q0 =
+// bytes 0-3, q1 = bytes 4-7), high bit j of the qh byte h, sign nibble j of
+// the group's sign word s (q8_k.rs:397-420).  Per qs dword the offset is
+// x_j + 256 y_j, one v_perm: x = q & 0xfc, y = (q & 3) | h << 2 | s4 << 3.
+__device__ __forceinline__ void iq3_group_soffs(uint32_t q0, uint32_t q1, uint32_t h, uint32_t s, uint32_t (&a)[8]) {
+    // bit j of a nibble to bit 0 of byte j (see iq3_group_addrs)
+    const uint32_t b0 = __umul24(h & 15u, 0x204081u) & 0x01010101u;
+    const uint32_t b1 = __umul24((h >> 4) & 15u, 0x204081u) & 0x01010101u;
+    // sign nibbles j = 0..7 to bytes: lo holds nibbles 0, 2, 4, 6 and hi 1, 3, 5, 7
+    const uint32_t lo = s & 0x0f0f0f0fu, hi = (s >> 4) & 0x0f0f0f0fu;
+    const uint32_t n0 = perm(hi, lo, 0x05010400u), n1 = perm(hi, lo, 0x07030602u);
+    const uint32_t y0 = (q0 & 0x03030303u) | (b0 << 2) | (n0 << 3), x0 = q0 & 0xfcfcfcfcu;
+    const uint32_t y1 = (q1 & 0x03030303u) | (b1 << 2) | (n1 << 3), x1 = q1 & 0xfcfcfcfcu;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t sel = 0x0c0c0000u | ((4u + j) << 8) | (uint32_t)j;
+        a[j] = perm(y0, x0, sel);
+        a[4 + j] = perm(y1, x1, sel);
+    }
+}
+
+// A lane's view of the signed IQ3S table.
+struct Iq3SignedRef {
+    const uint8_t *g;
+    __device__ __forceinline__ explicit Iq3SignedRef(const void *p) : g(static_cast<const uint8_t *>(p)) {}
+    __device__ __forceinline__ uint32_t word(uint32_t o) const { return *reinterpret_cast<const uint32_t *>(g + o); }
+};
 
 // Byte offset of the IQ3S pair of 9-bit index q | h << 8: (q & 15) * 256 +
 // (q & 0xf0) + 8 h, a bijection onto the 8-byte slots of 4 KiB.
@@ -536,45 +576,64 @@ struct GridImages {
 };
 static __constant__ GridImages c_grid_images = GridImages();
 
+// The signed IQ3S table image (iq3_signed_offset layout).
+struct Iq3SignedImage {
+    uint32_t w[8192];
+    constexpr Iq3SignedImage() : w{} {
+        const uint32_t g3[512] = {LBH_IQ3S_GRID_VALUES};
+        for (uint32_t i = 0; i < 512; ++i)
+            for (uint32_t s4 = 0; s4 < 16; ++s4) {
+                uint32_t v = 0;
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t m = (g3[i] >> (8 * b)) & 0xffu;
+                    v |= (((s4 >> b) & 1u) ? (256u - m) & 0xffu : m) << (8 * b);
+                }
+                w[iq3_signed_offset(i & 255u, i >> 8, s4) / 4] = v;
+            }
+    }
+};
+static __constant__ Iq3SignedImage c_iq3s_signed = Iq3SignedImage();
+
 template <int TY>
 __device__ __forceinline__ const uint4 *grid_image() {
+    if constexpr (TY == T_IQ3S_SGN) return reinterpret_cast<const uint4 *>(c_iq3s_signed.w);
     return reinterpret_cast<const uint4 *>(TY == T_IQ2_S ? c_grid_images.iq2s : c_grid_images.iq3s);
 }
 
-// Fills the grid for TY into `lds` (cooperatively, all threads of the block);
-// the caller synchronises afterwards.  grid_load / grid_store split it so the
-// table reads can be issued ahead of a kernel's weight loads (the first 256
-// threads of the block: three IQ2S or two IQ3S 16-byte pieces per thread).
-template <int TY>
+// Fills the grid for TY into `lds` (cooperatively, the first NT threads of
+// the block); the caller synchronises afterwards.  grid_load / grid_store
+// split it so the table reads can be issued ahead of a kernel's weight loads
+// (at NT = 256: three IQ2S or two IQ3S 16-byte pieces per thread).
+template <int TY, int NT = 256>
 struct GridIn {
     static constexpr int PIECES = GridLDS<TY>::BYTES / 16;
-    static constexpr int N = PIECES == 0 ? 1 : (PIECES + 255) / 256;
+    static constexpr int N = PIECES == 0 ? 1 : (PIECES + NT - 1) / NT;
     uint4 e[N];
 };
 
-template <int TY>
-__device__ __forceinline__ GridIn<TY> grid_load() {
-    GridIn<TY> g;
-    if constexpr (GridIn<TY>::PIECES > 0) {
+template <int TY, int NT = 256>
+__device__ __forceinline__ GridIn<TY, NT> grid_load() {
+    GridIn<TY, NT> g;
+    if constexpr (GridIn<TY, NT>::PIECES > 0) {
         const uint4 *img = grid_image<TY>();
 #pragma unroll
-        for (int k = 0; k < GridIn<TY>::N; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            g.e[k] = threadIdx.x < 256 && i < GridIn<TY>::PIECES ? img[i] : make_uint4(0u, 0u, 0u, 0u);
+        for (int k = 0; k < GridIn<TY, NT>::N; ++k) {
+            const int i = threadIdx.x + NT * k;
+            g.e[k] = threadIdx.x < NT && i < GridIn<TY, NT>::PIECES ? img[i] : make_uint4(0u, 0u, 0u, 0u);
         }
     }
     return g;
 }
 
-template <int TY>
-__device__ __forceinline__ void grid_store(const GridIn<TY> &g, void *lds) {
-    if constexpr (GridIn<TY>::PIECES > 0) {
-        if (threadIdx.x >= 256) return;
+template <int TY, int NT = 256>
+__device__ __forceinline__ void grid_store(const GridIn<TY, NT> &g, void *lds) {
+    if constexpr (GridIn<TY, NT>::PIECES > 0) {
+        if (threadIdx.x >= NT) return;
         uint4 *out = reinterpret_cast<uint4 *>(lds);
 #pragma unroll
-        for (int k = 0; k < GridIn<TY>::N; ++k) {
-            const int i = threadIdx.x + 256 * k;
-            if (i < GridIn<TY>::PIECES) out[i] = g.e[k];
+        for (int k = 0; k < GridIn<TY, NT>::N; ++k) {
+            const int i = threadIdx.x + NT * k;
+            if (i < GridIn<TY, NT>::PIECES) out[i] = g.e[k];
         }
     }
 }
@@ -822,6 +881,28 @@ __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, cons
             }
             bsum += mul24(gs, (int32_t)(2 * ps + 1));
         }
+    }
+    return bsum;
+}
+
+// IQ3_S integer block sum read from the signed table (same sums as above).
+template <int LPU, int GB = 0, class A>
+__device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ3_S, LPU> &w, const A &a, const Iq3SignedRef &grid) {
+    constexpr int G = 8 / LPU;
+    int32_t bsum = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        uint32_t ad[8], sw[8];
+        iq3_group_soffs(w.qs[2 * g], w.qs[2 * g + 1], byte_of(g < 4 ? w.qh : w.qh2, g & 3), w.sg[g], ad);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sw[j] = grid.word(ad[j]);
+        const uint32_t ps = (w.sc >> (4 * g)) & 15u;
+        uint32_t aq[8];
+        act_group(a, g, aq);
+        int32_t gs = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) gs = dot4(sw[j], aq[j], gs);
+        bsum += mul24(gs, (int32_t)(2 * ps + 1));
     }
     return bsum;
 }

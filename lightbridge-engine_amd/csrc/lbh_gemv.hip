@@ -41,7 +41,14 @@ __device__ __forceinline__ void store_y(const GemvArgs &p, int r, float v) {
 template <int TY, int LPU, bool FUSEQ, int D, int NT>
 __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     constexpr int GEMV_WAVES = NT / 64;
-    constexpr int GB = GridLDS<TY>::BYTES > 0 ? GridLDS<TY>::BYTES : 16;
+    // Large IQ3_S instances read the signed table (one LDS word per four
+    // weights, no sign work; 32 KiB to fill per workgroup), 256-thread ones
+    // the 6 KiB pair table, whose fill costs their short prologue less
+    // (measured on MI355X: IQ3_S 4096x1536 3.86 vs 3.93 us, 4096x13312 11.1 vs
+    // 11.3 us).
+    constexpr bool SGN = TY == T_IQ3_S && NT >= GEMV_THREADS_LARGE;
+    constexpr int GT = SGN ? T_IQ3S_SGN : TY;
+    constexpr int GB = GridLDS<GT>::BYTES > 0 ? GridLDS<GT>::BYTES : 16;
     __shared__ __align__(16) uint8_t s_grid[GB];
     __shared__ __align__(16) uint8_t s_q8[FUSEQ ? MAX_NB * 292 : 16];
     // K-quant dots read the quants residue-major: quantized once per workgroup
@@ -79,7 +86,7 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     // weight loads issued after the prologue's; the other D - 1 steps go out
     // after the barrier.
     int it = blockIdx.x * GEMV_WAVES + wid;
-    const GridIn<TY> gin = grid_load<TY>();
+    const GridIn<GT, NT> gin = grid_load<GT, NT>();
     // The input blocks of the first QP quantize passes are loaded here, ahead
     // of the weights: a pass whose loads went out after the weight loads
     // would wait for the whole weight burst to land before the barrier.
@@ -107,7 +114,7 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
         load_slice(P, (uint32_t)(r * NB + L.b), po, L.part, w[0]);
     }
 
-    grid_store<TY>(gin, s_grid);
+    grid_store<GT, NT>(gin, s_grid);
     if constexpr (FUSEQ) {
 #pragma unroll
         for (int q = 0; q < QP; ++q)
@@ -133,6 +140,8 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     }
 
     using A = typename std::conditional<AL, ActIQL, ActOf<TY, LPU>>::type;
+    // IQ2_S with LDS activations computes its sign selectors in VALU.
+    using GR = typename std::conditional<SGN, Iq3SignedRef, GridRef<TY, AL>>::type;
     A act;
     if constexpr (AL) {
         act.q = s_q8q + L.b * RES_STRIDE;
@@ -150,7 +159,7 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
         // single wave's LDS round trips is the dot's critical path).
         constexpr int GB = D == 1 ? 0 : TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
         const float v =
-            row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8, A, AL>(w, act, on, L, s_grid, s_fold[wid],
+            row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8, A, GR>(w, act, on, L, s_grid, s_fold[wid],
                                                                  p.block_sums, (long long)r * NB + L.b);
         if (on && L.leader()) store_y(p, r, v);
     };

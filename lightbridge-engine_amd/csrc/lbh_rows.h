@@ -80,8 +80,9 @@ using WOf = typename std::conditional<Traits<TY>::KQ, WSliceKQ<TY, LPU>, WSlice<
 // the row value is returned in the row's leader lane (part 0, block 0).
 // block_sums (optional) receives the integer stage of unit u.  GB: codebook
 // lookups gathered per GB groups (slice_sum); FW: fold_terms.  Contains wave
-// barriers: every lane of the wave must call it.
-template <int TY, int LPU, int GB = 0, int FW = 16, class A = ActOf<TY, LPU>, bool VSEL = false>
+// barriers: every lane of the wave must call it.  GR: the codebook accessor
+// (GridRef, or Iq3SignedRef over the signed IQ3S table).
+template <int TY, int LPU, int GB = 0, int FW = 16, class A = ActOf<TY, LPU>, class GR = GridRef<TY>>
 __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const A &act, bool on,
                                          const LaneMap<LPU> &L, const void *grid, FoldLDS<TY> &f,
                                          int32_t *block_sums, long long u) {
@@ -126,7 +127,7 @@ __device__ __forceinline__ float row_dot(const WOf<TY, LPU> &w, const A &act, bo
         int32_t bs = 0;
         uint32_t dbits = 0;
         if (on) {
-            bs = slice_sum<LPU, GB>(w, act, GridRef<TY, VSEL>(grid));
+            bs = slice_sum<LPU, GB>(w, act, GR(grid));
             dbits = w.d;
         }
         bs = unit_reduce<LPU>(bs);
