@@ -272,8 +272,8 @@ lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_de
                          void *workspace_dev, size_t workspace_len);
 
 /* Bytes of the per-GPU static scratch that lbh_gemm_q8_k_noalloc stages its
- * activation tiles in (lbh_gemm_workspace_bytes(n_tokens, k) must not exceed
- * it: 896 tokens at k = 4096, 512 tokens up to k = 7168). */
+ * activation tiles in: lbh_gemm_workspace_bytes(n_tokens, k) must not exceed it,
+ * which admits up to 928 tokens at k = 4096 and 544 tokens at k = 7168. */
 #define LBH_NOALLOC_SCRATCH_BYTES (8u << 20)
 
 /* [async] lbh_gemm_q8_k without a workspace argument, for callers that cannot
@@ -423,7 +423,9 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *router, const float *
 /* [async] One MoE block decode step entirely on the device: router + top-k, then the
  * routed and shared experts (lbh_moe_forward semantics) reading the device routing.
  * Unchecked: x must be finite.  A routing the selection rejects (a non-finite logit,
- * or a router chain whose bounded wait gave up) leaves y unchanged. */
+ * or a router chain whose bounded wait gave up) leaves y unchanged and is recorded
+ * on the router for lbh_router_take_status, where route_experts_into returns the
+ * error (crates/bridge-model-hy3/src/routing.rs:72-77). */
 lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev, size_t top_k,
                                  int32_t mode, float weight_scale, float *y_dev);
 
@@ -435,6 +437,15 @@ lbh_status lbh_moe_block_forward(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router,
  * FFN input, hidden_dev the residual stream [hidden]. */
 lbh_status lbh_moe_block_forward_residual(lbh_ctx *ctx, lbh_moe *moe, lbh_router *router, const float *x_dev,
                                           size_t top_k, int32_t mode, float weight_scale, float *hidden_dev);
+
+/* [sync] What the block decodes on this router rejected since the last call, then
+ * cleared: waits for the context's stream.  *rejected (optional) receives the number
+ * of rejected steps.  Returns LBH_DEVICE_TIMEOUT if a router chain's bounded wait
+ * gave up, else LBH_NON_FINITE_VALUE for the first rejected step with
+ * route_experts_into's payload (expert index, value bits, field 8 logit / 9 bias /
+ * 10 selection score), else LBH_OK.  No counterpart in the reference, whose
+ * synchronous routing returns that error from the step itself (routing.rs:72-77). */
+lbh_status lbh_router_take_status(lbh_ctx *ctx, lbh_router *router, uint64_t *rejected, lbh_error *err);
 
 /* ---- HBM expert cache ---------------------------------------------------------
  * Counterpart of CompressedCache<ExpertKey> (crates/bridge-cache/src/lib.rs:32-595)

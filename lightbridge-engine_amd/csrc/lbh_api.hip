@@ -579,17 +579,12 @@ lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x, uint8
 lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, int32_t *out) {
     if (!ctx || !m || !q8 || !out) return LBH_NULL_ARGUMENT;
     DeviceGuard g(ctx->device);
-    float *y = nullptr;
-    if (hipMallocAsync(reinterpret_cast<void **>(&y), m->rows * sizeof(float), ctx->stream) != hipSuccess)
-        return LBH_HIP_ERROR;
     GemvArgs a{};
     a.m = view_of(m);
     a.q8 = q8;
-    a.y = y;
+    a.y = nullptr;   // the row values are not stored
     a.block_sums = out;
-    hipError_t e = launch_gemv(a, ctx->tuning, ctx->stream);
-    (void)hipFreeAsync(y, ctx->stream);
-    return e == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
+    return launch_gemv(a, ctx->tuning, ctx->stream) == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
 
 lbh_status lbh_validate_vec_dot_q8_k(lbh_ctx *ctx, int32_t ty, const uint8_t *weights, size_t weights_len,
@@ -751,7 +746,7 @@ struct lbh_moe {
     hipStream_t side1;
     hipEvent_t sev[2];
     float *d_shared;
-    int two_stream;           // 1: the async forwards use side1 (default), 0: one stream
+    int two_stream;           // 1: the async forwards use side1, 0: one stream (default, measured faster)
 };
 
 namespace {
@@ -1085,12 +1080,15 @@ lbh_status lbh_moe_forward_leased(lbh_ctx *ctx, lbh_moe *m, const lbh_expert_lea
         for (int k = 0; k < 3; ++k) a.routed_planes[i][k] = planes[k];
     }
     a.n_launch = (int32_t)n_routed;
+    // The slots are read on this call's stream, whichever stream the cache was
+    // created on: once the first launch that reads them is queued, every lease
+    // records that use, also when a later launch fails (a refill must wait for
+    // the queued reader).
     if (launch_moe_gate_up(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
-    if (launch_moe_down(a, ctx->stream) != hipSuccess) return LBH_HIP_ERROR;
-    // The slots are read on this call's stream, whichever stream the cache was created on.
-    for (size_t i = 0; i < n_routed; ++i)
-        if (!cache_note_use(m->cache, &leases[i], ctx->stream)) return LBH_HIP_ERROR;
-    return LBH_OK;
+    const bool down_ok = launch_moe_down(a, ctx->stream) == hipSuccess;
+    bool noted = true;
+    for (size_t i = 0; i < n_routed; ++i) noted = cache_note_use(m->cache, &leases[i], ctx->stream) && noted;
+    return down_ok && noted ? LBH_OK : LBH_HIP_ERROR;
 }
 
 lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs,
@@ -1604,7 +1602,10 @@ struct lbh_router {
     float *logits;
     MoeRoute *route;     // device
     MoeRoute *route_host;
-    unsigned long long *status;        // [0] first invalid selection input, [1] ring give-up (sticky)
+    // [0] first invalid selection input of route_into, [1] ring give-up of the
+    // block decodes (sticky until lbh_router_take_status), [2..4] their
+    // rejected selections (RouterArgs::reject), [5] ring give-up of route_into.
+    unsigned long long *status;
     unsigned long long *status_host;
     long long spin_limit;              // RouterArgs::spin_limit (0: default)
 };
@@ -1624,6 +1625,23 @@ void free_router(lbh_router *r) {
     delete r;
 }
 
+constexpr int ROUTER_STATUS_WORDS = 6;
+
+// NonFiniteValue of a rejected selection (routing.rs:72-77): `bad` as
+// select_route codes it ((expert << 2) | field: 0 logit, 1 bias, 2 selection
+// score), with that expert's logit and bias bits; the score is recomputed.
+lbh_status selection_error(unsigned long long bad, uint32_t logit_bits, uint32_t bias_bits, lbh_error *err) {
+    const uint64_t e = bad >> 2;
+    const uint32_t field = (uint32_t)(bad & 3);
+    float l, bv;
+    std::memcpy(&l, &logit_bits, 4);
+    std::memcpy(&bv, &bias_bits, 4);
+    const float v = field == 0 ? l : field == 1 ? bv : 1.0f / (1.0f + expf_libm(-l)) + bv;
+    uint32_t vb;
+    std::memcpy(&vb, &v, 4);
+    return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, e, 0, 0, vb, 8 + field);
+}
+
 RouterArgs router_args(const lbh_router *r, const float *x, size_t top_k, int32_t mode, float scale) {
     RouterArgs a{};
     a.w = r->w;
@@ -1638,6 +1656,7 @@ RouterArgs router_args(const lbh_router *r, const float *x, size_t top_k, int32_
     a.weight_scale = scale;
     a.spin_limit = r->spin_limit;
     a.timeout = r->status + 1;
+    a.reject = r->status + 2;
     return a;
 }
 
@@ -1681,9 +1700,11 @@ lbh_status lbh_router_create(lbh_ctx *ctx, const float *weights, size_t n_expert
     if (e == hipSuccess) e = hipMalloc(&r->logits, n_experts * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&r->route, sizeof(MoeRoute));
     if (e == hipSuccess) e = hipMemset(r->route, 0, sizeof(MoeRoute));
-    if (e == hipSuccess) e = hipMalloc(&r->status, 2 * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMalloc(&r->status, ROUTER_STATUS_WORDS * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemset(r->status, 0, ROUTER_STATUS_WORDS * sizeof(unsigned long long));
     if (e == hipSuccess) e = hipHostMalloc(&r->route_host, sizeof(MoeRoute), hipHostMallocDefault);
-    if (e == hipSuccess) e = hipHostMalloc(&r->status_host, 2 * sizeof(unsigned long long), hipHostMallocDefault);
+    if (e == hipSuccess)
+        e = hipHostMalloc(&r->status_host, ROUTER_STATUS_WORDS * sizeof(unsigned long long), hipHostMallocDefault);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         free_router(r);
@@ -1720,13 +1741,15 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, si
     DeviceGuard g(ctx->device);
     RouterArgs a = router_args(r, x, top_k, mode, weight_scale);
     a.status = r->status;
+    a.timeout = r->status + 5;   // the block decodes' give-up word stays for lbh_router_take_status
+    a.reject = nullptr;
     // The router matvec is gemv_into on an F32 matrix: its input must be finite (gemv.rs:195-211).
     HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
     HIP_TRY(launch_find_nonfinite(x, (long long)x_len, &ctx->status->first_bad_input, ctx->stream));
-    HIP_TRY(hipMemsetAsync(r->status + 1, 0, sizeof(unsigned long long), ctx->stream));
+    HIP_TRY(hipMemsetAsync(r->status + 5, 0, sizeof(unsigned long long), ctx->stream));
     HIP_TRY(launch_router(a, ctx->stream));
-    HIP_TRY(hipMemcpyAsync(r->status_host, r->status, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                           ctx->stream));
+    HIP_TRY(hipMemcpyAsync(r->status_host, r->status, ROUTER_STATUS_WORDS * sizeof(unsigned long long),
+                           hipMemcpyDeviceToHost, ctx->stream));
     HIP_TRY(hipMemcpyAsync(r->route_host, r->route, sizeof(MoeRoute), hipMemcpyDeviceToHost, ctx->stream));
     lbh_status st = read_status(ctx, err);
     if (st) return st;
@@ -1735,31 +1758,36 @@ lbh_status lbh_router_route_into(lbh_ctx *ctx, lbh_router *r, const float *x, si
         return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, i, 0, 0, read_f32_bits(ctx, x + i), 0);
     }
     // A router chain whose bounded ring wait gave up left NaN logits behind.
-    if (r->status_host[1] != 0) return fail(err, LBH_DEVICE_TIMEOUT, LBH_F32);
+    if (r->status_host[5] != 0) return fail(err, LBH_DEVICE_TIMEOUT, LBH_F32);
     const unsigned long long bad = r->status_host[0];
     if (bad != ~0ull) {
         const uint64_t e = bad >> 2;
-        const uint32_t field = (uint32_t)(bad & 3);   // 0 logit, 1 bias, 2 score
-        float v = 0.0f;
-        if (field == 0) {
-            uint32_t b = read_f32_bits(ctx, r->logits + e);
-            std::memcpy(&v, &b, 4);
-        } else {
-            uint32_t lb = read_f32_bits(ctx, r->logits + e), bb = read_f32_bits(ctx, r->bias + e);
-            float l, bv;
-            std::memcpy(&l, &lb, 4);
-            std::memcpy(&bv, &bb, 4);
-            v = field == 1 ? bv : 1.0f / (1.0f + expf_libm(-l)) + bv;
-        }
-        uint32_t vb;
-        std::memcpy(&vb, &v, 4);
-        return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, e, 0, 0, vb, 8 + field);
+        return selection_error(bad, read_f32_bits(ctx, r->logits + e), r->bias ? read_f32_bits(ctx, r->bias + e) : 0u,
+                               err);
     }
     for (size_t i = 0; i < top_k; ++i) {
         ids[i] = r->route_host->ids[i];
         coefs[i] = r->route_host->coefs[i];
     }
     if (logits_host) HIP_TRY(hipMemcpy(logits_host, r->logits, r->n_experts * sizeof(float), hipMemcpyDeviceToHost));
+    return ok(err);
+}
+
+lbh_status lbh_router_take_status(lbh_ctx *ctx, lbh_router *r, uint64_t *rejected, lbh_error *err) {
+    if (!ctx || !r) return fail(err, LBH_NULL_ARGUMENT);
+    if (rejected) *rejected = 0;
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipMemcpyAsync(r->status_host, r->status, ROUTER_STATUS_WORDS * sizeof(unsigned long long),
+                           hipMemcpyDeviceToHost, ctx->stream));
+    HIP_TRY(hipMemsetAsync(r->status + 1, 0, 4 * sizeof(unsigned long long), ctx->stream));
+    HIP_TRY(hipStreamSynchronize(ctx->stream));
+    const unsigned long long n = r->status_host[2];
+    if (rejected) *rejected = n;
+    if (r->status_host[1] != 0) return fail(err, LBH_DEVICE_TIMEOUT, LBH_F32);
+    if (n != 0) {
+        const unsigned long long v = r->status_host[4];
+        return selection_error(r->status_host[3], (uint32_t)v, (uint32_t)(v >> 32), err);
+    }
     return ok(err);
 }
 

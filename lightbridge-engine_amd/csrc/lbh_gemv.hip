@@ -32,6 +32,7 @@ __device__ __forceinline__ bool status_set(const DevStatus *st) {
 }
 
 __device__ __forceinline__ void store_y(const GemvArgs &p, int r, float v) {
+    if (!p.y) return;   // integer-stage export only (lbh_gemv_block_sums)
     if (p.accumulate)
         p.y[r] = __fadd_rn(p.y[r], __fmul_rn(p.coef, v));
     else

@@ -33,7 +33,7 @@ struct GemvArgs {
     const uint8_t *q8;            // (nb) Q8_K blocks, or NULL when x is given
     const float *x;               // f32 input quantized inside the kernel (q8 == NULL)
     uint8_t *q8_out;              // optional: the Q8_K bytes of x, written by workgroup 0
-    float *y;
+    float *y;                     // NULL: row values not stored (integer-stage export only)
     float coef;
     int32_t accumulate;
     int32_t *block_sums;          // optional integer-stage export
@@ -81,6 +81,10 @@ struct RouterArgs {
     // rejects the route) and sets *timeout to 1 (sticky; optional).
     long long spin_limit;
     unsigned long long *timeout;
+    // Optional record of the selections a block decode rejected (the routed
+    // gate/up kernel writes it): [0] rejected selections, [1] the first one's
+    // code (as `bad` of select_route), [2] its logit bits | bias bits << 32.
+    unsigned long long *reject;
 };
 
 // Device status of one MoE call (~0 when clean).

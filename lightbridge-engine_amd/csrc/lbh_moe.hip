@@ -254,6 +254,18 @@ struct SharedSlot {
     __device__ int order(int) const { return n; }
 };
 
+// Records a rejected selection for lbh_router_take_status: the count, and the
+// first rejection's code and its logit and bias bits.
+__device__ __noinline__ void note_rejection(const RouterArgs &r, unsigned long long bad) {
+    if (atomicAdd(r.reject, 1ull) == 0) {
+        const int e = (int)(bad >> 2);
+        const unsigned long long lb = __float_as_uint(r.logits[e]);
+        const unsigned long long bb = r.mode == 1 ? __float_as_uint(r.bias[e]) : 0u;
+        r.reject[1] = bad;
+        r.reject[2] = lb | (bb << 32);
+    }
+}
+
 // Workgroups [0, wg_s) stream the shared expert, the rest the routed experts.
 template <int TYR, int LPUR, int TYS, int LPUS>
 __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
@@ -289,7 +301,10 @@ __global__ void __launch_bounds__(MOE_THREADS) k_moe_gate_up(MoeArgs a) {
 #pragma unroll
                 for (int q = 0; q < MOE_MAX_ROUTED; ++q) s_ids[q] = r.ids[q];
                 s_invalid = bad != ~0ull;
-                if ((int)blockIdx.x == wg_s) *const_cast<MoeRoute *>(a.route_dev) = r;
+                if ((int)blockIdx.x == wg_s) {
+                    *const_cast<MoeRoute *>(a.route_dev) = r;
+                    if (bad != ~0ull && a.router.reject) note_rejection(a.router, bad);
+                }
             }
         }
         __syncthreads();
@@ -393,7 +408,7 @@ __global__ void __launch_bounds__(64 * DOWN_MAX_WAVES) k_moe_down(MoeArgs a) {
     // status words are read once the prologue's loads are out and acted on
     // after it (a non-finite input or SwiGLU, or an invalid device route,
     // leaves y unchanged), so no wait for them holds back a prologue load.
-    const int route_count = scalar_read(a.route_dev ? &a.route_dev->n : &a.route.n);
+    const int route_count = a.route_dev ? scalar_read(&a.route_dev->n) : a.route.n;
     // Wave index and route count through readfirstlane: the task choice below
     // (and every descriptor derived from it) is wave-uniform.
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

@@ -119,6 +119,7 @@ def lib() -> C.CDLL:
             "lbh_debug_expf_host": ([p, p, sz, i32, p], None),
             "lbh_router_create": ([p, p, sz, sz, p, i32, C.POINTER(p), E], i32),
             "lbh_router_destroy": ([p], i32),
+            "lbh_router_take_status": ([p, p, C.POINTER(C.c_uint64), E], i32),
             "lbh_router_set_spin_limit": ([p, C.c_int64], i32),
             "lbh_router_route_into": ([p, p, p, sz, sz, i32, C.c_float, p, p, p, E], i32),
             "lbh_moe_block_forward": ([p, p, p, p, sz, i32, C.c_float, p], i32),
@@ -442,6 +443,13 @@ class Router:
     def set_spin_limit(self, limit: int) -> None:
         """Polls of the router chains' bounded waits (0 default, < 0 give up at once: a test knob)."""
         lib().lbh_router_set_spin_limit(self.handle, limit)
+
+    def take_status(self) -> int:
+        """Rejected block-decode steps since the last call (then cleared); raises the first
+        rejection's error (DeviceTimeout or NonFiniteValue) like route_experts_into."""
+        n = C.c_uint64(0)
+        _call(lib().lbh_router_take_status, self.be.ctx, self.handle, C.byref(n))
+        return int(n.value)
 
     def close(self) -> None:
         if self.handle:

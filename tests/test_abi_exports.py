@@ -46,3 +46,17 @@ def test_oracle_is_not_linked_into_the_product():
     for src in (ROOT / "lightbridge-engine_amd").rglob("*"):
         if src.suffix in (".py", ".hip", ".h", ".cpp") and src.is_file():
             assert "lb_oracle" not in src.read_text(errors="ignore"), src
+
+
+def test_noalloc_scratch_limit_is_the_documented_token_count():
+    """lbh_gemm_q8_k_noalloc admits a batch while lbh_gemm_workspace_bytes(n, k) fits
+    LBH_NOALLOC_SCRATCH_BYTES: exactly 928 tokens at k = 4096 and 544 at k = 7168,
+    the limits the header states (host arithmetic, no GPU)."""
+    import lbhip
+    hb = lbhip.HipBackend
+    limit = hb.NOALLOC_SCRATCH_BYTES
+    text = (ROOT / "include" / "lightbridge_hip.h").read_text()
+    assert int(re.search(r"#define LBH_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)", text).group(1)) << 20 == limit
+    for k, n in ((4096, 928), (7168, 544)):
+        assert hb.gemm_workspace_bytes(n, k) <= limit < hb.gemm_workspace_bytes(n + 1, k)
+        assert f"{n} tokens at k = {k}" in text

@@ -119,10 +119,16 @@ def test_router_give_up_is_reported_and_leaves_the_output(be, oracle):
     with pytest.raises(lbhip.BackendError) as e:
         r.route_into(x, 2)
     assert e.value.variant == "DeviceTimeout"
+    assert r.take_status() == 0               # the synchronous route reported its own give-up
     sentinel = np.full(1024, 7.5, np.float32)
     y = dev(sentinel)
     lbhip.moe_block_forward(be, layer.moe, r, x, y, 2)
     assert _same(host(y), sentinel)
+    lbhip.moe_block_forward(be, layer.moe, r, x, y, 2)
+    with pytest.raises(lbhip.BackendError) as e:   # the async steps' give-up, reported once
+        r.take_status()
+    assert e.value.variant == "DeviceTimeout"
+    assert r.take_status() == 0               # cleared by the read
     r.set_spin_limit(0)                       # default bound: routes again, bit-exact
     ids, coefs = r.route_into(x, 2)
     want_ids, want_coefs = oracle.route_softmax_topk(oracle.router_logits_f32(w, x.cpu().numpy()), 2)
@@ -130,6 +136,34 @@ def test_router_give_up_is_reported_and_leaves_the_output(be, oracle):
     lbhip.moe_block_forward(be, layer.moe, r, x, y, 2)
     want, _ = layer.oracle_out(oracle, want_ids, want_coefs, x.cpu().numpy())
     assert _same(host(y), want)
+    assert r.take_status() == 0               # a clean step records nothing
+    r.close()
+
+
+def test_block_decode_rejection_is_reported_with_the_reference_error(be, oracle):
+    """A block step whose selection sees a non-finite bias leaves the output and
+    records the rejection: take_status raises route_experts_into's error
+    (routing.rs:72-77: NonFiniteValue, expert index and value bits) once, counting
+    every rejected step."""
+    import lbhip
+    layer = Layer(be, oracle, 8, 1024, 256, 512, (IQ2_S, IQ3_S, Q4_K, Q5_K), seed=331)
+    w = synth.router_weights(8, 1024, 332)
+    bias = (np.random.default_rng(333).standard_normal(8) * 0.1).astype(np.float32)
+    bias[5] = np.inf
+    r = lbhip.Router(be, w, bias)
+    xh = np.random.default_rng(334).standard_normal(1024).astype(np.float32)
+    sentinel = np.full(1024, -2.25, np.float32)
+    y = dev(sentinel)
+    for _ in range(3):
+        lbhip.moe_block_forward(be, layer.moe, r, dev(xh), y, 2, mode=1)
+    assert _same(host(y), sentinel)
+    with pytest.raises(lbhip.BackendError) as e:
+        r.take_status()
+    with pytest.raises(oracle.OracleError) as oe:
+        oracle.route_sigmoid_bias(oracle.router_logits_f32(w, xh), bias, 2, 1.0)
+    assert e.value.variant == "NonFiniteValue"
+    assert e.value.index == oe.value.index == 5 and e.value.bits == oe.value.bits
+    assert r.take_status() == 0
     r.close()
 
 
