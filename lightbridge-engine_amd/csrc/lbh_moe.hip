@@ -256,7 +256,7 @@ struct SharedSlot {
 
 // Records a rejected selection for lbh_router_take_status: the count, and the
 // first rejection's code and its logit and bias bits.
-__device__ __noinline__ void note_rejection(const RouterArgs &r, unsigned long long bad) {
+__device__ __forceinline__ void note_rejection(const RouterArgs &r, unsigned long long bad) {
     if (atomicAdd(r.reject, 1ull) == 0) {
         const int e = (int)(bad >> 2);
         const unsigned long long lb = __float_as_uint(r.logits[e]);
