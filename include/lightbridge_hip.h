@@ -134,7 +134,13 @@ lbh_status lbh_quantize_q8_k_rows(lbh_ctx *ctx, const float *input_dev, size_t r
  * the exact byte length and the finiteness of every block's f16 d (and dmin),
  * the checks validate_vec_dot_q8_k repeats per call (q8_k.rs:121-161,
  * k_quants.rs:178-208), and stores the bytes in HBM in the backend's lossless
- * device layout. */
+ * device layout.  F32 matrices (ggml_type 0: rows x k floats, k a multiple of
+ * 256, else LBH_UNSUPPORTED_SHAPE) serve lbh_gemv_into, lbh_gemv_accumulate_
+ * scaled_into and the lbh_gemv_dequant_* forms, which compute dot_f32_row for
+ * them in every mode (gemv.rs:88-101, :128-146, :286-303); the Q8_K entry
+ * points (lbh_gemv_q8_k, lbh_gemv_f32, lbh_gemv_q8_k_into, lbh_gemv_block_sums,
+ * the MoE layers, the GEMM) refuse them with LBH_UNSUPPORTED_TYPE, and
+ * lbh_matrix_create_streamed takes the quantized types only. */
 
 /* [sync] `bytes` is host memory when bytes_on_device == 0, device memory otherwise. */
 lbh_status lbh_matrix_create(lbh_ctx *ctx, int32_t ggml_type, size_t rows, size_t k, const void *bytes,
@@ -164,7 +170,12 @@ size_t lbh_matrix_bytes(const lbh_matrix *m);
 /* ---- matvec ------------------------------------------------------------------ */
 
 /* [sync] gemv_into(CpuParallelQ8K) (crates/bridge-kernels-reference/src/gemv.rs:56-70, :88-115):
- * output[r] = vec_dot_q8_k(row r, Q8_K(input)).  q8_scratch_dev holds >= (k/256)*292 bytes. */
+ * output[r] = vec_dot_q8_k(row r, Q8_K(input)).  q8_scratch_dev holds >= (k/256)*292 bytes.
+ * An F32 matrix takes gemv_cpu_parallel_f32_into (gemv.rs:72-86): output[r] =
+ * dot_f32_row(r), bit-identical, after prepare_dequant's checks (dimensions,
+ * finite input, finite weights: NonFiniteValue field 1, index 0, `row` and
+ * `actual` = the first non-finite weight's row and column); the Q8_K scratch is
+ * not used. */
 lbh_status lbh_gemv_into(lbh_ctx *ctx, const lbh_matrix *m, const float *input_dev, size_t input_len,
                          float *output_dev, size_t output_len, uint8_t *q8_scratch_dev, size_t q8_len,
                          lbh_error *err);

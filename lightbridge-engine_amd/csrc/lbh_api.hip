@@ -212,10 +212,58 @@ lbh_status lbh_quantize_q8_k_rows(lbh_ctx *ctx, const float *input, size_t rows,
 
 // -------------------------------------------------------------- matrices
 
+// An F32 matrix (the reference routes it to dot_f32_row in every mode,
+// gemv.rs:88-101, :128-146): stored in the router layout (w[(j * rows + r) * 4
+// + c] = row r, input 4j + c) so the sequential row chains read coalesced
+// lines; k must be a multiple of 256 (the chains' step), rows < 2^31.
+static lbh_status create_f32(lbh_ctx *ctx, size_t rows, size_t k, const void *bytes, size_t byte_len,
+                             int32_t on_device, lbh_matrix **out, lbh_error *err) {
+    if (k == 0) return fail(err, LBH_ZERO_LOGICAL_ELEMENTS, LBH_F32);
+    if (rows == 0) return fail(err, LBH_DIMENSION_MISMATCH, LBH_F32, 0, 1, 0);
+    if (rows > SIZE_MAX / 4 / k) return fail(err, LBH_ARITHMETIC_OVERFLOW, LBH_F32);
+    const size_t want = rows * k * 4;
+    if (byte_len != want) return fail(err, LBH_ENCODED_LENGTH_MISMATCH, LBH_F32, 0, want, byte_len);
+    if (!bytes) return fail(err, LBH_NULL_ARGUMENT);
+    if (k % 256 || rows > 0x7ffffff0ull) return fail(err, LBH_UNSUPPORTED_SHAPE, LBH_F32, 0, 256, k);
+    DeviceGuard g(ctx->device);
+    uint8_t *staging = nullptr, *planes = nullptr;
+    const uint8_t *src = static_cast<const uint8_t *>(bytes);
+    hipError_t e = hipMalloc(&planes, want);
+    if (e == hipSuccess && !on_device) {
+        e = hipMalloc(&staging, want);
+        if (e == hipSuccess) e = hipMemcpyAsync(staging, bytes, want, hipMemcpyHostToDevice, ctx->stream);
+        src = staging;
+    }
+    if (e == hipSuccess)
+        e = launch_f32_layout(reinterpret_cast<const float *>(src), reinterpret_cast<float *>(planes), (long long)rows,
+                              (long long)k, 1, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (staging) (void)hipFree(staging);
+    if (e != hipSuccess) {
+        if (planes) (void)hipFree(planes);
+        return hip_fail(err, e);
+    }
+    lbh_matrix *m = new (std::nothrow) lbh_matrix();
+    if (!m) {
+        (void)hipFree(planes);
+        return fail(err, LBH_HIP_ERROR);
+    }
+    m->device = ctx->device;
+    m->type = LBH_F32;
+    m->rows = rows;
+    m->k = k;
+    m->nb = k / 256;
+    m->planes = planes;
+    m->bytes = want;
+    *out = m;
+    return ok(err);
+}
+
 lbh_status lbh_matrix_create(lbh_ctx *ctx, int32_t ty, size_t rows, size_t k, const void *bytes, size_t byte_len,
                              int32_t on_device, lbh_matrix **out, lbh_error *err) {
     if (!ctx || !out) return fail(err, LBH_NULL_ARGUMENT);
     *out = nullptr;
+    if (ty == LBH_F32) return create_f32(ctx, rows, k, bytes, byte_len, on_device, out, err);
     if (!is_dot_type(ty)) return fail(err, LBH_UNSUPPORTED_TYPE, ty);
     lbh_status st = check_elements(ty, k, err);
     if (st) return st;
@@ -387,7 +435,10 @@ lbh_status lbh_matrix_read_ggml(lbh_ctx *ctx, const lbh_matrix *m, void *host, s
     DeviceGuard g(ctx->device);
     uint8_t *tmp = nullptr;
     HIP_TRY(hipMalloc(&tmp, m->bytes));
-    hipError_t e = launch_repack(m->type, m->planes, tmp, (long long)(m->rows * m->nb), 0, ctx->stream);
+    hipError_t e = m->type == LBH_F32
+                       ? launch_f32_layout(reinterpret_cast<const float *>(m->planes), reinterpret_cast<float *>(tmp),
+                                           (long long)m->rows, (long long)m->k, 0, ctx->stream)
+                       : launch_repack(m->type, m->planes, tmp, (long long)(m->rows * m->nb), 0, ctx->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(host, tmp, m->bytes, hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     (void)hipFree(tmp);
@@ -456,11 +507,57 @@ lbh_status scan_verdict(lbh_ctx *ctx, int ty, const float *input, const float *o
     return ok(err);
 }
 
+// The sequential row chains of an F32 matrix (dot_f32_row, gemv.rs:286-303),
+// optionally accumulating (gemv.rs:161-171); skip_if as RouterArgs.
+hipError_t launch_f32_gemv(lbh_ctx *ctx, const lbh_matrix *m, const float *x, float *y, float coef, int accumulate,
+                           const DevStatus *skip_if) {
+    RouterArgs a{};
+    a.w = reinterpret_cast<const float *>(m->planes);
+    a.x = x;
+    a.logits = y;
+    a.n_experts = (int32_t)m->rows;
+    a.hidden = (int32_t)m->k;
+    a.accumulate = accumulate;
+    a.coef = coef;
+    a.skip_if = skip_if;
+    a.timeout = &ctx->status->pad;   // a chain whose bounded wait gave up
+    return launch_f32_chains(a, ctx->stream);
+}
+
+// gemv_into / gemv_accumulate_scaled_into / the DequantF32 forms on an F32
+// matrix (every mode computes dot_f32_row, gemv.rs:88-101, :128-146): the
+// accumulate checks and validate_dimensions as check_gemv_args, then
+// prepare_dequant's finite-weight check in row-major order (gemv.rs:230-240:
+// NonFiniteValue "GEMV weights", index 0 of the one-element decoded block;
+// `row` and `actual` give the weight's row and column), then the chains.
+lbh_status f32_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
+                       size_t out_len, int accumulate, float scale, lbh_error *err) {
+    DeviceGuard g(ctx->device);
+    lbh_status st = check_gemv_args(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
+    if (st) return st;
+    HIP_TRY(launch_find_nonfinite_f32w(reinterpret_cast<const float *>(m->planes), (long long)m->rows, (long long)m->k,
+                                       &ctx->status->first_bad_scale, ctx->stream));
+    HIP_TRY(launch_f32_gemv(ctx, m, input, out, scale, accumulate, ctx->status));
+    st = scan_verdict(ctx, LBH_F32, input, out, err);
+    if (st) return st;
+    const unsigned long long w = ctx->status_host->first_bad_scale;
+    if (w != ~0ull) {
+        const uint64_t r = w / m->k, c = w % m->k;
+        const uint32_t bits = read_f32_bits(ctx, reinterpret_cast<const float *>(m->planes) +
+                                                      ((c / 4) * m->rows + r) * 4 + c % 4);
+        return fail(err, LBH_NON_FINITE_VALUE, LBH_F32, 0, 0, c, bits, 1, r);
+    }
+    if (ctx->status_host->pad != 0) return fail(err, LBH_DEVICE_TIMEOUT, LBH_F32);
+    return ok(err);
+}
+
 // prepare_llama_q8k (crates/bridge-kernels-reference/src/gemv.rs:245-272) minus the
 // per-row scale scan, which matrix upload performed once.
 lbh_status gemv_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
                         size_t out_len, uint8_t *q8, size_t q8_len, int accumulate, float scale, lbh_error *err) {
     if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    // F32: dot_f32_row in every mode; the Q8_K scratch is not used (gemv.rs:88-101).
+    if (m->type == LBH_F32) return f32_checked(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
     DeviceGuard g(ctx->device);
     lbh_status st = check_gemv_args(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
     if (st) return st;
@@ -552,6 +649,7 @@ lbh_status lbh_gemv_accumulate_scaled_into(lbh_ctx *ctx, const lbh_matrix *m, co
 lbh_status lbh_gemv_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, float *y, float coef,
                          int32_t accumulate) {
     if (!ctx || !m || !q8 || !y) return LBH_NULL_ARGUMENT;
+    if (!is_dot_type(m->type)) return LBH_UNSUPPORTED_TYPE;   // F32: lbh_gemv_into / lbh_gemv_dequant_*
     DeviceGuard g(ctx->device);
     GemvArgs a{};
     a.m = view_of(m);
@@ -565,6 +663,7 @@ lbh_status lbh_gemv_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, f
 lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x, uint8_t *q8_out, float *y, float coef,
                         int32_t accumulate) {
     if (!ctx || !m || !x || !y) return LBH_NULL_ARGUMENT;
+    if (!is_dot_type(m->type)) return LBH_UNSUPPORTED_TYPE;   // F32: lbh_gemv_into / lbh_gemv_dequant_*
     DeviceGuard g(ctx->device);
     GemvArgs a{};
     a.m = view_of(m);
@@ -578,6 +677,7 @@ lbh_status lbh_gemv_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *x, uint8
 
 lbh_status lbh_gemv_block_sums(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, int32_t *out) {
     if (!ctx || !m || !q8 || !out) return LBH_NULL_ARGUMENT;
+    if (!is_dot_type(m->type)) return LBH_UNSUPPORTED_TYPE;   // F32: lbh_gemv_into / lbh_gemv_dequant_*
     DeviceGuard g(ctx->device);
     GemvArgs a{};
     a.m = view_of(m);
@@ -603,6 +703,7 @@ lbh_status lbh_vec_dot_q8_k_into(lbh_ctx *ctx, int32_t ty, const uint8_t *weight
 lbh_status lbh_gemv_q8_k_into(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8, size_t q8_len, float *y,
                               size_t y_len, float coef, int32_t accumulate, lbh_error *err) {
     if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    if (!is_dot_type(m->type)) return fail(err, LBH_UNSUPPORTED_TYPE, m->type);   // prepare_llama_q8k, gemv.rs:252-257
     if (accumulate && !std::isfinite(coef)) {
         uint32_t bits;
         std::memcpy(&bits, &coef, 4);
@@ -653,6 +754,7 @@ lbh_status lbh_gemv_q8_k_into(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *
 static lbh_status dequant_checked(lbh_ctx *ctx, const lbh_matrix *m, const float *input, size_t input_len, float *out,
                                   size_t out_len, int accumulate, float scale, lbh_error *err) {
     if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    if (m->type == LBH_F32) return f32_checked(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
     DeviceGuard g(ctx->device);
     lbh_status st = check_gemv_args(ctx, m, input, input_len, out, out_len, accumulate, scale, err);
     if (st) return st;
@@ -675,9 +777,9 @@ lbh_status lbh_gemv_dequant_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *
                                 int32_t accumulate) {
     if (!ctx || !m || !x || !y) return LBH_NULL_ARGUMENT;
     DeviceGuard g(ctx->device);
-    return launch_gemv_dequant(view_of(m), x, y, coef, accumulate, nullptr, ctx->stream) == hipSuccess
-               ? LBH_OK
-               : LBH_HIP_ERROR;
+    const hipError_t e = m->type == LBH_F32 ? launch_f32_gemv(ctx, m, x, y, coef, accumulate, nullptr)
+                                            : launch_gemv_dequant(view_of(m), x, y, coef, accumulate, nullptr, ctx->stream);
+    return e == hipSuccess ? LBH_OK : LBH_HIP_ERROR;
 }
 
 lbh_status lbh_debug_empty_kernel(lbh_ctx *ctx) {

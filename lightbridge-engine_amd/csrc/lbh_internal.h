@@ -74,7 +74,12 @@ struct RouterArgs {
     unsigned long long *status; // optional: (first bad expert << 2) | field
     int32_t n_experts, hidden, top_k, mode;
     float weight_scale;
-    int32_t pad;
+    // F32 matvec use of the chains (lbh_gemv_* on an F32 matrix): accumulate
+    // != 0 stores logits[e] + coef * sum (gemv_accumulate_scaled_into), and
+    // skip_if (optional) suppresses the stores when a validation scan fired.
+    int32_t accumulate;
+    float coef;
+    const DevStatus *skip_if;
     // Bounded waits of the router chains' LDS ring: polls before giving up
     // (0: the default 2^22; < 0: give up at once, a host-forced test of that
     // path).  A chain that gives up stores a NaN logit (the selection then
@@ -244,6 +249,17 @@ bool batch_types_supported(int gate_r, int down_r, int gate_s, int down_s);
 
 hipError_t launch_router(const RouterArgs &a, hipStream_t s);
 hipError_t launch_router_logits(const RouterArgs &a, hipStream_t s);
+// The router chains over any number of rows: output[r] = dot_f32_row(r, x)
+// of an F32 matrix in the router layout (rows <= 2^31 - 8, k % 256 == 0).
+hipError_t launch_f32_chains(const RouterArgs &a, hipStream_t s);
+// F32 matrix [rows, k] between GGML row-major order and the router layout
+// (w[(j * rows + r) * 4 + c] = row r, input 4j + c); to_device selects the
+// direction.  k % 4 == 0.
+hipError_t launch_f32_layout(const float *src, float *dst, long long rows, long long k, int to_device, hipStream_t s);
+// First non-finite weight of an F32 matrix in the router layout, as the
+// row-major index r * k + i (atomicMin into *first).
+hipError_t launch_find_nonfinite_f32w(const float *w, long long rows, long long k, unsigned long long *first,
+                                      hipStream_t s);
 hipError_t launch_moe_router_shared(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_gate_up(const MoeArgs &a, hipStream_t s);
 hipError_t launch_moe_down(const MoeArgs &a, hipStream_t s);

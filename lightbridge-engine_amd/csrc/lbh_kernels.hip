@@ -25,6 +25,31 @@ __global__ void k_find_nonfinite(const float *__restrict__ x, long long n, unsig
     }
 }
 
+// One thread per (row, group of four inputs).
+__global__ void k_f32_layout(const float *__restrict__ src, float *__restrict__ dst, long long rows, long long k,
+                             int to_device) {
+    const long long k4 = k / 4, n = rows * k4;
+    for (long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (long long)gridDim.x * blockDim.x) {
+        const long long j = t / rows, r = t - j * rows;   // consecutive threads: consecutive rows of one group
+        const long long g = r * k + 4 * j, d = (j * rows + r) * 4;
+        if (to_device)
+            *reinterpret_cast<float4 *>(dst + d) = *reinterpret_cast<const float4 *>(src + g);
+        else
+            *reinterpret_cast<float4 *>(dst + g) = *reinterpret_cast<const float4 *>(src + d);
+    }
+}
+
+__global__ void k_find_nonfinite_f32w(const float *__restrict__ w, long long rows, long long k,
+                                      unsigned long long *first) {
+    const long long n = rows * k;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x) {
+        if ((__float_as_uint(w[i]) & 0x7f800000u) == 0x7f800000u) {
+            const long long q = i / 4, c = i - 4 * q, j = q / rows, r = q - j * rows;
+            atomicMin(first, (unsigned long long)(r * k + 4 * j + c));
+        }
+    }
+}
+
 __global__ void k_reset_status(DevStatus *st) {
     if (threadIdx.x == 0) {
         st->first_bad_input = ~0ull;
@@ -188,6 +213,23 @@ hipError_t launch_find_nonfinite(const float *x, long long n, unsigned long long
     int grid = cdiv(n, 256);
     grid = grid > 4096 ? 4096 : grid;
     hipLaunchKernelGGL(k_find_nonfinite, dim3(grid), dim3(256), 0, s, x, n, first);
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_layout(const float *src, float *dst, long long rows, long long k, int to_device, hipStream_t s) {
+    if (rows <= 0 || k <= 0 || k % 4) return hipErrorInvalidValue;
+    long long grid = (rows * (k / 4) + 255) / 256;
+    grid = grid > 65536 ? 65536 : grid;
+    hipLaunchKernelGGL(k_f32_layout, dim3((int)grid), dim3(256), 0, s, src, dst, rows, k, to_device);
+    return hipGetLastError();
+}
+
+hipError_t launch_find_nonfinite_f32w(const float *w, long long rows, long long k, unsigned long long *first,
+                                      hipStream_t s) {
+    if (rows <= 0 || k <= 0) return hipSuccess;
+    long long grid = (rows * k + 255) / 256;
+    grid = grid > 4096 ? 4096 : grid;
+    hipLaunchKernelGGL(k_find_nonfinite_f32w, dim3((int)grid), dim3(256), 0, s, w, rows, k, first);
     return hipGetLastError();
 }
 

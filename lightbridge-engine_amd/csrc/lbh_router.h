@@ -184,7 +184,12 @@ __device__ __forceinline__ void router_chain_wg(const RouterArgs &a, int e0, uin
             }
         }
         if (!ok) sum = __int_as_float(0x7fc00000);
-        if (lane < RT_EXPERTS && e0 + lane < n) a.logits[e0 + lane] = sum;
+        const bool skip = a.skip_if && (a.skip_if->first_bad_input != ~0ull || a.skip_if->first_bad_dest != ~0ull ||
+                                        a.skip_if->first_bad_scale != ~0ull);
+        if (lane < RT_EXPERTS && e0 + lane < n && !skip) {
+            float *o = a.logits + e0 + lane;
+            *o = a.accumulate ? __fadd_rn(*o, __fmul_rn(a.coef, sum)) : sum;   // gemv.rs:161-171
+        }
     }
 }
 

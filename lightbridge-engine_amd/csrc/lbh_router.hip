@@ -43,6 +43,12 @@ hipError_t launch_router_logits(const RouterArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+hipError_t launch_f32_chains(const RouterArgs &a, hipStream_t s) {
+    if (a.n_experts < 1 || a.n_experts > 0x7ffffff0 || a.hidden < 256 || a.hidden % 256) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_router_logits, dim3((a.n_experts + RT_EXPERTS - 1) / RT_EXPERTS), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_router(const RouterArgs &a, hipStream_t s) {
     if (a.n_experts < 1 || a.n_experts > 256 || a.top_k < 1 || a.top_k > MOE_MAX_ROUTED || a.top_k > a.n_experts ||
         a.hidden % 256)

@@ -560,7 +560,7 @@ class DeviceMatrix:
             _call(lib().lbh_matrix_create, be.ctx, ty, rows, k, C.c_void_p(data.data_ptr()), data.numel(), 1,
                   C.byref(h))
         else:
-            arr = np.ascontiguousarray(data, dtype=np.uint8)
+            arr = np.ascontiguousarray(data).reshape(-1).view(np.uint8)   # the GGML bytes (F32: the floats' bytes)
             _call(lib().lbh_matrix_create, be.ctx, ty, rows, k, C.c_void_p(arr.ctypes.data), arr.size, 0,
                   C.byref(h))
         self.handle = h

@@ -219,7 +219,7 @@ def test_non_finite_weight_scale_is_rejected_at_upload(be, ty, field):
 def test_upload_shape_errors(be):
     import lbhip
     with pytest.raises(lbhip.QuantError, match="UnsupportedType"):
-        be.upload(0, 1, 256, np.zeros(1024, np.uint8))
+        be.upload(1, 1, 256, np.zeros(512, np.uint8))      # F16: not a matrix type of the path
     with pytest.raises(lbhip.QuantError, match="EncodedLengthMismatch"):
         be.upload(Q4_K, 2, 256, np.zeros(143, np.uint8))
     with pytest.raises(lbhip.QuantError, match="LogicalElementsNotDivisible"):
