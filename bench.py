@@ -54,6 +54,7 @@ MOE_WEIGHT_BYTES = (TOP_K * (2 * FFN * 16 * 82 + HIDDEN * 6 * 110) + 2 * HIDDEN 
 EXPERT_BYTES = 2 * FFN * 16 * 82 + HIDDEN * 6 * 110                    # 6,733,824 per routed expert
 SHARED_BYTES = 2 * HIDDEN * 16 * 144 + HIDDEN * 16 * 176               # 30,408,704
 BATCH_TOKENS = 64
+COLD_COPIES = 8
 # HBM bytes per launch (read + write) measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain copy of
 # known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
@@ -165,8 +166,11 @@ def host_cpu():
 
 
 def _cpu_fields(threads):
-    d = {"cores": threads, "threads": threads}
+    d = {"threads": threads}
     d.update(host_cpu())
+    d["cores"] = min(threads, d["physical_cores"] or threads)
+    d["cores_note"] = ("physical cores the timed threads can occupy: min(threads, physical cores in this "
+                       "process's CPU affinity); threads are not pinned")
     return d
 
 
@@ -419,6 +423,31 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
     timer.time(g_dev, 1)
     us_dev = timer.time(g_dev, reps) / (reps * T) * 1e6
     spread_host, spread_dev = timer.spread(g_host, 11, T), timer.spread(g_dev, 11, T)
+    del g_host, g_dev
+
+    # Cold figure: token i reads shared expert and router copy i % COLD_COPIES
+    # (8 x 33.5 MB in rotation, beyond the 256 MB Infinity Cache), so neither is
+    # served from a cache that a single copy re-read every token would hit.
+    cold_layers = [(be.moe_create(experts, tuple(be.upload(ty, HIDDEN, HIDDEN, w)
+                                                 for ty, w in zip((synth.Q4_K, synth.Q4_K, synth.Q5_K), shared_np))),
+                    lbhip.Router(be, router_w)) for _ in range(COLD_COPIES)]
+    cold = lambda i: cold_layers[i % COLD_COPIES]  # noqa: E731
+    g_host_c = timer.graph(lambda: [be.moe_forward(cold(i)[0], routes[i][0], routes[i][1], xs[i], ys[i])
+                                    for i in range(T)])
+    timer.time(g_host_c, 1)
+    us_host_c = timer.time(g_host_c, reps) / (reps * T) * 1e6
+    g_dev_c = timer.graph(lambda: [lbhip.moe_block_forward(be, cold(i)[0], cold(i)[1], xs[i], ys[i], TOP_K)
+                                   for i in range(T)])
+    timer.time(g_dev_c, 1)
+    us_dev_c = timer.time(g_dev_c, reps) / (reps * T) * 1e6
+    del g_host_c, g_dev_c
+    torch.cuda.synchronize()
+    for layer, r in cold_layers:
+        shared_c = layer._keep[1]
+        layer.close()
+        r.close()
+        for m in shared_c:
+            m.close()
 
     torch.cuda.synchronize()
     host = lambda t: t.cpu().numpy()  # noqa: E731
@@ -431,6 +460,15 @@ def bench_moe(args, be, timer, torch, np, synth, lbhip):
            "with_device_router": {"us_per_token": round(us_dev, 2), "tokens_per_s": round(1e6 / us_dev, 1),
                                   "GB/s": round(MOE_WEIGHT_BYTES / us_dev / 1e3, 1),
                                   "per_replay_spread": spread_dev},
+           "cold_shared_and_router": {
+               "what": f"token i reads shared-expert and router copy i % {COLD_COPIES} "
+                       f"({COLD_COPIES} x {(SHARED_BYTES + N_EXPERTS * HIDDEN * 4) / 1e6:.1f} MB in rotation); "
+                       "the figures above re-read one copy every token",
+               "routing_given_us_per_token": round(us_host_c, 2),
+               "routing_given_GB/s": round((MOE_WEIGHT_BYTES - N_EXPERTS * HIDDEN * 4) / us_host_c / 1e3, 1),
+               "with_device_router_us_per_token": round(us_dev_c, 2),
+               "with_device_router_GB/s": round(MOE_WEIGHT_BYTES / us_dev_c / 1e3, 1),
+               "with_device_router_roofline_frac": round(MOE_WEIGHT_BYTES / us_dev_c / 1e3 / HBM_PEAK_GBS, 4)},
            "algorithmic_weight_bytes_per_token": MOE_WEIGHT_BYTES}
     state = dict(experts_np=experts_np, shared_np=shared_np, router_w=router_w, xs_np=xs_np,
                  last_y=host(ys[T - 1]), moe=moe, router=router, experts=experts, shared=shared)

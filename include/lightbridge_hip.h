@@ -61,6 +61,8 @@ typedef enum lbh_status {
     LBH_NULL_ARGUMENT = 101,
     LBH_UNSUPPORTED_SHAPE = 102,
     LBH_DEVICE_TIMEOUT = 103,   /* a bounded in-kernel wait gave up (the result was discarded) */
+    LBH_SCRATCH_IN_USE = 104,   /* lbh_gemm_q8_k_noalloc: the GPU's static scratch is still in use by a
+                                   call on another stream */
 } lbh_status;
 
 /* Error payload: the fields of the corresponding QuantError/KernelError variant. */
@@ -107,7 +109,9 @@ enum lbh_tuning_key {
     LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop (0: resident x CUs) */
     LBH_TUNE_GEMM_SHAPE = 3,       /* K-quant GEMM tile staging: 0 = through registers, two blocks ahead;
                                       1 = direct buffer-to-LDS loads, one block ahead */
-    LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 2, 3 or 4 */
+    LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 1, 2, 3 or 4; 1 runs the
+                                      one-lane-per-unit IQ instances as 1024-thread workgroups with
+                                      the activations in LDS (the default for large IQ shapes) */
 };
 lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value);
 /* Compute units of the context's device. */
@@ -294,8 +298,11 @@ lbh_status lbh_gemm_q8_k(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_de
  * LBH_NOALLOC_SCRATCH_BYTES that each GPU holds from library load to process
  * end.  Calls whose tiles exceed it fail with LBH_SCRATCH_TOO_SMALL (expected =
  * bytes needed, actual = the limit).  Every call on one GPU uses that GPU's one
- * array: calls that overlap on one GPU (other streams, other contexts) race and
- * must be ordered by the caller. */
+ * array.  An eager call on a stream other than the last eager call's, while
+ * that call has not finished, is refused with LBH_SCRATCH_IN_USE (nothing is
+ * launched; actual = n_tokens); calls on one stream are ordered by it.  Calls
+ * recorded under stream capture are not checked: replays of graphs that hold
+ * this call must not overlap other uses of the array on the same GPU. */
 lbh_status lbh_gemm_q8_k_noalloc(lbh_ctx *ctx, const lbh_matrix *m, const uint8_t *q8_dev, size_t n_tokens,
                                  float *y_dev, lbh_error *err);
 

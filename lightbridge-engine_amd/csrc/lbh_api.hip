@@ -34,13 +34,28 @@ constexpr int MAX_DEVICES = 64;
 std::mutex g_scratch_mu;
 uint8_t *g_scratch_ptr[MAX_DEVICES];
 
+// Use guard of a device's scratch: the stream of the last eager call and an
+// event recorded after its launches (created with the lookup, kept until the
+// process ends, as the array is).  A call on another stream while that event
+// is pending would overwrite tiles the earlier GEMM may still read.
+struct ScratchUse {
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool pending = false;
+};
+ScratchUse g_scratch_use[MAX_DEVICES];
+
 hipError_t scratch_of_device(int device, uint8_t **out) {
     if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     if (!g_scratch_ptr[device]) {
         void *p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
+        if (!g_scratch_use[device].done) {
+            e = hipEventCreateWithFlags(&g_scratch_use[device].done, hipEventDisableTiming);
+            if (e != hipSuccess) return e;
+        }
         g_scratch_ptr[device] = static_cast<uint8_t *>(p);
     }
     *out = g_scratch_ptr[device];
@@ -1381,8 +1396,31 @@ lbh_status lbh_gemm_q8_k_noalloc(lbh_ctx *ctx, const lbh_matrix *m, const uint8_
     const size_t need = gemm_b_bytes((int)n_tokens, (int)m->nb);
     if (need > LBH_NOALLOC_SCRATCH_BYTES)
         return fail(err, LBH_SCRATCH_TOO_SMALL, LBH_Q8_K, n_tokens, need, LBH_NOALLOC_SCRATCH_BYTES);
+    // Eager calls: refuse a call on another stream while the last one is
+    // pending, then mark this one.  Under stream capture nothing runs yet and
+    // events may be neither queried nor recorded: the caller orders replays.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    const hipError_t ce = hipStreamIsCapturing(ctx->stream, &cap);
+    if (ce != hipSuccess) return hip_fail(err, ce);
+    const bool eager = cap == hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    ScratchUse &use = g_scratch_use[ctx->device];
+    if (eager && use.pending && use.last != ctx->stream) {
+        const hipError_t q = hipEventQuery(use.done);
+        if (q == hipErrorNotReady) return fail(err, LBH_SCRATCH_IN_USE, LBH_Q8_K, 0, 0, n_tokens);
+        if (q != hipSuccess) return hip_fail(err, q);
+        use.pending = false;
+    }
     const lbh_status st = gemm_q8_k_into(ctx, m, q8, n_tokens, y, ctx->scratch);
-    return st == LBH_OK ? ok(err) : fail(err, st);
+    if (st != LBH_OK) return fail(err, st);
+    if (eager) {
+        DeviceGuard g(ctx->device);
+        const hipError_t re = hipEventRecord(use.done, ctx->stream);
+        if (re != hipSuccess) return hip_fail(err, re);
+        use.last = ctx->stream;
+        use.pending = true;
+    }
+    return ok(err);
 }
 
 }  // extern "C"

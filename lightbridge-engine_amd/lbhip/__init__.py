@@ -30,7 +30,7 @@ STATUS = {
     20: "DimensionMismatch", 21: "ScratchTooSmall", 22: "NonFiniteValue",
     23: "RoutedExpertOrder", 24: "DuplicateRoutedExpert", 25: "InvalidParameter",
     36: "SourceReadFailed",
-    100: "HipError", 101: "NullArgument", 102: "UnsupportedShape", 103: "DeviceTimeout",
+    100: "HipError", 101: "NullArgument", 102: "UnsupportedShape", 103: "DeviceTimeout", 104: "ScratchInUse",
 }
 QUANT_ERRORS = {1, 2, 3, 4, 6, 7, 8, 9, 10}
 
@@ -320,7 +320,8 @@ class HipBackend:
 
     def gemm_q8_k_noalloc(self, m: "DeviceMatrix", q8, n_tokens: int, y) -> None:
         """gemm_q8_k staging its activation tiles in the library's static per-GPU
-        scratch (no workspace, no allocation); calls on one GPU must not overlap."""
+        scratch (no workspace, no allocation); an eager call on another stream
+        while the last one is pending raises ScratchInUse."""
         _call(lib().lbh_gemm_q8_k_noalloc, self.ctx, m.handle, _dev_ptr(q8), n_tokens, _dev_ptr(y))
 
     NOALLOC_SCRATCH_BYTES = 8 << 20

@@ -76,3 +76,40 @@ def test_noalloc_gemm_refuses_batches_beyond_the_scratch(be):
     torch.cuda.synchronize()
     assert bool((y == 0.0).all())                  # zero activations: every dot is 0
     m.close()
+
+
+def test_noalloc_gemm_refuses_an_overlapping_call_on_another_stream(be):
+    """A call queued on stream 1 behind a long (bounded) spin still holds the
+    scratch: a call on stream 2 is refused with ScratchInUse and launches
+    nothing; once stream 1 has finished, stream 2's call runs and gives the
+    same result."""
+    import lbhip
+    n, rows, k = 64, 256, 4096
+    m = be.upload(Q5_K, rows, k, synth.random_matrix(Q5_K, rows, k, seed=930))
+    m.prepare_gemm()
+    q8h = np.random.default_rng(931).integers(0, 256, (n * 16, 292), dtype=np.uint8)
+    q8h[:, :4] = np.array([0.01], np.float32).view(np.uint8)                  # finite d
+    q8 = torch.from_numpy(q8h.reshape(-1)).cuda()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    y1 = torch.full((n, rows), float("nan"), device="cuda")
+    y2 = torch.full((n, rows), 5.0, device="cuda")
+    torch.cuda.synchronize()
+    try:
+        be.set_stream(s1)
+        with torch.cuda.stream(s1):
+            torch.cuda._sleep(200_000_000)          # a bounded spin: ~0.1 s at the shader clock
+        be.gemm_q8_k_noalloc(m, q8, n, y1)
+        be.set_stream(s2)
+        with pytest.raises(lbhip.BackendError) as e:
+            be.gemm_q8_k_noalloc(m, q8, n, y2)
+        assert e.value.variant == "ScratchInUse" and e.value.actual == n
+        s1.synchronize()
+        assert bool((y2 == 5.0).all())
+        be.gemm_q8_k_noalloc(m, q8, n, y2)
+        s2.synchronize()
+        assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+        assert bool(torch.isfinite(y1).all())
+    finally:
+        torch.cuda.synchronize()
+        be.set_stream(torch.cuda.current_stream())
+        m.close()
