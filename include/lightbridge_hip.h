@@ -107,8 +107,10 @@ lbh_status lbh_ctx_set_stream(lbh_ctx *ctx, void *stream);
 enum lbh_tuning_key {
     LBH_TUNE_GEMV_LPU = 1,         /* lanes per (row, block) unit: 1, 2 or 4 */
     LBH_TUNE_GEMV_MAX_BLOCKS = 2,  /* workgroup cap of the persistent matvec row loop (0: resident x CUs) */
-    LBH_TUNE_GEMM_SHAPE = 3,       /* K-quant GEMM tile staging: 0 = through registers, two blocks ahead;
-                                      1 = direct buffer-to-LDS loads, one block ahead */
+    LBH_TUNE_GEMM_SHAPE = 3,       /* K-quant GEMM schedule: 0 = default (3 from 97 tokens, else 2);
+                                      1 = 2 x 2 tiles of 32 x 32, direct buffer-to-LDS loads one block
+                                      ahead; 2 = 2 x 2 tiles staged through registers two blocks ahead;
+                                      3 = 3 x 4 tiles, the nine chains in three passes over K */
     LBH_TUNE_GEMV_DEPTH = 4,       /* matvec row steps in flight per wave: 1, 2, 3 or 4; 1 runs the
                                       one-lane-per-unit IQ instances as 1024-thread workgroups with
                                       the activations in LDS (the default for large IQ shapes) */

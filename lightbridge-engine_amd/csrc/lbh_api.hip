@@ -177,7 +177,7 @@ lbh_status lbh_ctx_set_tuning(lbh_ctx *ctx, int32_t key, int32_t value) {
         ctx->tuning.depth = value;
         return LBH_OK;
     case LBH_TUNE_GEMM_SHAPE:
-        if (value < 0 || value > 1) return LBH_INVALID_PARAMETER;
+        if (value < 0 || value > 3) return LBH_INVALID_PARAMETER;
         ctx->gemm_shape = value;
         return LBH_OK;
     default: return LBH_INVALID_PARAMETER;

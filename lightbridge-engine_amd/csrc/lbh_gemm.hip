@@ -22,9 +22,13 @@
 // (128 mn_j, mn_j), B holds (bh_j, bl_j), |partial sums| < 8 * 63 * 8128.
 //
 // Layouts (built once per matrix by k_prep_a, per call by k_prep_b):
-//   A tile (32 rows, block b): 17 operands x 64 lanes x 16 B, then the 32
-//     rows' d, then their dmin, as f32.  Operand 2l + p, lane j: row j % 32, the
-//     8 f16 of sub-blocks 4p + 2 (j / 32) + e / 4, element 8 (e % 4) + l.
+//   A tile (32 rows, block b): 17 operands x 64 lanes x 16 B, operand o at
+//     position op_pos(o) (0-3, 16, 4-15: the order the three-pass schedule
+//     reads them in), then the 32 rows' d, -dmin, d, d as f32 (a pass of the
+//     three-pass schedule stages rows 0-1 or 2-3: chain 2's scale row 1 is
+//     then -dmin in pass 0 and d after it, at a fixed address).
+//     Operand 2l + p, lane j: row j % 32, the 8 f16 of sub-blocks
+//     4p + 2 (j / 32) + e / 4, element 8 (e % 4) + l.
 //     Operand 16, lane j: sub-blocks 4 (j / 32) + e / 2, (128 mn, mn).
 //   B tile (32 tokens, block b): the same operands for token j % 32 (Q8_K
 //     bytes; operand 16 = (bh, bl)), then the 32 tokens' d8.
@@ -40,9 +44,13 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int OPS = 17;                          // 8 residues x 2 halves + the minimum
 constexpr int OP_BYTES = 1024;                   // 64 lanes x 8 f16
-constexpr int A_TILE = OPS * OP_BYTES + 32 * 8;  // + d[32], dmin[32] of the tile's rows
+constexpr int A_TILE = OPS * OP_BYTES + 32 * 16; // + the rows' scales: d, -dmin, d, d (32 f32 each)
 constexpr int B_TILE = OPS * OP_BYTES + 32 * 4;  // + d8 of the tile's tokens
 constexpr int PIECES = OPS + 1;                  // 1 KiB staging units per tile (the last one partial)
+
+// Position of operand o in a tile: residue operands 0-3, the minimum operand,
+// residue operands 4-15.
+__host__ __device__ constexpr int op_pos(int o) { return o < 4 ? o : o == 16 ? 4 : o + 1; }
 
 __device__ __forceinline__ uint32_t pack_f16(_Float16 lo, _Float16 hi) {
     return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
@@ -95,7 +103,7 @@ __global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out) {
                 }
                 o[e >> 1] = pack_f16((_Float16)w[0], (_Float16)w[1]);
             }
-            *reinterpret_cast<uint4 *>(dst + (2 * l + p) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4 *>(dst + op_pos(2 * l + p) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     }
     {
@@ -104,7 +112,7 @@ __global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out) {
             const int jj = 4 * h + (e >> 1);
             o[e >> 1] = pack_f16((_Float16)(128 * mn[jj]), (_Float16)mn[jj]);
         }
-        *reinterpret_cast<uint4 *>(dst + 16 * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4 *>(dst + op_pos(16) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
     }
     if (lane < 32) {
         float2 v = make_float2(0.0f, 0.0f);
@@ -112,9 +120,14 @@ __global__ void __launch_bounds__(64) k_prep_a(MatView m, uint8_t *a_out) {
             const uint32_t hdr = *reinterpret_cast<const uint32_t *>(blk);
             v = make_float2(f16_to_f32(hdr & 0xffffu), f16_to_f32(hdr >> 16));
         }
+        // -dmin: the minimum term is added, sum + (-dmin * d8) * minimum_sum,
+        // the same f32 value as the reference's sum - (dmin * d8) * minimum_sum
+        // (x - y is x + (-y), and (-a) * b is -(a * b) under round to nearest).
         float *dm = reinterpret_cast<float *>(tile_base + OPS * OP_BYTES);
         dm[lane] = v.x;
-        dm[32 + lane] = v.y;
+        dm[32 + lane] = -v.y;
+        dm[64 + lane] = v.x;
+        dm[96 + lane] = v.x;
     }
 }
 
@@ -158,7 +171,7 @@ __global__ void __launch_bounds__(64) k_prep_b(const uint8_t *q8, int n_tokens, 
                 }
                 o[e >> 1] = pack_f16(x[0], x[1]);
             }
-            *reinterpret_cast<uint4 *>(dst + (2 * l + p) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<uint4 *>(dst + op_pos(2 * l + p) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
         }
     }
     {
@@ -172,7 +185,7 @@ __global__ void __launch_bounds__(64) k_prep_b(const uint8_t *q8, int n_tokens, 
                       (int)*reinterpret_cast<const int16_t *>(blk + 262 + 4 * jj);
             o[e >> 1] = pack_f16((_Float16)(bsp >> 7), (_Float16)(bsp & 127));
         }
-        *reinterpret_cast<uint4 *>(dst + 16 * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4 *>(dst + op_pos(16) * OP_BYTES) = make_uint4(o[0], o[1], o[2], o[3]);
     }
     if (lane < 32)
         reinterpret_cast<float *>(tile_base + OPS * OP_BYTES)[lane] = valid ? *reinterpret_cast<const float *>(blk) : 0.0f;
@@ -278,11 +291,12 @@ __device__ __forceinline__ void wait_dma() { asm volatile("s_waitcnt vmcnt(0)" :
 __device__ __forceinline__ v16f residue_mfma(const v8h *Av, const v8h *Bv, int l) {
     const v16f zero = {};
     if (l == 8) {
-        v8h a = Av[16 * 64], b = Bv[16 * 64];
+        v8h a = Av[op_pos(16) * 64], b = Bv[op_pos(16) * 64];
         asm volatile("" : "+v"(a), "+v"(b));
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, zero, 0, 0, 0);
     }
-    v8h a0 = Av[2 * l * 64], b0 = Bv[2 * l * 64], a1 = Av[(2 * l + 1) * 64], b1 = Bv[(2 * l + 1) * 64];
+    const int p0 = op_pos(2 * l), p1 = op_pos(2 * l + 1);
+    v8h a0 = Av[p0 * 64], b0 = Bv[p0 * 64], a1 = Av[p1 * 64], b1 = Bv[p1 * 64];
     asm volatile("" : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1));
     const v16f c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, c, 0, 0, 0);
@@ -334,11 +348,11 @@ __device__ __forceinline__ void fold_block(Chains<HV> &ch, const uint8_t *At, co
     if (HV == 0) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const float4 m = dv[8 + 2 * q + h];   // dmin
+            const float4 m = dv[8 + 2 * q + h];   // -dmin
             const float ms[4] = {__fmul_rn(m.x, d8), __fmul_rn(m.y, d8), __fmul_rn(m.z, d8), __fmul_rn(m.w, d8)};
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                ch.msum[4 * q + e] = __fsub_rn(ch.msum[4 * q + e], __fmul_rn(ms[e], cn[4 * q + e]));
+                ch.msum[4 * q + e] = __fadd_rn(ch.msum[4 * q + e], __fmul_rn(ms[e], cn[4 * q + e]));
         }
     }
 }
@@ -456,18 +470,292 @@ __global__ void __launch_bounds__(64 * NW) k_kq_gemm(GemmArgs g) {
     const int wrt = lin / tok_wgs, wtt = lin - wrt * tok_wgs;
     const int rt0 = wrt * RG, tt0 = wtt * TG;
 
+    // The descriptors span only the workgroup's valid tiles: the partial last
+    // staging piece of the last tile then reads zeros past it, never memory
+    // past the allocation.
     StageSrc src;
+    src.last_a = n_rt - 1 - rt0 < RG - 1 ? n_rt - 1 - rt0 : RG - 1;
+    src.last_b = n_tt - 1 - tt0 < TG - 1 ? n_tt - 1 - tt0 : TG - 1;
     src.ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(M.a + (long long)rt0 * g.nb * A_TILE), (short)0,
-                                               RG * g.nb * A_TILE, 0x00020000);
+                                               (src.last_a + 1) * g.nb * A_TILE, 0x00020000);
     src.rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(g.b + (long long)tt0 * g.nb * B_TILE), (short)0,
-                                               TG * g.nb * B_TILE, 0x00020000);
-    src.last_a = n_rt - 1 - rt0;
-    src.last_b = n_tt - 1 - tt0;
+                                               (src.last_b + 1) * g.nb * B_TILE, 0x00020000);
 
     if (hv == 0)
         gemm_tile<MODE, 0>(g, M, S, src, rg, tg, tw, wid, lane, rt0, tt0);
     else
         gemm_tile<MODE, 1>(g, M, S, src, rg, tg, tw, wid, lane, rt0, tt0);
+}
+
+// ------------------------------------------------------- three-pass GEMM
+//
+// The nine chains of a (row, token) pair are independent until the final sum
+// result = ((sum_min + s_0) + s_1) + ... + s_7, so they can run as three
+// passes over K in the reference's order, the running result kept in
+// registers between them:
+//   pass 0: lane chains 0, 1 and the minimum chain (tile positions 0-4)
+//   pass 1: lane chains 2, 3, 4 (positions 5-10)
+//   pass 2: lane chains 5, 6, 7 (positions 11-16)
+// A pass stages only its own operands (six slots: pass p's positions
+// 6p - (p > 0) + 0..5, pass 0's sixth slot zeros), plus the tile's scales,
+// so one workgroup covers RG x TG = 12 tiles of 32 x 32 with one wave per
+// tile and three chains per wave (3 waves per SIMD), and each staged tile
+// serves TG (A) or RG (B) tiles: about 60% of the 2 x 2 schedule's staged
+// bytes per output.  Chain c of a pass is the MFMA pair on slots 2c, 2c + 1;
+// pass 0's minimum chain pairs its operand with the zero slot (the second
+// instruction adds exact zeros).  A stage is (RG + TG) tiles x 7 KiB (six
+// operand slots, then the 1 KiB piece holding d/-dmin or d8), triple-buffered
+// in LDS by direct buffer-to-LDS loads two stages ahead.
+constexpr int P3_WAVES = 12;
+constexpr int P3_SLOTS = 7;                                   // 6 operands + the scale piece
+constexpr int P3_TILE = P3_SLOTS * OP_BYTES;
+constexpr int P3_MAX_TILES = 7;                               // RG + TG
+constexpr int P3_PAD = P3_MAX_TILES * P3_TILE;                // target of the padding loads
+constexpr int P3_BUF = P3_PAD + OP_BYTES;
+static_assert(op_pos(16) == 4 && op_pos(4) == 5, "pass windows: 0-4 (+ zeros), 5-10, 11-16");
+
+// The three stage buffers are distinct LDS arrays, each addressed statically
+// (the stage loop is unrolled by three): the compiler's wait before an LDS
+// read then covers only the buffer-to-LDS loads into that array, not the
+// prefetches into the other two, which stay in flight.
+__shared__ __align__(16) uint8_t p3_lds0[P3_BUF];
+__shared__ __align__(16) uint8_t p3_lds1[P3_BUF];
+__shared__ __align__(16) uint8_t p3_lds2[P3_BUF];
+
+template <int BUF>
+__device__ __forceinline__ uint8_t *p3_buffer() {
+    return BUF == 0 ? p3_lds0 : BUF == 1 ? p3_lds1 : p3_lds2;
+}
+
+template <int RG_, int TG_>
+struct P3 {
+    static_assert(RG_ * TG_ == P3_WAVES, "one wave per tile");
+    static_assert(RG_ + TG_ <= P3_MAX_TILES, "stages fit the LDS buffers");
+    static constexpr int RG = RG_, TG = TG_;
+    static constexpr int UA = (RG * P3_SLOTS + P3_WAVES - 1) / P3_WAVES;   // A loads per wave per stage
+    static constexpr int UB = (TG * P3_SLOTS + P3_WAVES - 1) / P3_WAVES;   // B loads per wave per stage
+    static constexpr int UPW = UA + UB;
+};
+
+// This wave's share of a stage's loads, fixed for the whole K loop: load k of
+// the A side is unit u = wid + 12 k of the RG x 7 A units (slot u % 7 of A
+// tile u / 7), likewise for the TG x 7 B units; units past a side's count
+// are padding.  Per unit: its LDS offset in a stage buffer, the byte offset
+// in the side's descriptor of its piece in block 0 of pass 0 (the scale
+// piece: the same in every pass), and three masks: pad (0x80000000 for a
+// unit past the stage), zero (all ones for pass 0's sixth slot), win (all
+// ones unless the scale piece, which ignores the pass window).
+struct P3Unit {
+    int lds, off;
+    uint32_t pad, zero, win;
+};
+template <int SIDE_TILES, int TILE_BYTES>
+__device__ __forceinline__ P3Unit p3_unit(int u, int lds_tile0, int last, int nb) {
+    P3Unit x;
+    const int ti = u / P3_SLOTS, slot = u - ti * P3_SLOTS;
+    const bool in_stage = u < SIDE_TILES * P3_SLOTS;
+    x.pad = in_stage ? 0u : 0x80000000u;
+    x.zero = slot == 5 ? ~0u : 0u;
+    x.win = slot == 6 ? 0u : ~0u;
+    x.lds = in_stage ? (lds_tile0 + ti) * P3_TILE + slot * OP_BYTES : P3_PAD;
+    x.off = (ti < last ? ti : last) * nb * TILE_BYTES + (slot == 6 ? OPS : slot) * OP_BYTES;
+    return x;
+}
+
+// Issues this wave's loads of the stage at (poff, bA, bB) into buffer BUF:
+// poff = the pass's window start in bytes, bA / bB = the block's offset in a
+// tile row of the A / B side, dead = 0x80000000 for a stage past the end (all
+// its loads padding), z0 = 0x80000000 in pass 0 (its sixth slot is zeros),
+// soff = where the A scale piece starts (0 in pass 0, 256 after).
+// A padding load reads from beyond the descriptor range (zeros, no memory
+// traffic): units past the stage into the buffer's padding piece, pass 0's
+// sixth slot into that slot.  Every wave issues UPW loads per stage, with no
+// branch between them, so one wait count serves all and the compiler's own
+// waits before the LDS reads stay exact.
+template <class S, int BUF>
+__device__ __forceinline__ void p3_issue(const StageSrc &src, const P3Unit (&ua)[S::UA], const P3Unit (&ub)[S::UB],
+                                         int poff, int bA, int bB, uint32_t dead, uint32_t z0, uint32_t soff,
+                                         uint32_t lane16) {
+    uint8_t *buf = p3_buffer<BUF>();
+#pragma unroll
+    for (int k = 0; k < S::UA + S::UB; ++k) {
+        const bool is_a = k < S::UA;
+        const P3Unit &x = is_a ? ua[k] : ub[k - S::UA];
+        const uint32_t vo = lane16 | (x.pad | dead | (z0 & x.zero));
+        uint32_t off = (uint32_t)(x.off + (is_a ? bA : bB)) + ((uint32_t)poff & x.win);
+        if (is_a) off += soff & ~x.win;   // A scale piece: rows 0-1 in pass 0, rows 2-3 after
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(is_a ? src.ra : src.rb, (lds_void *)(buf + x.lds), 16, vo, off, 0, 0);
+    }
+}
+
+// One block of the wave's tile (At, Bt: its A and B tiles in the stage
+// buffer): chain c += (scale * d8) * integer sum, in the reference's order
+// (q8_k.rs:314-326), with scale = staged row 0 (d) for chains 0, 1 and row 1
+// for chain 2 (-dmin in pass 0, the minimum chain; d in passes 1 and 2).  The
+// same instructions in every pass.
+__device__ __forceinline__ void p3_block(float (&ch)[3][16], const uint8_t *At, const uint8_t *Bt, int lane) {
+    const int h = lane >> 5;
+    const v8h *Av = reinterpret_cast<const v8h *>(At) + lane;
+    const v8h *Bv = reinterpret_cast<const v8h *>(Bt) + lane;
+    const float d8 = reinterpret_cast<const float *>(Bt + 6 * OP_BYTES)[lane & 31];
+    const float4 *dv = reinterpret_cast<const float4 *>(At + 6 * OP_BYTES);
+    float sc[16], s2[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 d = dv[2 * q + h], e = dv[8 + 2 * q + h];
+        sc[4 * q] = __fmul_rn(d.x, d8);
+        sc[4 * q + 1] = __fmul_rn(d.y, d8);
+        sc[4 * q + 2] = __fmul_rn(d.z, d8);
+        sc[4 * q + 3] = __fmul_rn(d.w, d8);
+        s2[4 * q] = __fmul_rn(e.x, d8);
+        s2[4 * q + 1] = __fmul_rn(e.y, d8);
+        s2[4 * q + 2] = __fmul_rn(e.z, d8);
+        s2[4 * q + 3] = __fmul_rn(e.w, d8);
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const v16f zero = {};
+        v8h a0 = Av[2 * c * 64], b0 = Bv[2 * c * 64], a1 = Av[(2 * c + 1) * 64], b1 = Bv[(2 * c + 1) * 64];
+        asm volatile("" : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1));
+        const v16f x = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero, 0, 0, 0);
+        const v16f cur = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, x, 0, 0, 0);
+        const float *scale = c == 2 ? s2 : sc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ch[c][i] = __fadd_rn(ch[c][i], __fmul_rn(scale[i], cur[i]));
+        asm volatile("" : "+v"(ch[c][0]), "+v"(ch[c][1]), "+v"(ch[c][2]), "+v"(ch[c][3]), "+v"(ch[c][4]),
+                     "+v"(ch[c][5]), "+v"(ch[c][6]), "+v"(ch[c][7]), "+v"(ch[c][8]), "+v"(ch[c][9]),
+                     "+v"(ch[c][10]), "+v"(ch[c][11]), "+v"(ch[c][12]), "+v"(ch[c][13]), "+v"(ch[c][14]),
+                     "+v"(ch[c][15]));
+    }
+}
+
+// Stage position: pass p, block b of the stage computed (cp, cb) and of the
+// stage issued two ahead (ip, ib), advanced without divisions; ipoff, ibA,
+// ibB the issued stage's pass window and block offsets.
+struct P3Pos {
+    int cp, cb, ip, ib, ipoff, ibA, ibB;
+};
+__device__ __forceinline__ void p3_next_issue(P3Pos &ps, int nb) {
+    ps.ibA += A_TILE, ps.ibB += B_TILE;
+    if (++ps.ib == nb) {
+        ps.ib = 0, ps.ibA = 0, ps.ibB = 0, ++ps.ip;
+        ps.ipoff = (6 * ps.ip - 1) * OP_BYTES;
+    }
+}
+// The issued stage's masks for p3_issue, made opaque to the compiler (an empty
+// asm statement) so it cannot specialise the loads on the pass.
+template <class S, int BUF>
+__device__ __forceinline__ void p3_issue_at(const StageSrc &src, const P3Unit (&ua)[S::UA],
+                                            const P3Unit (&ub)[S::UB], const P3Pos &ps, uint32_t lane16) {
+    uint32_t dead = (uint32_t)(2 - ps.ip) & 0x80000000u;   // ip == 3: past the end
+    uint32_t z0 = (uint32_t)(ps.ip - 1) & 0x80000000u;     // ip == 0
+    uint32_t soff = ~z0 >> 23 & 256u;                      // 0 in pass 0, 256 after
+    asm volatile("" : "+s"(dead), "+s"(z0), "+s"(soff));
+    p3_issue<S, BUF>(src, ua, ub, ps.ipoff, ps.ibA, ps.ibB, dead, z0, soff, lane16);
+}
+
+// Stage s of the K loop in buffer BUF = s % 3: wait for this wave's loads of
+// stage s (stage s + 1's stay in flight), barrier (every wave's loads of
+// stage s have landed and every wave has finished stage s - 1, whose buffer
+// is refilled next), issue stage s + 2 (padding past the end: the control
+// flow is the same in every stage, which keeps the compiler's own wait before
+// each LDS read down to the loads into that buffer), then the block's MFMAs
+// and folds for pass cp.  At a pass's last block the pass's chains go onto
+// the running result v in the reference's order (pass 0: minimum chain, then
+// lane chains 0, 1) and restart.
+template <class S, int BUF>
+__device__ __forceinline__ void p3_stage(float (&ch)[3][16], float (&v)[16], const StageSrc &src,
+                                         const P3Unit (&ua)[S::UA], const P3Unit (&ub)[S::UB], P3Pos &ps, int nb,
+                                         int lane, int rt, int tt) {
+    static_assert(S::UPW == 5, "the wait count below is one stage's loads");
+    asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    p3_issue_at<S, (BUF + 2) % 3>(src, ua, ub, ps, (uint32_t)lane * 16);
+    p3_next_issue(ps, nb);
+    // The lane index goes through an empty asm statement per stage, so the
+    // lane addresses into this buffer are formed here, not kept in registers
+    // across the loop for all three buffers.
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const uint8_t *buf = p3_buffer<BUF>();
+    const int p = ps.cp;
+    p3_block(ch, buf + rt * P3_TILE, buf + (S::RG + tt) * P3_TILE, ln);
+    if (ps.cb == nb - 1) {
+        if (p == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = __fadd_rn(__fadd_rn(ch[2][i], ch[0][i]), ch[1][i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = __fadd_rn(__fadd_rn(__fadd_rn(v[i], ch[0][i]), ch[1][i]), ch[2][i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) ch[0][i] = ch[1][i] = ch[2][i] = 0.0f;
+    }
+    if (++ps.cb == nb) ps.cb = 0, ++ps.cp;
+}
+
+template <int RG_, int TG_>
+__global__ void __launch_bounds__(64 * P3_WAVES) k_kq_gemm3(GemmArgs g) {
+    using S = P3<RG_, TG_>;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rt = wid % S::RG, tt = wid / S::RG;
+    const MatGemm &M = g.mat[blockIdx.y];
+    const int nb = g.nb;
+    const int n_rt = (M.rows + 31) / 32, n_tt = (g.n_tokens + 31) / 32;
+    const int row_wgs = (n_rt + S::RG - 1) / S::RG, tok_wgs = (n_tt + S::TG - 1) / S::TG;
+    // XCD-aware order: workgroups are dealt to the eight XCDs round robin;
+    // each XCD takes a contiguous run of row groups with all their token
+    // groups, so the token groups of a row group run together on one XCD and
+    // its A tiles are fetched into that XCD's L2 once.
+    const int nwg = row_wgs * tok_wgs;
+    const int id = (int)blockIdx.x;
+    if (id >= nwg) return;
+    const int nfull = nwg & ~7;
+    const int lin = id < nfull ? (id % 8) * (nfull / 8) + id / 8 : id;   // a bijection of [0, nwg)
+    const int wrt = lin / tok_wgs, wtt = lin - wrt * tok_wgs;
+    const int rt0 = wrt * S::RG, tt0 = wtt * S::TG;
+
+    // The descriptors span only the workgroup's valid tiles (the scale piece
+    // of the last one reads zeros past it, never memory past the allocation).
+    StageSrc src;
+    src.last_a = n_rt - 1 - rt0 < S::RG - 1 ? n_rt - 1 - rt0 : S::RG - 1;
+    src.last_b = n_tt - 1 - tt0 < S::TG - 1 ? n_tt - 1 - tt0 : S::TG - 1;
+    src.ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(M.a + (long long)rt0 * nb * A_TILE), (short)0,
+                                               (src.last_a + 1) * nb * A_TILE, 0x00020000);
+    src.rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(g.b + (long long)tt0 * nb * B_TILE), (short)0,
+                                               (src.last_b + 1) * nb * B_TILE, 0x00020000);
+
+    P3Unit ua[S::UA], ub[S::UB];
+#pragma unroll
+    for (int k = 0; k < S::UA; ++k) ua[k] = p3_unit<S::RG, A_TILE>(wid + P3_WAVES * k, 0, src.last_a, nb);
+#pragma unroll
+    for (int k = 0; k < S::UB; ++k) ub[k] = p3_unit<S::TG, B_TILE>(wid + P3_WAVES * k, S::RG, src.last_b, nb);
+
+    const int total = 3 * nb;   // stages: (pass, block), a multiple of three
+    P3Pos ps{0, 0, 0, 0, 0, 0, 0};
+    p3_issue_at<S, 0>(src, ua, ub, ps, (uint32_t)lane * 16);
+    p3_next_issue(ps, nb);
+    p3_issue_at<S, 1>(src, ua, ub, ps, (uint32_t)lane * 16);
+    p3_next_issue(ps, nb);
+    float ch[3][16], v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ch[0][i] = ch[1][i] = ch[2][i] = v[i] = 0.0f;
+    for (int s = 0; s < total; s += 3) {
+        p3_stage<S, 0>(ch, v, src, ua, ub, ps, nb, lane, rt, tt);
+        p3_stage<S, 1>(ch, v, src, ua, ub, ps, nb, lane, rt, tt);
+        p3_stage<S, 2>(ch, v, src, ua, ub, ps, nb, lane, rt, tt);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the padding loads land before the LDS is released
+
+    const int h = lane >> 5;
+    const int t = (tt0 + tt) * 32 + (lane & 31);
+    if (t >= g.n_tokens) return;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int row = (rt0 + rt) * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+        if (row < M.rows) M.y[(long long)t * M.ldy + row] = v[i];
+    }
 }
 
 // ---------------------------------------------------------------- launchers
@@ -506,9 +794,28 @@ static hipError_t gemm_mode(const GemmArgs &g, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int RG_, int TG_>
+static hipError_t gemm_p3(const GemmArgs &g, hipStream_t s) {
+    using S = P3<RG_, TG_>;
+    int rows = 0;
+    for (int i = 0; i < g.n_mat; ++i) rows = g.mat[i].rows > rows ? g.mat[i].rows : rows;
+    const int grid = cdiv(cdiv(rows, 32), S::RG) * cdiv(cdiv(g.n_tokens, 32), S::TG);
+    hipLaunchKernelGGL((k_kq_gemm3<RG_, TG_>), dim3(grid, g.n_mat), dim3(64 * P3_WAVES), 0, s, g);
+    return hipGetLastError();
+}
+
+// shape: 0 default (three passes from 97 tokens: four token tiles per
+// workgroup; the 2 x 2 schedule staged through registers below), 1 the 2 x 2
+// schedule with direct buffer-to-LDS staging, 2 the 2 x 2 schedule staged
+// through registers, 3 three passes.
 hipError_t launch_kq_gemm(const GemmArgs &g, hipStream_t s) {
     if (g.n_mat < 1 || g.n_mat > GEMM_MAX_MATS || g.n_tokens < 1 || g.nb < 1 || g.nb > 64) return hipErrorInvalidValue;
-    return g.shape == 1 ? gemm_mode<1>(g, s) : gemm_mode<0>(g, s);
+    switch (g.shape) {
+    case 1: return gemm_mode<1>(g, s);
+    case 2: return gemm_mode<0>(g, s);
+    case 3: return gemm_p3<3, 4>(g, s);
+    default: return g.n_tokens > 96 ? gemm_p3<3, 4>(g, s) : gemm_mode<0>(g, s);
+    }
 }
 
 }  // namespace lbh

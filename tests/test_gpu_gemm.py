@@ -4,7 +4,9 @@ Every output y[t, r] must equal the reference's per-row dot
 (dot_q4_or_q5_k, crates/bridge-quant-layout/src/q8_k.rs:247-327) of row r with
 token t's Q8_K row, bit for bit: random blocks, negative d/dmin, the integer
 extremes (scale 63, mins 63, 5-bit quants 31, activations at +-127), ragged row
-and token counts, both tile staging modes, and the BASELINE configs[4] shape
+and token counts (row and token tiles not multiples of a workgroup's), every
+schedule (2 x 2 tiles staged through registers or buffer-to-LDS loads; 3 x 4
+tiles in three passes), and the BASELINE configs[4] shape
 (Q5_K 12288 x 4096, 512 tokens) in full.
 """
 import numpy as np
@@ -55,7 +57,8 @@ def oracle_gemm(oracle, ty, w, rows, k, q8):
 
 
 @pytest.mark.parametrize("ty", [Q4_K, Q5_K])
-@pytest.mark.parametrize("rows,k,n", [(16, 256, 1), (40, 1024, 33), (300, 4096, 70), (64, 512, 32)])
+@pytest.mark.parametrize("rows,k,n", [(16, 256, 1), (40, 1024, 33), (300, 4096, 70), (64, 512, 32),
+                                      (200, 1024, 100), (100, 512, 150), (96, 256, 129), (1000, 2048, 300)])
 def test_gemm_random_bit_exact(be, oracle, ty, rows, k, n):
     w = synth.random_matrix(ty, rows, k, seed=rows + k + ty)
     # negative scales on some blocks: flip the f16 sign bits of d and dmin
@@ -68,7 +71,8 @@ def test_gemm_random_bit_exact(be, oracle, ty, rows, k, n):
 
 
 @pytest.mark.parametrize("ty", [Q4_K, Q5_K])
-def test_gemm_integer_extremes(be, oracle, ty):
+@pytest.mark.parametrize("shape", [0, 3])
+def test_gemm_integer_extremes(be, oracle, ty, shape):
     rows, k, n = 48, 512, 40
     bb = synth.BLOCK_BYTES[ty]
     w = np.full((rows, (k // 256) * bb), 0xFF, np.uint8)
@@ -82,10 +86,15 @@ def test_gemm_integer_extremes(be, oracle, ty):
     xs[6, ::7] = -3.0
     q8 = q8_rows(oracle, xs.astype(np.float32))
     assert np.abs(q8[0, 4:260].view(np.int8)).max() == 127
-    assert _same(run_gemm(be, ty, w, rows, k, q8), oracle_gemm(oracle, ty, w, rows, k, q8))
+    be.set_tuning(be.TUNE_GEMM_SHAPE, shape)
+    try:
+        got = run_gemm(be, ty, w, rows, k, q8)
+    finally:
+        be.set_tuning(be.TUNE_GEMM_SHAPE, 0)
+    assert _same(got, oracle_gemm(oracle, ty, w, rows, k, q8))
 
 
-@pytest.mark.parametrize("shape", [0, 1])
+@pytest.mark.parametrize("shape", [0, 1, 2, 3])
 def test_gemm_staging_modes_give_the_same_bits(be, oracle, shape):
     rows, k, n = 200, 1024, 100
     w = synth.random_matrix(Q5_K, rows, k, seed=9)
