@@ -590,38 +590,50 @@ __device__ __forceinline__ void p3_issue(const StageSrc &src, const P3Unit (&ua)
 
 // One block of the wave's tile (At, Bt: its A and B tiles in the stage
 // buffer): chain c += (scale * d8) * integer sum, in the reference's order
-// (q8_k.rs:314-326), with scale = staged row 0 (d) for chains 0, 1 and row 1
-// for chain 2 (-dmin in pass 0, the minimum chain; d in passes 1 and 2).  The
-// same instructions in every pass.
-__device__ __forceinline__ void p3_block(float (&ch)[3][16], const uint8_t *At, const uint8_t *Bt, int lane) {
+// (q8_k.rs:314-326), with scale = staged row 0 (d) for chains 0 and 1, and
+// for chain 2 row 1 in pass 0 (-dmin: the minimum chain) and d after it.
+// The operands of chain c + 1 are read from LDS while chain c's MFMAs run
+// and its fold issues.
+__device__ __forceinline__ void p3_block(float (&ch)[3][16], const uint8_t *At, const uint8_t *Bt, int lane,
+                                         bool first_pass) {
     const int h = lane >> 5;
     const v8h *Av = reinterpret_cast<const v8h *>(At) + lane;
     const v8h *Bv = reinterpret_cast<const v8h *>(Bt) + lane;
     const float d8 = reinterpret_cast<const float *>(Bt + 6 * OP_BYTES)[lane & 31];
     const float4 *dv = reinterpret_cast<const float4 *>(At + 6 * OP_BYTES);
-    float sc[16], s2[16];
+    v8h a0 = Av[0], b0 = Bv[0], a1 = Av[64], b1 = Bv[64];
+    float sc[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float4 d = dv[2 * q + h], e = dv[8 + 2 * q + h];
+        const float4 d = dv[2 * q + h];
         sc[4 * q] = __fmul_rn(d.x, d8);
         sc[4 * q + 1] = __fmul_rn(d.y, d8);
         sc[4 * q + 2] = __fmul_rn(d.z, d8);
         sc[4 * q + 3] = __fmul_rn(d.w, d8);
-        s2[4 * q] = __fmul_rn(e.x, d8);
-        s2[4 * q + 1] = __fmul_rn(e.y, d8);
-        s2[4 * q + 2] = __fmul_rn(e.z, d8);
-        s2[4 * q + 3] = __fmul_rn(e.w, d8);
     }
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
         const v16f zero = {};
-        v8h a0 = Av[2 * c * 64], b0 = Bv[2 * c * 64], a1 = Av[(2 * c + 1) * 64], b1 = Bv[(2 * c + 1) * 64];
         asm volatile("" : "+v"(a0), "+v"(b0), "+v"(a1), "+v"(b1));
         const v16f x = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b0, zero, 0, 0, 0);
         const v16f cur = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b1, x, 0, 0, 0);
-        const float *scale = c == 2 ? s2 : sc;
+        if (c < 2) {
+            a0 = Av[2 * (c + 1) * 64], b0 = Bv[2 * (c + 1) * 64];
+            a1 = Av[(2 * c + 3) * 64], b1 = Bv[(2 * c + 3) * 64];
+        }
+        __builtin_amdgcn_sched_barrier(0);   // the reads go out before this chain's fold
+        if (c < 2 || !first_pass) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) ch[c][i] = __fadd_rn(ch[c][i], __fmul_rn(scale[i], cur[i]));
+            for (int i = 0; i < 16; ++i) ch[c][i] = __fadd_rn(ch[c][i], __fmul_rn(sc[i], cur[i]));
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 e = dv[8 + 2 * q + h];
+                const float ms[4] = {__fmul_rn(e.x, d8), __fmul_rn(e.y, d8), __fmul_rn(e.z, d8), __fmul_rn(e.w, d8)};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) ch[2][4 * q + k] = __fadd_rn(ch[2][4 * q + k], __fmul_rn(ms[k], cur[4 * q + k]));
+            }
+        }
         asm volatile("" : "+v"(ch[c][0]), "+v"(ch[c][1]), "+v"(ch[c][2]), "+v"(ch[c][3]), "+v"(ch[c][4]),
                      "+v"(ch[c][5]), "+v"(ch[c][6]), "+v"(ch[c][7]), "+v"(ch[c][8]), "+v"(ch[c][9]),
                      "+v"(ch[c][10]), "+v"(ch[c][11]), "+v"(ch[c][12]), "+v"(ch[c][13]), "+v"(ch[c][14]),
@@ -679,7 +691,7 @@ __device__ __forceinline__ void p3_stage(float (&ch)[3][16], float (&v)[16], con
     asm volatile("" : "+v"(ln));
     const uint8_t *buf = p3_buffer<BUF>();
     const int p = ps.cp;
-    p3_block(ch, buf + rt * P3_TILE, buf + (S::RG + tt) * P3_TILE, ln);
+    p3_block(ch, buf + rt * P3_TILE, buf + (S::RG + tt) * P3_TILE, ln, p == 0);
     if (ps.cb == nb - 1) {
         if (p == 0) {
 #pragma unroll
