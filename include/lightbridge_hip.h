@@ -351,6 +351,17 @@ lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *moe, const uint32_t 
                                      size_t n_routed, const float *input_dev, size_t input_len, float *output_dev,
                                      size_t output_len, lbh_error *err);
 
+/* [sync] moe_routed_by_id_into in the DequantF32 execution mode (the same
+ * moe.rs:64-147 with ReferenceExecutionMode::DequantF32; the CLI's --backend
+ * dequant-f32): every matvec decodes the weights to f32 and runs the sequential f32
+ * dot on the f32 input (dot_dequant_row, gemv.rs:33-41), no Q8_K step.  Same
+ * arguments, order of the sums and error precedence as lbh_moe_routed_by_id_into;
+ * bit-identical to the reference in that mode.  A checking path (one device
+ * round trip per expert), not a decode loop's. */
+lbh_status lbh_moe_routed_by_id_dequant_f32_into(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *ids, const float *coefs,
+                                                 size_t n_routed, const float *input_dev, size_t input_len,
+                                                 float *output_dev, size_t output_len, lbh_error *err);
+
 /* [async] The same computation without validation or status readback (graph
  * capturable): ids must be ascending, distinct and < n_experts (the last is checked),
  * coefs and x finite. */

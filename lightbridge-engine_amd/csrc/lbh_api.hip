@@ -863,6 +863,7 @@ struct lbh_moe {
     hipStream_t side1;
     hipEvent_t sev[2];
     float *d_shared;
+    float *dq;                // DequantF32 checked forward: one expert's gate and up values
     int two_stream;           // 1: the async forwards use side1, 0: one stream (default, measured faster)
 };
 
@@ -895,6 +896,7 @@ void free_moe(lbh_moe *m) {
     if (m->side1) (void)hipStreamDestroy(m->side1);
     if (m->d_shared) (void)hipFree(m->d_shared);
     if (m->h) (void)hipFree(m->h);
+    if (m->dq) (void)hipFree(m->dq);
     if (m->status) (void)hipFree(m->status);
     if (m->status_host) (void)hipHostFree(m->status_host);
     delete m;
@@ -1055,6 +1057,7 @@ lbh_status build_moe(lbh_ctx *ctx, size_t n_experts, ExpertDev *table, lbh_exper
         if (e == hipSuccess) e = hipMemcpy(m->experts_dev, table, n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice);
     }
     if (e == hipSuccess) e = hipMalloc(&m->h, slots * max_ffn * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&m->dq, 2 * max_ffn * sizeof(float));
     if (e == hipSuccess && has_shared) {
         m->two_stream = 0;   // measured slower on MI355X (see lbh_moe_set_streams)
         e = hipMalloc(&m->d_shared, hidden * sizeof(float));
@@ -1289,6 +1292,92 @@ lbh_status lbh_moe_routed_by_id_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *i
         HIP_TRY(launch_moe_down(a, ctx->stream));
         HIP_TRY(hipStreamSynchronize(ctx->stream));
         return fail(err, LBH_NON_FINITE_VALUE, 0, row, 0, 0, read_f32_bits(ctx, output + row), 3);
+    }
+    return ok(err);
+}
+
+// moe_routed_by_id_into in the DequantF32 mode (moe.rs:64-147 with
+// ReferenceExecutionMode::DequantF32, the mode of the CLI's dequant-f32
+// backend): every matvec is dot_dequant_row (gemv_dequant_f32_into,
+// gemv.rs:33-41), on the f32 input with no Q8_K step.  The reference's order:
+// per routed expert its checks (moe.rs:94-129) and its preflight
+// (swiglu_project_into: gate, up, SwiGLU, down into scratch), the shared
+// expert's preflight, then output.fill(0) and one accumulating pass per expert
+// in id order and the shared expert at 1.0 (expert_swiglu_accumulate_into,
+// activation.rs:104-144), each first rejecting a non-finite destination
+// (gemv.rs:126-127).  The preflight's down projection cannot fail (its input
+// h was just checked finite and uploaded weights decode finite), so only gate,
+// up and SwiGLU run there, and the accumulating passes reuse that h (the same
+// values the reference computes again).
+lbh_status lbh_moe_routed_by_id_dequant_f32_into(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs,
+                                                 size_t n_routed, const float *input, size_t input_len, float *output,
+                                                 size_t output_len, lbh_error *err) {
+    if (!ctx || !m) return fail(err, LBH_NULL_ARGUMENT);
+    if (n_routed == 0) return fail(err, LBH_DIMENSION_MISMATCH, 0, 3, 1, 0);
+    if (input_len != m->hidden) return fail(err, LBH_DIMENSION_MISMATCH, 0, 0, m->hidden, input_len);
+    if (output_len != m->hidden) return fail(err, LBH_DIMENSION_MISMATCH, 0, 1, m->hidden, output_len);
+    if (!ids || !coefs || !input || !output) return fail(err, LBH_NULL_ARGUMENT);
+    if (n_routed > MOE_MAX_ROUTED) return fail(err, LBH_UNSUPPORTED_SHAPE, 0, 0, MOE_MAX_ROUTED, n_routed);
+    DeviceGuard g(ctx->device);
+    // The first routed expert's gate gemv_into scans the input (gemv.rs:195-211)
+    // after that expert's own checks.
+    auto input_scan = [&]() -> lbh_status {
+        HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+        HIP_TRY(launch_find_nonfinite(input, (long long)input_len, &ctx->status->first_bad_input, ctx->stream));
+        const lbh_status st = read_status(ctx, err);
+        if (st) return st;
+        if (ctx->status_host->first_bad_input != ~0ull) return input_error(ctx, m->type_gate_r, input, err);
+        return LBH_OK;
+    };
+    float *gbuf = m->dq, *ubuf = m->dq + m->h_stride;
+    auto preflight = [&](const ExpertDev &e, int slot, size_t ffn) -> lbh_status {
+        float *h = m->h + (size_t)slot * m->h_stride;
+        HIP_TRY(launch_gemv_dequant(e.gate, input, gbuf, 0.0f, 0, nullptr, ctx->stream));
+        HIP_TRY(launch_gemv_dequant(e.up, input, ubuf, 0.0f, 0, nullptr, ctx->stream));
+        HIP_TRY(launch_expf(gbuf, h, (long long)ffn, 1, ubuf, ctx->stream));   // SwiGLU, activation.rs:170-178
+        HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+        HIP_TRY(launch_find_nonfinite(h, (long long)ffn, &ctx->status->first_bad_input, ctx->stream));
+        const lbh_status st = read_status(ctx, err);
+        if (st) return st;
+        const unsigned long long bad = ctx->status_host->first_bad_input;
+        if (bad != ~0ull) return fail(err, LBH_NON_FINITE_VALUE, 0, bad, 0, 0, read_f32_bits(ctx, h + bad), 5);
+        return LBH_OK;
+    };
+    for (size_t i = 0; i < n_routed; ++i) {
+        uint32_t bits;
+        std::memcpy(&bits, &coefs[i], 4);
+        if ((bits & 0x7f800000u) == 0x7f800000u) return fail(err, LBH_NON_FINITE_VALUE, 0, 0, 0, 0, bits, 6);
+        if (i > 0 && ids[i] == ids[i - 1]) return fail(err, LBH_DUPLICATE_ROUTED_EXPERT, 0, ids[i]);
+        if (i > 0 && ids[i] < ids[i - 1]) return fail(err, LBH_ROUTED_EXPERT_ORDER, 0, ids[i], ids[i - 1], ids[i]);
+        if (ids[i] >= m->n_experts) return fail(err, LBH_INVALID_PARAMETER, 0, ids[i], m->n_experts, ids[i]);
+        lbh_status st = i == 0 ? input_scan() : LBH_OK;
+        if (!st) st = preflight(m->experts_host[ids[i]], (int)i, m->ffn_r);
+        if (st) return st;
+    }
+    if (m->has_shared) {
+        const lbh_status st = preflight(m->shared, MOE_SHARED_SLOT, m->ffn_s);
+        if (st) return st;
+    }
+    // output.fill(0.0) (moe.rs:141), then the accumulating passes.  A [sync]
+    // entry point: its memset never goes into a captured graph.
+    HIP_TRY(hipMemsetAsync(output, 0, output_len * sizeof(float), ctx->stream));
+    auto accumulate = [&](const MatView &down, int slot, float coef) -> lbh_status {
+        HIP_TRY(launch_reset_status(ctx->status, ctx->stream));
+        HIP_TRY(launch_find_nonfinite(output, (long long)output_len, &ctx->status->first_bad_dest, ctx->stream));
+        HIP_TRY(launch_gemv_dequant(down, m->h + (size_t)slot * m->h_stride, output, coef, 1, ctx->status,
+                                    ctx->stream));
+        const lbh_status st = read_status(ctx, err);
+        if (st) return st;
+        if (ctx->status_host->first_bad_dest != ~0ull) return dest_error(ctx, 0, output, err);
+        return LBH_OK;
+    };
+    for (size_t i = 0; i < n_routed; ++i) {
+        const lbh_status st = accumulate(m->experts_host[ids[i]].down, (int)i, coefs[i]);
+        if (st) return st;
+    }
+    if (m->has_shared) {
+        const lbh_status st = accumulate(m->shared.down, MOE_SHARED_SLOT, 1.0f);
+        if (st) return st;
     }
     return ok(err);
 }

@@ -213,7 +213,9 @@ __device__ __forceinline__ void dequant_group(const Planes &P, uint32_t u, int s
 template <int TY>
 __global__ void __launch_bounds__(256) k_gemv_dequant(DequantArgs p) {
     __shared__ __align__(16) float s_prod[2][DQ_ROWS * DQ_STRIDE];
-    if (p.status && p.status->first_bad_input != ~0ull) return;
+    // A non-finite input or (accumulating) destination: the reference rejects
+    // the call before it writes (gemv.rs:126-127, :195-211).
+    if (p.status && (p.status->first_bad_input != ~0ull || p.status->first_bad_dest != ~0ull)) return;
     const int nb = p.m.nb;
     const int rows = p.m.rows;
     const int r0 = blockIdx.x * DQ_ROWS;

@@ -114,6 +114,7 @@ def lib() -> C.CDLL:
             "lbh_moe_set_tiles": ([p, i32, i32, i32], i32),
             "lbh_moe_set_streams": ([p, i32], i32),
             "lbh_moe_routed_by_id_into": ([p, p, p, p, sz, p, sz, p, sz, E], i32),
+            "lbh_moe_routed_by_id_dequant_f32_into": ([p, p, p, p, sz, p, sz, p, sz, E], i32),
             "lbh_moe_forward": ([p, p, p, p, sz, p, p], i32),
             "lbh_debug_expf": ([p, p, p, sz, i32, p, E], i32),
             "lbh_debug_expf_host": ([p, p, sz, i32, p], None),
@@ -366,6 +367,14 @@ class HipBackend:
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
         coefs = np.ascontiguousarray(coefs, dtype=np.float32)
         _call(lib().lbh_moe_routed_by_id_into, self.ctx, moe.handle, C.c_void_p(ids.ctypes.data),
+              C.c_void_p(coefs.ctypes.data), ids.size, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel())
+
+    def moe_routed_by_id_dequant_f32_into(self, moe: "MoeLayer", ids, coefs, x, y) -> None:
+        """moe_routed_by_id_into in the DequantF32 execution mode (moe.rs:64-147;
+        every matvec dot_dequant_row, gemv.rs:33-41)."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        coefs = np.ascontiguousarray(coefs, dtype=np.float32)
+        _call(lib().lbh_moe_routed_by_id_dequant_f32_into, self.ctx, moe.handle, C.c_void_p(ids.ctypes.data),
               C.c_void_p(coefs.ctypes.data), ids.size, _dev_ptr(x), x.numel(), _dev_ptr(y), y.numel())
 
     def moe_forward_batch(self, moe: "MoeLayer", ids, coefs, x, y) -> None:

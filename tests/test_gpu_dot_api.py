@@ -332,3 +332,11 @@ def test_dequant_errors(be):
     expect_error(be, lambda: be.gemv_dequant_accumulate_scaled_into(m, dev(np.ones(k, np.float32)), y,
                                                                      float("nan")), "NonFiniteValue", field=2)
     assert np.all(host(y).view(np.uint32) == SENTINEL_BITS)
+    # A non-finite destination is rejected before anything is written
+    # (gemv.rs:126-127): the other rows keep their values.
+    d0 = np.arange(rows, dtype=np.float32)
+    d0[5] = np.inf
+    d = dev(d0)
+    expect_error(be, lambda: be.gemv_dequant_accumulate_scaled_into(m, dev(np.ones(k, np.float32)), d, 0.5),
+                 "NonFiniteValue", index=5, field=3)
+    assert np.array_equal(host(d).view(np.uint32), d0.view(np.uint32))
