@@ -55,10 +55,10 @@ EXPERT_BYTES = 2 * FFN * 16 * 82 + HIDDEN * 6 * 110                    # 6,733,8
 SHARED_BYTES = 2 * HIDDEN * 16 * 144 + HIDDEN * 16 * 176               # 30,408,704
 BATCH_TOKENS = 64
 COLD_COPIES = 8
-# HBM bytes per launch (read + write) measured with rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
-# over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain copy of
-# known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2384009 + 6144, "down": 2988392 + 19648, "prefill": 325213737 + 25165824}
+# Bytes per launch (read from beyond L2 + written) measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain
+# copy of known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
+MEASURED_TRAFFIC = {"gate": 2402491 + 6144, "down": 3011019 + 19648, "prefill": 193273707 + 25672352}
 
 
 def parse():
@@ -791,6 +791,18 @@ def pmc_workloads():
         be.gemv_f32(gates[c], x, h)
         be.gemv_f32(downs[c], h, y)
     torch.cuda.synchronize()
+    # the Hy3 dense FFN matvecs (IQ2_S gate 13312x4096, IQ3_S down 4096x13312), 4 copies each
+    for ty, rows, k, seed in ((22, 13312, H, 121), (21, H, 13312, 122)):
+        wl = torch.from_numpy(synth.random_matrix(ty, rows, k, seed).reshape(-1)).cuda()
+        ml = [be.upload(ty, rows, k, wl) for _ in range(4)]
+        xl, yl = torch.randn(k, device='cuda'), torch.zeros(rows, device='cuda')
+        torch.cuda.synchronize()
+        for c in range(4):
+            be.gemv_f32(ml[c], xl, yl)
+        torch.cuda.synchronize()
+        for m_ in ml:
+            m_.close()
+        del wl, ml
     # configs[0] Q4_K matvec
     wq = torch.from_numpy(synth.random_matrix(12, H, H, 111).reshape(-1)).cuda()
     qs = [be.upload(12, H, H, wq) for _ in range(8)]
