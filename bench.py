@@ -697,7 +697,7 @@ def bench_prefill(args, be, timer, torch, np, synth):
     [512 x 12288] on the f16 matrix cores with exact integer sums (lbh_gemm_q8_k: activation
     tiles + GEMM)."""
     w = synth.random_matrix(synth.Q5_K, PF_ROWS, HIDDEN, seed=801)
-    copies = 4   # 4 x (34.6 MB packed + 108.5 MB MFMA-ready) in rotation: > the 256 MB Infinity Cache
+    copies = 4   # 4 x (34.6 MB packed + 110.1 MB MFMA-ready) in rotation: > the 256 MB Infinity Cache
     wd = torch.from_numpy(w.reshape(-1)).cuda()
     ms = [be.upload(synth.Q5_K, PF_ROWS, HIDDEN, wd) for _ in range(copies)]
     for m in ms:
@@ -718,6 +718,7 @@ def bench_prefill(args, be, timer, torch, np, synth):
     spread = timer.spread(g, 50, copies)
     torch.cuda.synchronize()
     tops = PF_OPS / us / 1e6
+    footprint = ms[0].device_bytes
     res = {"workload": "configs[4]: prefill 512 tokens, Q8_K activations [512 x 4096] x Q5_K [12288 x 4096] -> f32 "
                        "[512 x 12288], f16 MFMA (v_mfma_f32_32x32x16_f16) on integer operands: exact "
                        "per-(block, lane residue) sums",
@@ -730,9 +731,12 @@ def bench_prefill(args, be, timer, torch, np, synth):
                                      "the i8 instruction at this shape), whose own peak is 2.5 PFLOP/s",
                         "frac_of_f16_instruction_peak": round(tops / MFMA_F16_PEAK_TFLOPS, 4)},
            "hbm_GB/s_algorithmic": round(PF_BYTES / us / 1e3, 1),
+           "prepared_matrix_hbm_bytes": {"total": footprint, "packed": ms[0].nbytes,
+                                         "mfma_ready_copy": footprint - ms[0].nbytes,
+                                         "vs_ggml_bytes": round(footprint / (PF_ROWS * HIDDEN // 256 * 176), 2)},
            "note": "the exact per-block f32 folds (9 chains x 16 blocks per output, separately rounded) run on the "
-                   "VALU at ~19 ops per (row, token, block); they and the tile staging bound the kernel, not the "
-                   "matrix cores"}
+                   "VALU at ~20 ops per (row, token, block); they and the LDS operand reads bound the kernel, not "
+                   "the matrix cores or HBM"}
     check = dict(w=w, q8=q8[:8].cpu().numpy(), y=ys[copies - 1, :8].cpu().numpy())
     for m in ms:
         m.close()

@@ -275,9 +275,12 @@ lbh_status lbh_gemv_dequant_f32(lbh_ctx *ctx, const lbh_matrix *m, const float *
  * in f16), every (block, lane residue) sum is an exact integer below 2^24, and the
  * nine f32 chains per block run in the reference order. */
 
-/* [sync] Builds the matrix's MFMA-ready copy (Q4_K / Q5_K only; 3.8x (Q4_K) or 3.1x
+/* [sync] Builds the matrix's MFMA-ready copy (Q4_K / Q5_K only; 3.9x (Q4_K) or 3.2x
  * (Q5_K) the packed bytes, allocated once and freed with the matrix). */
 lbh_status lbh_matrix_prepare_gemm(lbh_ctx *ctx, lbh_matrix *m, lbh_error *err);
+/* HBM bytes the matrix holds: the packed planes (lbh_matrix_bytes) plus the MFMA-ready
+ * copy once prepared (no reference counterpart: the reference's PackedMatrix is its bytes). */
+size_t lbh_matrix_device_bytes(const lbh_matrix *m);
 
 /* Device workspace bytes of lbh_gemm_q8_k for n_tokens tokens of k elements (0 if k % 256). */
 size_t lbh_gemm_workspace_bytes(size_t n_tokens, size_t k);

@@ -1436,6 +1436,11 @@ lbh_status lbh_matrix_prepare_gemm(lbh_ctx *ctx, lbh_matrix *m, lbh_error *err) 
     return ok(err);
 }
 
+size_t lbh_matrix_device_bytes(const lbh_matrix *m) {
+    if (!m) return 0;
+    return m->bytes + (m->gemm_a ? gemm_a_bytes((int)m->rows, (int)m->nb) : 0);
+}
+
 size_t lbh_gemm_workspace_bytes(size_t n_tokens, size_t k) {
     if (n_tokens == 0 || k == 0 || k % 256) return 0;
     return gemm_b_bytes((int)n_tokens, (int)(k / 256));

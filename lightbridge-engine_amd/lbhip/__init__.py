@@ -95,6 +95,7 @@ def lib() -> C.CDLL:
             "lbh_matrix_k": ([p], sz),
             "lbh_matrix_type": ([p], i32),
             "lbh_matrix_bytes": ([p], sz),
+            "lbh_matrix_device_bytes": ([p], sz),
             "lbh_gemv_into": ([p, p, p, sz, p, sz, p, sz, E], i32),
             "lbh_gemv_accumulate_scaled_into": ([p, p, p, sz, p, sz, C.c_float, p, sz, E], i32),
             "lbh_gemv_q8_k": ([p, p, p, p, C.c_float, i32], i32),
@@ -592,6 +593,11 @@ class DeviceMatrix:
     def prepare_gemm(self) -> None:
         """Build the MFMA-ready copy used by gemm_q8_k (Q4_K / Q5_K)."""
         _call(lib().lbh_matrix_prepare_gemm, self.be.ctx, self.handle)
+
+    @property
+    def device_bytes(self) -> int:
+        """HBM bytes held: the packed planes plus the MFMA-ready copy once prepared."""
+        return lib().lbh_matrix_device_bytes(self.handle)
 
     def read_ggml(self) -> np.ndarray:
         out = np.zeros(self.nbytes, np.uint8)

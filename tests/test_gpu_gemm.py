@@ -117,7 +117,10 @@ def test_gemm_requires_preparation_and_workspace(be, oracle):
     ws = torch.zeros(be.gemm_workspace_bytes(2, 256), dtype=torch.uint8, device="cuda")
     with pytest.raises(lbhip.KernelError):
         be.gemm_q8_k(m, q8, 2, y, ws)           # not prepared
+    assert m.device_bytes == m.nbytes == 32 * 144
     m.prepare_gemm()
+    # one tile of 32 rows x one block: 17 operands of 1 KiB plus the 32 rows' four scale rows
+    assert m.device_bytes == m.nbytes + 17 * 1024 + 32 * 16
     with pytest.raises(lbhip.KernelError):
         be.gemm_q8_k(m, q8, 2, y, ws[:16])      # workspace too small
     iq = be.upload(22, 32, 256, synth.random_matrix(22, 32, 256, seed=2))
