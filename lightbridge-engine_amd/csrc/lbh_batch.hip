@@ -115,15 +115,13 @@ __device__ __forceinline__ void decode(const WSlice<T_IQ2_S, LPU> &w, const void
     const GridRef<T_IQ2_S> grid(gridp);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+        const Iq2sGroup q = iq2s_group(w, g);
         const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
 #pragma unroll
         for (int lg = 0; lg < 4; ++lg) {
-            const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
-            const uint2 code = grid.code(idx);
-            const uint2 sm = grid.sel(byte_of(w.sg[g], lg));
-            const uint32_t sel_lo = sm.x | code.x;
-            const uint32_t sel_hi = sm.y | code.y;
+            const uint2 code = grid.code_at(q.addr(lg));
+            const uint32_t sel_lo = q.sel(2 * lg) | code.x;
+            const uint32_t sel_hi = q.sel(2 * lg + 1) | code.y;
             o.w[8 * g + 2 * lg] = perm(IQ2S_NEG, IQ2S_POS, sel_lo);
             o.w[8 * g + 2 * lg + 1] = perm(IQ2S_NEG, IQ2S_POS, sel_hi);
         }
@@ -728,14 +726,16 @@ constexpr int MX_THREADS = 256;
 constexpr int MX_WAVES = MX_THREADS / 64;
 
 
-// LDS tables: the f16 magnitudes of every codebook entry (IQ2_S 1024 x 8,
-// IQ3_S 512 x 4), then 256 sign masks of eight f16 (bit 15 of element i is
-// bit i of the sign byte); built at compile time, copied to LDS per workgroup.
+// LDS tables: the f16 magnitudes of every codebook entry (IQ2_S 1024 x 8, the
+// entry of index q | h << 8 at byte 2 * iq2s_code_addr(q, h); IQ3_S 512 x 4),
+// then for IQ3_S 256 sign masks of eight f16 (bit 15 of element i is bit i of
+// the sign byte); built at compile time, copied to LDS per workgroup.
 template <int TY>
 struct MxTab {
     static constexpr int ENTRY = TY == T_IQ2_S ? 16 : 8;
     static constexpr int GRID = (TY == T_IQ2_S ? 1024 : 512) * ENTRY;
-    static constexpr int BYTES = GRID + 256 * 16;
+    static constexpr int SIGNS = TY == T_IQ3_S ? 256 * 16 : 0;
+    static constexpr int BYTES = GRID + SIGNS;
 };
 
 // f16 bits of a non-negative integer below 2048 (exact).
@@ -761,8 +761,9 @@ constexpr MxTables make_mx_tables() {
     MxTables t{};
     for (int i = 0; i < 1024; ++i)
         for (int k = 0; k < 4; ++k)
-            t.iq2[i][k] = f16_pair_of((uint32_t)(k_iq2s_vals[i] >> (16 * k)) & 0xffu,
-                                      (uint32_t)(k_iq2s_vals[i] >> (16 * k + 8)) & 0xffu);
+            t.iq2[iq2s_code_addr((uint32_t)i & 255u, (uint32_t)i >> 8) / 8][k] =
+                f16_pair_of((uint32_t)(k_iq2s_vals[i] >> (16 * k)) & 0xffu,
+                            (uint32_t)(k_iq2s_vals[i] >> (16 * k + 8)) & 0xffu);
     for (int i = 0; i < 512; ++i)
         for (int k = 0; k < 2; ++k)
             t.iq3[i][k] = f16_pair_of((k_iq3s_vals[i] >> (16 * k)) & 0xffu, (k_iq3s_vals[i] >> (16 * k + 8)) & 0xffu);
@@ -784,7 +785,8 @@ __device__ __forceinline__ void mx_fill(uint8_t *tab) {
     const uint4 *sg = reinterpret_cast<const uint4 *>(&c_mx_tab.sign[0][0]);
     uint4 *o = reinterpret_cast<uint4 *>(tab);
     for (int i = threadIdx.x; i < MxTab<TY>::GRID / 16; i += MX_THREADS) o[i] = g[i];
-    for (int i = threadIdx.x; i < 256; i += MX_THREADS) o[MxTab<TY>::GRID / 16 + i] = sg[i];
+    if constexpr (MxTab<TY>::SIGNS > 0)
+        for (int i = threadIdx.x; i < 256; i += MX_THREADS) o[MxTab<TY>::GRID / 16 + i] = sg[i];
 }
 
 // Eight f16 magnitudes with their signs applied, times the integer scale ls.
@@ -798,13 +800,18 @@ __device__ __forceinline__ mx_h8 mx_signed_scaled(uint4 mag, uint4 sgn, uint32_t
 
 // A operand of instruction m: the lane's slice holds sub-blocks 2p, 2p + 1;
 // m covers entry m % 4 of sub-block m / 4 (q8_k.rs:337-364 index, sign and
-// scale layout, as slice_sum in lbh_dev.h).
+// scale layout, read from the device encoding as slice_sum in lbh_dev.h).
+// The sign of weight 4t + i sits at bit t of byte i of the group's sign dword:
+// (b0, b0, b1, b1) << (7 - t) puts those of weights 4t, 4t + 1 at bits 15 and
+// 31, the sign bits of the f16 pair (b2, b2, b3, b3: weights 4t + 2, 4t + 3).
 __device__ __forceinline__ mx_h8 mx_a(const WSlice<T_IQ2_S, 4> &w, const uint8_t *tab, int m) {
     const int g = m >> 2, lg = m & 3;
-    const uint32_t h = byte_of(w.qh, g);
-    const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
-    const uint4 mag = reinterpret_cast<const uint4 *>(tab)[idx];
-    const uint4 sgn = reinterpret_cast<const uint4 *>(tab + MxTab<T_IQ2_S>::GRID)[byte_of(w.sg[g], lg)];
+    const Iq2sGroup q = iq2s_group(w, g);
+    const uint4 mag = *reinterpret_cast<const uint4 *>(tab + 2 * q.addr(lg));
+    const uint32_t p01 = perm(q.s, q.s, 0x01010000u), p23 = perm(q.s, q.s, 0x03030202u);
+    const int t0 = 2 * lg, t1 = 2 * lg + 1;
+    const uint4 sgn = make_uint4((p01 << (7 - t0)) & 0x80008000u, (p23 << (7 - t0)) & 0x80008000u,
+                                 (p01 << (7 - t1)) & 0x80008000u, (p23 << (7 - t1)) & 0x80008000u);
     const uint32_t ls = 1u + 2u * ((byte_of(w.sc, g) >> (4 * (lg >> 1))) & 15u);
     return mx_signed_scaled(mag, sgn, ls);
 }

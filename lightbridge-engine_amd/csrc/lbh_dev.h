@@ -411,8 +411,10 @@ __device__ __forceinline__ void load_act_res(const uint8_t *blk, const uint8_t *
 //
 // LDS copies of the IQ codebooks, laid out so a signed grid dword is one v_perm:
 //   IQ2S: uint2 x 1024 (8 KiB) of byte codes 0/1/2 for the magnitudes 8/25/43
-//         (the only values in the codebook); v_perm with selector code + 4*sign
-//         picks from the constant dwords {8,25,43} / {-8,-25,-43}.
+//         (the only values in the codebook), entry q | h << 8 at byte address
+//         iq2s_code_addr(q, h) (the address the encoded qs and qh bytes give,
+//         lbh_layout.h); v_perm with selector code + 4*sign picks from the
+//         constant dwords {8,25,43} / {-8,-25,-43}.
 //   IQ3S: uint32 x 512 (2 KiB) magnitude words; the negation is one VALU
 //         subtraction (neg_bytes), cheaper than the 4 more LDS bytes per
 //         lookup a stored (magnitude, negation) pair costs.
@@ -434,7 +436,29 @@ constexpr int T_IQ3S_SGN = 0x100 | T_IQ3_S;
 template <int TY>
 struct GridLDS {
     static constexpr int MAIN = TY == T_IQ2_S ? 1024 * 8 : TY == T_IQ3_S ? 512 * 8 : 0;
-    static constexpr int BYTES = TY == T_IQ3S_SGN ? 8192 * 4 : MAIN > 0 ? MAIN + 256 * 8 : 0;
+    static constexpr int BYTES = TY == T_IQ3S_SGN ? 8192 * 4 : TY == T_IQ3_S ? MAIN + 256 * 8 : MAIN;
+};
+
+// Byte address of IQ2S code entry q | h << 8 (q: 8 bits, h: 2 bits).
+__host__ __device__ constexpr uint32_t iq2s_code_addr(uint32_t q, uint32_t h) {
+    return 256u * ((q >> 5) | (h << 3)) + 8u * (q & 31u);
+}
+
+// One IQ2S group of four lookups in the device encoding (lbh_layout.h): its
+// rotated qs dword q, the qh dword hw holding its high bits at bits 2k, 2k + 1
+// of each byte, and its sign dword s.  addr(j) is lookup j's code address,
+// sel(t) the v_perm sign bits of its weights 4t .. 4t + 3 (t = 2j, 2j + 1).
+struct Iq2sGroup {
+    uint32_t x, y, s;
+    // k: the group's field in hw (a compile-time constant after unrolling)
+    __device__ __forceinline__ static Iq2sGroup make(uint32_t q, uint32_t hw, int k, uint32_t s) {
+        const uint32_t hs = (k < 2 ? hw << (3 - 2 * k) : hw >> (2 * k - 3)) & 0x18181818u;
+        return Iq2sGroup{q & 0xf8f8f8f8u, (q & 0x07070707u) | hs, s};
+    }
+    __device__ __forceinline__ uint32_t addr(int j) const {
+        return __builtin_amdgcn_perm(y, x, 0x0c0c0000u | ((4u + (uint32_t)j) << 8) | (uint32_t)j);
+    }
+    __device__ __forceinline__ uint32_t sel(int t) const { return (t >= 2 ? s >> (t - 2) : s << (2 - t)) & 0x04040404u; }
 };
 constexpr int IQ3_SIGN_OFF = 512 * 8;
 
@@ -501,17 +525,18 @@ __device__ __forceinline__ void iq3_group_addrs(uint32_t q0, uint32_t q1, uint32
     }
 }
 
-// A lane's view of a codebook in LDS.  VSEL computes the sign selectors in
-// VALU (three ops per nibble) instead of reading the sign table: one LDS read
-// fewer per eight weights, for kernels whose LDS issue, not VALU, is short.
+// A lane's view of a codebook in LDS.  VSEL computes the IQ3S sign selectors
+// in VALU (three ops per nibble) instead of reading the sign table: one LDS
+// read fewer per eight weights, for kernels whose LDS issue, not VALU, is
+// short.
 template <int TY, bool VSEL = false>
 struct GridRef {
     const uint8_t *g;
     __device__ __forceinline__ explicit GridRef(const void *p) : g(static_cast<const uint8_t *>(p)) {}
-    // IQ2S code entry of 10-bit index i; IQ3S pair at byte offset o
-    // (iq3_pair_offset); selectors of sign byte sb (sign_lut_entry /
-    // iq3_sign_entry).
-    __device__ __forceinline__ uint2 code(uint32_t i) const { return reinterpret_cast<const uint2 *>(g)[i]; }
+    // IQ2S code entry at byte address a (iq2s_code_addr); IQ3S pair at byte
+    // offset o (iq3_pair_offset); IQ3S selectors of sign byte sb
+    // (iq3_sign_entry).
+    __device__ __forceinline__ uint2 code_at(uint32_t a) const { return *reinterpret_cast<const uint2 *>(g + a); }
     __device__ __forceinline__ uint2 pair(uint32_t o) const { return *reinterpret_cast<const uint2 *>(g + o); }
     __device__ __forceinline__ uint2 sel(uint32_t sb) const {
         if constexpr (VSEL) {
@@ -523,14 +548,6 @@ struct GridRef {
         }
     }
 };
-
-// Sign-byte table appended to the IQ2S codes: entry s = the v_perm selector
-// bits (4 in byte i when bit i is set) of the low and the high nibble of s,
-// so applying eight sign bits is one LDS read and two ORs.  Computed, not
-// loaded: nib * 0x810204 moves bit i to bit 8i + 2 with no carries.
-__device__ __forceinline__ uint2 sign_lut_entry(uint32_t s) {
-    return make_uint2(((s & 15u) * 0x810204u) & 0x04040404u, ((s >> 4) * 0x810204u) & 0x04040404u);
-}
 
 // Sign-byte table appended to the IQ3S entries: entry s = the full v_perm
 // selectors applying the low and the high nibble of s to a (magnitude,
@@ -545,7 +562,7 @@ __device__ __forceinline__ uint32_t iq3_signed(uint2 pr, uint32_t sel) { return 
 // The LDS images of both tables (GridLDS layout), built at compile time from
 // the codebooks: a workgroup's fill is a plain copy with 16-byte loads.
 struct GridImages {
-    uint32_t iq2s[2 * (1024 + 256)];
+    uint32_t iq2s[2 * 1024];
     uint32_t iq3s[2 * (512 + 256)];
     constexpr GridImages() : iq2s{}, iq3s{} {
         const uint64_t g2[1024] = {LBH_IQ2S_GRID_VALUES};
@@ -555,12 +572,8 @@ struct GridImages {
                 const uint32_t m = (uint32_t)(g2[i] >> (8 * e)) & 0xffu;
                 c[e >> 2] |= (m == 8 ? 0u : m == 25 ? 1u : 2u) << (8 * (e & 3));
             }
-            iq2s[2 * i] = c[0], iq2s[2 * i + 1] = c[1];
-        }
-        // sign_lut_entry: nib * 0x810204 moves bit i to bit 8i + 2 with no carries.
-        for (uint32_t sb = 0; sb < 256; ++sb) {
-            iq2s[2 * (1024 + sb)] = ((sb & 15u) * 0x810204u) & 0x04040404u;
-            iq2s[2 * (1024 + sb) + 1] = ((sb >> 4) * 0x810204u) & 0x04040404u;
+            const uint32_t a = iq2s_code_addr((uint32_t)i & 255u, (uint32_t)i >> 8) / 4;
+            iq2s[a] = c[0], iq2s[a + 1] = c[1];
         }
         const uint32_t g3[512] = {LBH_IQ3S_GRID_VALUES};
         for (uint32_t i = 0; i < 512; ++i) {
@@ -717,7 +730,9 @@ __device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t
         w.qs[0] = a.x, w.qs[1] = a.y;
         w.sg[0] = c.x, w.sg[1] = c.y;
         const uint32_t e = u16 + 2u * (uint32_t)p;
-        w.qh = bld16(P, e, 4 * P.U16);
+        // the qh dword of groups 4 (p / 2) .. + 3, shifted so that this part's
+        // groups 2p, 2p + 1 hold fields 0 and 1
+        w.qh = bld32(P, u16 + 4u * (uint32_t)(p >> 1), 4 * P.U16) >> (4 * (p & 1));
         w.sc = bld16(P, e + 8, 4 * P.U16);
         w.qh2 = w.sc2 = 0;
     }
@@ -727,70 +742,55 @@ __device__ __forceinline__ void load_slice(const Planes &P, uint32_t u, uint32_t
 constexpr uint32_t IQ2S_POS = 0x002b1908u;
 constexpr uint32_t IQ2S_NEG = 0x00d5e7f8u;
 
-// IQ2_S integer block sum over the slice's groups (q8_k.rs:337-364).  With
-// GB > 0 the codebook and sign-table reads of GB groups at a time are issued
-// before any of them is used (one LDS round trip per GB groups instead of
-// one per pair of lookups, at the cost of the registers that hold them: a
-// latency-bound matvec with one wave per SIMD gains, kernels that rely on
-// occupancy keep GB = 0, the compiler's interleaved schedule).
+// IQ2_S integer block sum over the slice's groups (q8_k.rs:337-364), from the
+// device encoding (lbh_layout.h): per group one v_perm per lookup for its
+// code address and one shift-and-mask per four weights for their signs.  With
+// GB > 0 the codebook reads of GB groups at a time are issued before any of
+// them is used (one LDS round trip per GB groups instead of one per lookup,
+// at the cost of the registers that hold them: a latency-bound matvec with one
+// wave per SIMD gains, kernels that rely on occupancy keep GB = 0, the
+// compiler's interleaved schedule).
+template <int LPU>
+__device__ __forceinline__ Iq2sGroup iq2s_group(const WSlice<T_IQ2_S, LPU> &w, int g) {
+    constexpr int G = 8 / LPU;
+    return Iq2sGroup::make(w.qs[g], G == 8 && g >= 4 ? w.qh2 : w.qh, g & 3, w.sg[g]);
+}
+
 template <int LPU, int GB = 0, class A, bool VS>
 __device__ __forceinline__ int32_t slice_sum(const WSlice<T_IQ2_S, LPU> &w, const A &a, const GridRef<T_IQ2_S, VS> &grid) {
     constexpr int G = 8 / LPU;
+    constexpr int GC = GB == 0 ? 1 : G < GB ? G : GB;
     int32_t bsum = 0;
-    if constexpr (GB == 0) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
+    for (int g0 = 0; g0 < G; g0 += GC) {
+        uint2 code[GC][4];
+        if constexpr (GB > 0) {
+#pragma unroll
+            for (int k = 0; k < GC; ++k) {
+                const Iq2sGroup q = iq2s_group(w, g0 + k);
+#pragma unroll
+                for (int lg = 0; lg < 4; ++lg) code[k][lg] = grid.code_at(q.addr(lg));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int k = 0; k < GC; ++k) {
+            const int g = g0 + k;
+            const Iq2sGroup q = iq2s_group(w, g);
             const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
             uint32_t aq[8];
             act_group(a, g, aq);
             int32_t part[2] = {0, 0};
 #pragma unroll
             for (int lg = 0; lg < 4; ++lg) {
-                const uint32_t idx = byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u);
-                const uint2 code = grid.code(idx);
-                // selector bits of the eight sign bits: byte i takes the
-                // negated source (selector 4 + code) when sign bit i is set
-                const uint2 sm = grid.sel(byte_of(w.sg[g], lg));
-                const uint32_t sel_lo = sm.x | code.x;
-                const uint32_t sel_hi = sm.y | code.y;
+                const uint2 c = GB > 0 ? code[k][lg] : grid.code_at(q.addr(lg));
+                // byte i takes the negated source (selector 4 + code) when its sign is set
+                const uint32_t sel_lo = q.sel(2 * lg) | c.x;
+                const uint32_t sel_hi = q.sel(2 * lg + 1) | c.y;
                 part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), aq[2 * lg], part[lg >> 1]);
                 part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), aq[2 * lg + 1], part[lg >> 1]);
             }
             bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
-        }
-    } else {
-        constexpr int GC = G < GB ? G : GB;
-#pragma unroll
-        for (int g0 = 0; g0 < G; g0 += GC) {
-            uint2 code[GC][4], sm[GC][4];
-#pragma unroll
-            for (int k = 0; k < GC; ++k) {
-                const int g = g0 + k;
-                const uint32_t h = byte_of(g < 4 ? w.qh : w.qh2, g & 3);
-#pragma unroll
-                for (int lg = 0; lg < 4; ++lg) {
-                    code[k][lg] = grid.code(byte_of(w.qs[g], lg) | ((h << (8 - 2 * lg)) & 0x300u));
-                    sm[k][lg] = grid.sel(byte_of(w.sg[g], lg));
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int k = 0; k < GC; ++k) {
-                const int g = g0 + k;
-                const uint32_t sc = byte_of(g < 4 ? w.sc : w.sc2, g & 3);
-                uint32_t aq[8];
-                act_group(a, g, aq);
-                int32_t part[2] = {0, 0};
-#pragma unroll
-                for (int lg = 0; lg < 4; ++lg) {
-                    const uint32_t sel_lo = sm[k][lg].x | code[k][lg].x;
-                    const uint32_t sel_hi = sm[k][lg].y | code[k][lg].y;
-                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_lo), aq[2 * lg], part[lg >> 1]);
-                    part[lg >> 1] = dot4(perm(IQ2S_NEG, IQ2S_POS, sel_hi), aq[2 * lg + 1], part[lg >> 1]);
-                }
-                bsum += mul24((int32_t)(1 + 2 * (sc & 15u)), part[0]) + mul24((int32_t)(1 + 2 * (sc >> 4)), part[1]);
-            }
         }
     }
     return bsum;

@@ -37,12 +37,17 @@ __device__ __forceinline__ uint32_t grm32(const uint8_t *g, int t) {
     return (uint32_t)g[t] | ((uint32_t)g[t + 8] << 8) | ((uint32_t)g[t + 16] << 16) | ((uint32_t)g[t + 24] << 24);
 }
 
-// One GGML block at `blk` into the one-lane-per-unit slice of its type.
+// One GGML block at `blk` into the one-lane-per-unit slice of its type (IQ2_S
+// through its device encoding, iq2s_encode).
 __device__ __forceinline__ void load_slice_ggml(const uint8_t *blk, WSlice<T_IQ2_S, 1> &w) {
-    w.d = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
+    uint8_t g[82], e[82];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w.qs[i] = gb32(blk + 2 + 4 * i), w.sg[i] = gb32(blk + 34 + 4 * i);
-    w.qh = gb32(blk + 66), w.qh2 = gb32(blk + 70), w.sc = gb32(blk + 74), w.sc2 = gb32(blk + 78);
+    for (int i = 0; i < 82; ++i) g[i] = blk[i];
+    iq2s_encode(g, e);
+    w.d = (uint32_t)e[0] | ((uint32_t)e[1] << 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w.qs[i] = gb32(e + 2 + 4 * i), w.sg[i] = gb32(e + 34 + 4 * i);
+    w.qh = gb32(e + 66), w.qh2 = gb32(e + 70), w.sc = gb32(e + 74), w.sc2 = gb32(e + 78);
 }
 
 __device__ __forceinline__ void load_slice_ggml(const uint8_t *blk, WSlice<T_IQ3_S, 1> &w) {
@@ -163,20 +168,23 @@ __device__ __forceinline__ void dequant_group(const Planes &P, uint32_t u, int s
         }
     } else if constexpr (TY == T_IQ2_S) {
         const float d = f16_to_f32(bld16(P, u * 2, 5 * P.U16));
+        // device encoding (lbh_layout.h): rotated qs bytes, the qh dword of
+        // groups 4 (sub / 4) .. + 3, bit-sliced sign dword
         const uint32_t qs = bld32(P, u * 16 + 4 * (sub & 3), (sub >> 2) * P.U16);
         const uint32_t sg = bld32(P, u * 16 + 4 * (sub & 3), (2 + (sub >> 2)) * P.U16);
-        const uint32_t qh = bld8(P, u * 16 + sub, 4 * P.U16);
+        const uint32_t qh = bld32(P, u * 16 + 4 * (sub >> 2), 4 * P.U16);
         const uint32_t sc = bld8(P, u * 16 + 8 + sub, 4 * P.U16);
         const float bs[2] = {__fmul_rn(__fmul_rn(d, __fadd_rn(0.5f, (float)(sc & 15u))), 0.25f),
                              __fmul_rn(__fmul_rn(d, __fadd_rn(0.5f, (float)(sc >> 4))), 0.25f)};
 #pragma unroll
         for (int lg = 0; lg < 4; ++lg) {
-            const uint32_t idx = byte_of(qs, lg) | ((qh << (8 - 2 * lg)) & 0x300u);
+            const uint32_t h = (byte_of(qh, lg) >> (2 * (sub & 3))) & 3u;
+            const uint32_t idx = iq2s_unrot_q(byte_of(qs, lg)) | (h << 8);
             const uint64_t grid = c_iq2s_grid[idx];
-            const uint32_t s = byte_of(sg, lg);
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
-                const float sign = (s >> l) & 1u ? -1.0f : 1.0f;
+                // weight 8 lg + l of the group: bit 2 lg + l / 4 of sign byte l % 4
+                const float sign = (byte_of(sg, l & 3) >> (2 * lg + (l >> 2))) & 1u ? -1.0f : 1.0f;
                 const float w = __fmul_rn(__fmul_rn(bs[lg >> 1], (float)((grid >> (8 * l)) & 0xffu)), sign);
                 out[8 * lg + l] = __fmul_rn(w, x[8 * lg + l]);
             }

@@ -91,17 +91,42 @@ __device__ __forceinline__ long long dev_offset(int ty, long long U, long long u
     return chunk(3 + idx / 16, idx % 16);
 }
 
+// One unit's GGML bytes `g` to the device layout (IQ2_S through its bit
+// encoding, iq2s_encode), and back.
+template <int TY>
+__device__ __forceinline__ void unit_to_device(const uint8_t *g, uint8_t *dst, long long U, long long u) {
+    constexpr int BB = layout_of(TY).block_bytes;
+    if constexpr (TY == T_IQ2_S) {
+        uint8_t in[BB], e[BB];
+        for (int p = 0; p < BB; ++p) in[p] = g[p];
+        iq2s_encode(in, e);
+        for (int p = 0; p < BB; ++p) dst[dev_offset(TY, U, u, p)] = e[p];
+    } else {
+        for (int p = 0; p < BB; ++p) dst[dev_offset(TY, U, u, p)] = g[p];
+    }
+}
+
+template <int TY>
+__device__ __forceinline__ void unit_to_ggml(const uint8_t *src, uint8_t *g, long long U, long long u) {
+    constexpr int BB = layout_of(TY).block_bytes;
+    if constexpr (TY == T_IQ2_S) {
+        uint8_t e[BB], out[BB];
+        for (int p = 0; p < BB; ++p) e[p] = src[dev_offset(TY, U, u, p)];
+        iq2s_decode(e, out);
+        for (int p = 0; p < BB; ++p) g[p] = out[p];
+    } else {
+        for (int p = 0; p < BB; ++p) g[p] = src[dev_offset(TY, U, u, p)];
+    }
+}
+
 template <int TY>
 __global__ void k_repack(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, long long U, int to_device) {
     constexpr int BB = layout_of(TY).block_bytes;
     for (long long u = (long long)blockIdx.x * blockDim.x + threadIdx.x; u < U; u += (long long)gridDim.x * blockDim.x) {
-        for (int p = 0; p < BB; ++p) {
-            const long long o = dev_offset(TY, U, u, p);
-            if (to_device)
-                dst[o] = src[u * BB + p];
-            else
-                dst[u * BB + p] = src[o];
-        }
+        if (to_device)
+            unit_to_device<TY>(src + u * BB, dst, U, u);
+        else
+            unit_to_ggml<TY>(src, dst + u * BB, U, u);
     }
 }
 
@@ -112,7 +137,7 @@ __global__ void k_repack_range(const uint8_t *__restrict__ src, uint8_t *__restr
                                long long n) {
     constexpr int BB = layout_of(TY).block_bytes;
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
-        for (int p = 0; p < BB; ++p) dst[dev_offset(TY, U, u0 + i, p)] = src[i * BB + p];
+        unit_to_device<TY>(src + i * BB, dst, U, u0 + i);
 }
 
 // First non-finite f16 d / dmin in unit order (validate_scales, k_quants.rs:178-208).

@@ -22,6 +22,23 @@
 // 4 * (l % 8) + l / 8, so dword t of a group holds the four elements whose
 // index is congruent to t mod 8 — the lane split of the reference K-quant dot
 // (crates/bridge-quant-layout/src/q8_k.rs:301-312) becomes one dot4 per lane.
+//
+// IQ2_S blocks are stored bit-permuted inside their qs, sign and qh bytes (a
+// bijection on the 82 bytes; d and the scales unchanged), so the decode of a
+// group of 32 weights (four 8-weight lookups l = 4g + j, q8_k.rs:337-364)
+// needs no per-lookup bit extraction:
+//   qs byte l    the low 8 bits q of lookup l's grid index, rotated:
+//                (q & 31) << 3 | q >> 5.  With the lookup's two high bits h at
+//                bits 3-4 of a byte, (rotated & 0xf8) + 256 * ((rotated & 7) |
+//                h << 3) is a byte address of an 8 KiB table (one v_perm for a
+//                lookup, the qs dword supplying four);
+//   qh dword j   (bytes 4j..4j+3 of the qh bytes) byte j', bits 2k, 2k + 1:
+//                the high bits of lookup j' of group 4j + k (a 4 x 4 transpose
+//                of the 2-bit fields of qh[4j..4j+3]);
+//   sign dword g (sign bytes 4g..4g+3) byte i, bit k: the sign of weight
+//                32g + 4k + i, so the four signs of weights 32g + 4k .. + 3 sit
+//                at bit k of consecutive bytes (one shift and mask give the
+//                v_perm selector bits that apply them).
 #pragma once
 #include <stdint.h>
 
@@ -50,5 +67,47 @@ __host__ __device__ constexpr bool is_dot_type(int ty) {
 
 // Position of byte l (0..31) of a 32-byte group in residue-major order.
 __host__ __device__ constexpr int residue_pos(int l) { return 4 * (l % 8) + l / 8; }
+
+// IQ2_S block bytes: d 0-1, qs 2-33, signs 34-65, qh 66-73, scales 74-81.
+__host__ __device__ constexpr uint8_t iq2s_rot_q(uint32_t q) { return (uint8_t)(((q & 31u) << 3) | (q >> 5)); }
+__host__ __device__ constexpr uint8_t iq2s_unrot_q(uint32_t r) { return (uint8_t)((r >> 3) | ((r & 7u) << 5)); }
+
+// GGML bytes g of one IQ2_S block -> its device encoding e (82 bytes each).
+__host__ __device__ inline void iq2s_encode(const uint8_t *g, uint8_t *e) {
+    e[0] = g[0], e[1] = g[1];
+    for (int l = 0; l < 32; ++l) e[2 + l] = iq2s_rot_q(g[2 + l]);
+    for (int grp = 0; grp < 8; ++grp)
+        for (int i = 0; i < 4; ++i) {
+            uint32_t v = 0;
+            for (int k = 0; k < 8; ++k) v |= ((uint32_t)(g[34 + 4 * grp + (k >> 1)] >> (4 * (k & 1) + i)) & 1u) << k;
+            e[34 + 4 * grp + i] = (uint8_t)v;
+        }
+    for (int j = 0; j < 2; ++j)
+        for (int jj = 0; jj < 4; ++jj) {
+            uint32_t v = 0;
+            for (int k = 0; k < 4; ++k) v |= ((uint32_t)(g[66 + 4 * j + k] >> (2 * jj)) & 3u) << (2 * k);
+            e[66 + 4 * j + jj] = (uint8_t)v;
+        }
+    for (int s = 74; s < 82; ++s) e[s] = g[s];
+}
+
+// The inverse of iq2s_encode.
+__host__ __device__ inline void iq2s_decode(const uint8_t *e, uint8_t *g) {
+    g[0] = e[0], g[1] = e[1];
+    for (int l = 0; l < 32; ++l) g[2 + l] = iq2s_unrot_q(e[2 + l]);
+    for (int grp = 0; grp < 8; ++grp)
+        for (int jj = 0; jj < 4; ++jj) {
+            uint32_t v = 0;
+            for (int b = 0; b < 8; ++b) v |= ((uint32_t)(e[34 + 4 * grp + (b & 3)] >> (2 * jj + (b >> 2))) & 1u) << b;
+            g[34 + 4 * grp + jj] = (uint8_t)v;
+        }
+    for (int j = 0; j < 2; ++j)
+        for (int k = 0; k < 4; ++k) {
+            uint32_t v = 0;
+            for (int jj = 0; jj < 4; ++jj) v |= ((uint32_t)(e[66 + 4 * j + jj] >> (2 * k)) & 3u) << (2 * jj);
+            g[66 + 4 * j + k] = (uint8_t)v;
+        }
+    for (int s = 74; s < 82; ++s) g[s] = e[s];
+}
 
 }  // namespace lbh
