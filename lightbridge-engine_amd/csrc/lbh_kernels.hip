@@ -91,16 +91,67 @@ __device__ __forceinline__ long long dev_offset(int ty, long long U, long long u
     return chunk(3 + idx / 16, idx % 16);
 }
 
+// The IQ2_S sign dword of one group in its device encoding (iq2s_encode):
+// byte i, bit k = bit 4k + i of the GGML dword (bit b of sign byte j is the
+// sign of weight 8j + b = 4k + i, k = 2j + b / 4).  Per output byte: every
+// fourth bit from i, compressed.
+__device__ __forceinline__ uint32_t iq2s_sign_dword(uint32_t o) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t x = (o >> i) & 0x11111111u;    // bit 4k
+        x = (x | (x >> 3)) & 0x03030303u;       // bits 2m, 2m + 1 -> byte m bits 0-1
+        x = (x | (x >> 6)) & 0x000f000fu;
+        x = (x | (x >> 12)) & 0xffu;
+        r |= x << (8 * i);
+    }
+    return r;
+}
+
+// The IQ2_S qh dword of groups 4j .. 4j + 3 in its device encoding: byte l,
+// bits 2k, 2k + 1 = bits 2l, 2l + 1 of GGML byte k (a 4 x 4 transpose of
+// 2-bit fields).
+__device__ __forceinline__ uint32_t iq2s_qh_dword(uint32_t o) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int l = 0; l < 4; ++l) r |= ((o >> (8 * k + 2 * l)) & 3u) << (8 * l + 2 * k);
+    return r;
+}
+
 // One unit's GGML bytes `g` to the device layout (IQ2_S through its bit
 // encoding, iq2s_encode), and back.
 template <int TY>
 __device__ __forceinline__ void unit_to_device(const uint8_t *g, uint8_t *dst, long long U, long long u) {
     constexpr int BB = layout_of(TY).block_bytes;
     if constexpr (TY == T_IQ2_S) {
-        uint8_t in[BB], e[BB];
-        for (int p = 0; p < BB; ++p) in[p] = g[p];
-        iq2s_encode(in, e);
-        for (int p = 0; p < BB; ++p) dst[dev_offset(TY, U, u, p)] = e[p];
+        // d, then 20 dwords (qs 0-7, signs 8-15, qh 16-17, scales 18-19):
+        // halfword loads from an even address (every block of a buffer that
+        // starts even), else byte loads
+        uint32_t v[20], d;
+        if ((reinterpret_cast<uintptr_t>(g) & 1u) == 0) {
+            const uint16_t *h = reinterpret_cast<const uint16_t *>(g);
+            d = h[0];
+#pragma unroll
+            for (int i = 0; i < 20; ++i) v[i] = (uint32_t)h[1 + 2 * i] | ((uint32_t)h[2 + 2 * i] << 16);
+        } else {
+            d = (uint32_t)g[0] | ((uint32_t)g[1] << 8);
+#pragma unroll
+            for (int i = 0; i < 20; ++i)
+                v[i] = (uint32_t)g[2 + 4 * i] | ((uint32_t)g[3 + 4 * i] << 8) | ((uint32_t)g[4 + 4 * i] << 16) |
+                       ((uint32_t)g[5 + 4 * i] << 24);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = ((v[i] & 0x1f1f1f1fu) << 3) | ((v[i] >> 5) & 0x07070707u);
+#pragma unroll
+        for (int i = 8; i < 16; ++i) v[i] = iq2s_sign_dword(v[i]);
+        v[16] = iq2s_qh_dword(v[16]), v[17] = iq2s_qh_dword(v[17]);
+        uint4 *c = reinterpret_cast<uint4 *>(dst + u * 16);
+        const long long cs = U;   // chunk plane stride in uint4
+#pragma unroll
+        for (int k = 0; k < 5; ++k) c[k * cs] = make_uint4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        reinterpret_cast<uint16_t *>(dst + 5 * U * 16)[u] = (uint16_t)d;
     } else {
         for (int p = 0; p < BB; ++p) dst[dev_offset(TY, U, u, p)] = g[p];
     }
