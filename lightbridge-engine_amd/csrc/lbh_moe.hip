@@ -84,10 +84,20 @@ __device__ __forceinline__ ExpertDev routed_view(const MoeArgs &a, int s) {
         const uint32_t id = a.route_dev ? scalar_read(&a.route_dev->ids[su]) : a.route.ids[su];
         return scalar_read(&a.experts[__builtin_amdgcn_readfirstlane((int)id)]);
     }
-    ExpertDev v = a.routed_shape;
-    v.gate.planes = a.routed_planes[su][0];
-    v.up.planes = a.routed_planes[su][1];
-    v.down.planes = a.routed_planes[su][2];
+    // The shape and the slot's plane pointers are read from the
+    // kernel-argument segment through its own pointer (MoeArgs is the
+    // launch's only argument, at offset 0): a copy of the by-value argument's
+    // shape, then modified, made the compiler keep a private copy of it, and
+    // a kernel that declares a private segment has its workgroups' launch
+    // limited by the scratch allocation.
+    using KBytes = const __attribute__((address_space(4))) uint8_t *;
+    using KPtr = const __attribute__((address_space(4))) uint64_t *;
+    const KBytes args = (KBytes)__builtin_amdgcn_kernarg_segment_ptr();
+    const KPtr rp = (KPtr)(args + __builtin_offsetof(MoeArgs, routed_planes)) + 3 * su;
+    ExpertDev v = scalar_read((const ExpertDev *)(args + __builtin_offsetof(MoeArgs, routed_shape)));
+    v.gate.planes = reinterpret_cast<const uint8_t *>(rp[0]);
+    v.up.planes = reinterpret_cast<const uint8_t *>(rp[1]);
+    v.down.planes = reinterpret_cast<const uint8_t *>(rp[2]);
     return v;
 }
 __device__ __forceinline__ float route_coef(const MoeArgs &a, int s) {
