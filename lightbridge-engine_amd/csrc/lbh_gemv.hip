@@ -27,6 +27,16 @@ constexpr int GEMV_THREADS_LARGE = 512;
 constexpr int GEMV_THREADS_XL = 1024;
 constexpr int MAX_NB = 64;
 
+#ifdef LBH_WAVE_TIMELINE
+// Per-wave timeline of the matvec (a profiling build only: make timeline):
+// s_memrealtime (100 MHz) at the kernel's start, the end of the prologue, the
+// barrier, the first step's weights landed, that step folded, and the end;
+// then the wave's step count and workgroup.
+constexpr int TL_WAVES = 16384;
+__device__ unsigned long long g_wave_timeline[TL_WAVES * 8];
+__device__ __forceinline__ unsigned long long tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+#endif
+
 __device__ __forceinline__ bool status_set(const DevStatus *st) {
     return st && (st->first_bad_input != ~0ull || st->first_bad_dest != ~0ull);
 }
@@ -86,6 +96,10 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     // row another lane loads) so the wait before the stores counts exactly the
     // weight loads issued after the prologue's; the other D - 1 steps go out
     // after the barrier.
+#ifdef LBH_WAVE_TIMELINE
+    unsigned long long tl[6] = {tl_now(), 0, 0, 0, 0, 0};
+    int tl_steps = 0;
+#endif
     int it = blockIdx.x * GEMV_WAVES + wid;
     const GridIn<GT, NT> gin = grid_load<GT, NT>();
     // The input blocks of the first QP quantize passes are loaded here, ahead
@@ -136,7 +150,13 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
             if (i < NB * 64) *reinterpret_cast<uint32_t *>(s_q8q + (i >> 6) * RES_STRIDE + 4 * (i & 63)) = cp[c];
         }
     }
+#ifdef LBH_WAVE_TIMELINE
+    tl[1] = tl_now();
+#endif
     __syncthreads();
+#ifdef LBH_WAVE_TIMELINE
+    tl[2] = tl_now();
+#endif
 #pragma unroll
     for (int d = 1; d < D; ++d) issue(it + d * nw, w[d]);
     if (status_set(p.status)) return;
@@ -159,6 +179,12 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
     }
 
     auto process = [&](int it, const W &w) {
+#ifdef LBH_WAVE_TIMELINE
+        if (tl_steps == 0) {
+            __builtin_amdgcn_s_waitcnt(0);
+            tl[3] = tl_now();
+        }
+#endif
         const int r = it * L.rpw + L.slot;
         const bool on = L.lane_on && r < rows;
         // One wave per SIMD: the codebook reads are gathered (the latency of a
@@ -168,6 +194,9 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
             row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8, A, GR>(w, act, on, L, s_grid, s_fold[wid],
                                                                  p.block_sums, (long long)r * NB + L.b);
         if (on && L.leader()) store_y(p, r, v);
+#ifdef LBH_WAVE_TIMELINE
+        if (tl_steps++ == 0) tl[4] = tl_now();
+#endif
     };
 
     // Software pipeline over a ring of D register buffers, unrolled D times so
@@ -183,6 +212,17 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
             it += nw;
         }
     }
+#ifdef LBH_WAVE_TIMELINE
+    tl[5] = tl_now();
+    const int gw = blockIdx.x * GEMV_WAVES + wid;
+    if (lane == 0 && gw < TL_WAVES) {
+        unsigned long long *o = g_wave_timeline + (long long)gw * 8;
+#pragma unroll
+        for (int i = 0; i < 6; ++i) o[i] = tl[i];
+        o[6] = (unsigned long long)tl_steps;
+        o[7] = blockIdx.x;
+    }
+#endif
 }
 
 static inline int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
@@ -297,3 +337,15 @@ hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
 }
 
 }  // namespace lbh
+
+#ifdef LBH_WAVE_TIMELINE
+// The per-wave timeline of the last matvec launches (8 words per wave, wave
+// index = workgroup * waves per workgroup + wave): read and clear.
+extern "C" int lbh_wave_timeline_read(void *host, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(lbh::g_wave_timeline), bytes, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int lbh_wave_timeline_clear() {
+    static unsigned long long zeros[lbh::TL_WAVES * 8];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(lbh::g_wave_timeline), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#endif
