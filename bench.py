@@ -58,7 +58,7 @@ COLD_COPIES = 8
 # Bytes per launch (read from beyond L2 + written) measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain
 # copy of known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2402491 + 6144, "down": 3011019 + 19648, "prefill": 193273707 + 25672352}
+MEASURED_TRAFFIC = {"gate": 2368682 + 6144, "down": 3022281 + 19648, "prefill": 193271527 + 25638800}
 
 
 def parse():
