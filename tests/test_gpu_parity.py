@@ -102,6 +102,15 @@ def test_matrix_upload_round_trips_the_ggml_bytes(be, ty):
     assert np.array_equal(m.read_ggml(), w.reshape(-1))
     m2 = be.upload(ty, 33, 1536, dev(w.reshape(-1)))
     assert np.array_equal(m2.read_ggml(), w.reshape(-1))
+    # GGML bytes at an odd device address (the upload repack's byte-load path)
+    buf = dev(np.concatenate([np.zeros(1, np.uint8), w.reshape(-1)]))
+    m3 = be.upload(ty, 33, 1536, buf[1:])
+    assert np.array_equal(m3.read_ggml(), w.reshape(-1))
+    x = np.random.default_rng(ty).standard_normal(1536).astype(np.float32)
+    y2, y3 = torch.zeros(33, device="cuda"), torch.zeros(33, device="cuda")
+    be.gemv_f32(m2, dev(x), y2)
+    be.gemv_f32(m3, dev(x), y3)
+    assert np.array_equal(host(y2).view(np.uint32), host(y3).view(np.uint32))
 
 
 @pytest.mark.parametrize("ty,name", [(Q4_K, "q4-k"), (Q5_K, "q5-k"), (IQ2_S, "iq2-s"), (IQ3_S, "iq3-s")])
