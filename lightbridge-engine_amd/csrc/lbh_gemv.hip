@@ -123,13 +123,18 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
         }
     }
     W w[D];
-    // Large IQ3_S instances: every wave's prologue loads go out before any
-    // wave's weight loads (a plain s_barrier, no memory wait), so the
+    // 512-thread IQ3_S instances: every wave's prologue loads go out before
+    // any wave's weight loads (a plain s_barrier, no memory wait), so the
     // activation and table reads do not queue behind the weight burst
-    // (measured on MI355X: IQ3_S 4096x13312 11.2 -> 10.7 us, 4096x8192 7.4 ->
-    // 7.0 us; the IQ2_S instances measured slower with it).
-    if constexpr (TY == T_IQ3_S && NT >= GEMV_THREADS_LARGE) __builtin_amdgcn_s_barrier();
-    {
+    // (measured on MI355X: IQ3_S 4096x8192 7.4 -> 7.0 us; the IQ2_S instances
+    // measured slower with it).  1024-thread IQ3_S instances, whose one step
+    // per wave requests the whole matrix at once, issue it after the prologue
+    // barrier instead: the prologue then ends at about 2.5 us instead of 4 us,
+    // and the decode overlaps the rest of the stream (IQ3_S 4096x13312 10.7 ->
+    // 10.2 us; the IQ2_S instance gains nothing from it).
+    constexpr bool LATE = TY == T_IQ3_S && NT == GEMV_THREADS_XL;
+    if constexpr (TY == T_IQ3_S && NT == GEMV_THREADS_LARGE) __builtin_amdgcn_s_barrier();
+    if constexpr (!LATE) {
         int r = it * L.rpw + (L.lane_on ? L.slot : L.rpw - 1);
         r = r < rows ? r : rows - 1;
         load_slice(P, (uint32_t)(r * NB + L.b), po, L.part, w[0]);
@@ -157,6 +162,11 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
 #ifdef LBH_WAVE_TIMELINE
     tl[2] = tl_now();
 #endif
+    if constexpr (LATE) {
+        int r = it * L.rpw + (L.lane_on ? L.slot : L.rpw - 1);
+        r = r < rows ? r : rows - 1;
+        load_slice(P, (uint32_t)(r * NB + L.b), po, L.part, w[0]);
+    }
 #pragma unroll
     for (int d = 1; d < D; ++d) issue(it + d * nw, w[d]);
     if (status_set(p.status)) return;
@@ -287,8 +297,6 @@ static hipError_t launch_typed(const GemvArgs &a, const GemvTuning &t, int depth
 
 template <int TY>
 static hipError_t launch_lpu(const GemvArgs &a, const GemvTuning &t, int lpu, int depth, hipStream_t s) {
-    // A wave step must hold at least one whole row: NB * LPU <= 64.
-    while (lpu > 1 && a.m.nb * lpu > 64) lpu >>= 1;
     switch (lpu) {
     case 4: return launch_typed<TY, 4>(a, t, depth, s);
     case 2: return launch_typed<TY, 2>(a, t, depth, s);
@@ -312,20 +320,32 @@ static int default_lpu(const GemvArgs &a, int cu_count) {
 
 // Built-in depth: one row step per wave in 1024-thread workgroups (activations
 // read from LDS, four waves per SIMD) for one-lane IQ matvecs with at least 12
-// wave steps per CU, two steps in flight otherwise (measured on MI355X, fused
-// Q8_K: IQ2_S 13312x4096 8.9 -> 8.0 us, IQ3_S 4096x13312 12.3 -> 11.3 us;
-// IQ3_S 4096x8192, 8 steps per CU, 7.7 vs 9.1 us stays at two).
+// wave steps per CU (measured on MI355X, fused Q8_K: IQ2_S 13312x4096 8.9 ->
+// 8.0 us, IQ3_S 4096x13312 12.3 -> 11.3 us; IQ3_S 4096x8192, 8 steps per CU,
+// 7.7 vs 9.1 us stays at two).  Matrices whose row steps fit one wave per SIMD
+// also take one buffer: the second would never be filled, and the smaller
+// register footprint is faster (IQ2_S 1536x4096 4.02 -> 3.96 us, IQ3_S
+// 4096x1536 3.86 -> 3.83 us, Q4_K 4096x4096 4.58 -> 4.48 us; IQ2_S 1024x4096
+// at four lanes per unit stays at two, 3.72 vs 3.75 us).  Two steps in
+// flight otherwise.
 static int default_depth(const GemvArgs &a, int lpu, int cu_count) {
     const bool iq = a.m.type == T_IQ2_S || a.m.type == T_IQ3_S;
     const long long steps = (long long)a.m.rows * a.m.nb / 64;
-    return iq && lpu == 1 && steps >= 12LL * (cu_count > 0 ? cu_count : 256) ? 1 : 2;
+    const long long cus = cu_count > 0 ? cu_count : 256;
+    if (iq && lpu == 1 && steps >= 12LL * cus) return 1;
+    const int rpw = (64 / lpu) / a.m.nb;
+    const long long items = (a.m.rows + rpw - 1) / rpw;
+    return items <= 4 * cus && (lpu <= 2 || !iq) ? 1 : 2;
 }
 
 hipError_t launch_gemv(const GemvArgs &a, const GemvTuning &t, hipStream_t s) {
     const int nb = a.m.nb;
     if (nb < 1 || nb > MAX_NB || a.m.rows < 1) return hipErrorInvalidValue;
     if (!a.q8 && !a.x) return hipErrorInvalidValue;
-    const int lpu = t.lpu > 0 ? t.lpu : default_lpu(a, t.cu_count);
+    int lpu = t.lpu > 0 ? t.lpu : default_lpu(a, t.cu_count);
+    lpu = lpu >= 4 ? 4 : lpu >= 2 ? 2 : 1;
+    // A wave step must hold at least one whole row: NB * LPU <= 64.
+    while (lpu > 1 && nb * lpu > 64) lpu >>= 1;
     const int depth = t.depth > 0 ? t.depth : default_depth(a, lpu, t.cu_count);
     switch (a.m.type) {
     case T_IQ2_S: return launch_lpu<T_IQ2_S>(a, t, lpu, depth, s);
