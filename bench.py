@@ -494,11 +494,22 @@ def bench_batch(args, be, timer, torch, np, synth, state):
         be.route_experts_batch(logits[r], TOP_K, ids[r], coefs[r])
         be.moe_forward_batch(moe, ids[r], coefs[r], xs[r], ys[r])
 
-    g = timer.graph(lambda: [step(r) for r in range(R)])
-    timer.time(g, 2)
     reps = max(2, args.batch_reps)
-    us = timer.time(g, reps) / (reps * R) * 1e6
-    spread = timer.spread(g, 20, R)
+
+    def timed():
+        g = timer.graph(lambda: [step(r) for r in range(R)])
+        timer.time(g, 2)
+        t_us = timer.time(g, reps) / (reps * R) * 1e6
+        sp = timer.spread(g, 20, R)
+        del g
+        return t_us, sp
+
+    # The layer's matrices as uploaded, then with the 16-row tile copies of every
+    # routed expert that the matrix-core streams read (lbh_moe_make_batch_tile_copies).
+    us_plain, _ = timed()
+    moe.make_batch_tile_copies()
+    tile_bytes = moe.batch_tile_copy_bytes
+    us, spread = timed()
     torch.cuda.synchronize()
     ids_h = ids.cpu().numpy().view(np.uint32)
     hits = [len(np.unique(ids_h[r])) for r in range(R)]
@@ -509,13 +520,19 @@ def bench_batch(args, be, timer, torch, np, synth, state):
                        "per-expert gate/up + SwiGLU + down, ordered combine",
            "tokens_per_step": T, "steps_timed": reps * R, "us_per_step": round(us, 2), "per_replay_spread": spread,
            "tokens_per_s": round(T / us * 1e6, 1),
+           "us_per_step_without_tile_copies": round(us_plain, 2),
+           "tile_copy_hbm_bytes": int(tile_bytes),
            "distinct_experts_hit_per_step": hits,
            "algorithmic_bytes_per_step": int(bytes_step),
            "GB/s": round(bytes_step / us / 1e3, 1), "roofline_frac": round(bytes_step / us / 1e3 / HBM_PEAK_GBS, 4),
            "note": "the 33.5 MB shared expert is read once per step (K-quant GEMM on the f16 matrix cores); routed "
                    "experts once per chunk of up to 16 tokens, chunks of 4+ tokens on the f16 matrix cores (exact "
-                   "integer block sums), smaller ones on the VALU integer dots"}
+                   "integer block sums), smaller ones on the VALU integer dots; us_per_step is timed with a second "
+                   "copy of every routed expert's matrices with the 16 rows of each block adjacent (read by the "
+                   "matrix-core streams only; tile_copy_hbm_bytes of HBM), us_per_step_without_tile_copies on the "
+                   "matrices as uploaded"}
     check = dict(ids=ids_h[0].copy(), coefs=coefs[0].cpu().numpy(), xs=xs[0].cpu().numpy(), ys=ys[0].cpu().numpy())
+    moe.make_batch_tile_copies([])
     return res, check
 
 

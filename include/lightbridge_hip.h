@@ -403,6 +403,31 @@ lbh_status lbh_moe_set_batch_tiles(lbh_moe *moe, int32_t tokens_per_chunk, int32
 lbh_status lbh_moe_set_batch_engine(lbh_moe *moe, int32_t mx_min_tokens, int32_t mx_rows_gate_up,
                                     int32_t mx_rows_down);
 
+/* [sync] Tile copies for the batched matrix-core streams (no counterpart in the
+ * reference, whose batch is a loop over tokens).  Those streams read a 16-row x
+ * one-block tile per step; in the matrix layout the 16 rows of a block lie a row
+ * apart, so each step reads 16 pieces of 16 cache lines whose other pieces come
+ * back in later steps.  This call gives the IQ2_S / IQ3_S gate, up and down
+ * matrices (rows a multiple of 16) of the listed routed experts a second copy,
+ * owned by the layer, with the 16 rows of every block adjacent.  The
+ * matrix-core streams then read those copies; every other kernel keeps reading
+ * the caller's matrices.  The results are the same bits.  The cost is a second
+ * copy of those bytes in HBM (lbh_moe_batch_tile_copy_bytes).
+ *   experts = NULL: every routed expert.  n_experts = 0 with a list: drop the
+ *   copies.  Each call replaces the previous copies.  It waits for the device's
+ *   work in flight before releasing them.
+ * The copies are taken at this call: call it again after an expert's bytes
+ * change.  Until lbh_moe_set_batch_engine is called, the layer's engine follows
+ * the copies.  With copies, chunks of 3+ tokens run on the matrix cores, one wave
+ * per 16-row tile.  Without, chunks of 4+ tokens run on the split tiles.  Each
+ * measured fastest in its case.  Layers over an expert cache have no static
+ * expert table and return LBH_INVALID_PARAMETER. */
+lbh_status lbh_moe_make_batch_tile_copies(lbh_ctx *ctx, lbh_moe *moe, const uint32_t *experts, size_t n_experts,
+                                          lbh_error *err);
+
+/* HBM bytes of the layer's tile copies (0 when none). */
+size_t lbh_moe_batch_tile_copy_bytes(const lbh_moe *moe);
+
 /* [async] Batched form of lbh_moe_forward: ids_dev / coefs_dev are device arrays
  * [n_tokens][top_k] (each token's ids ascending and distinct), x_dev [n_tokens][hidden],
  * y_dev [n_tokens][hidden].  Unchecked; a routing with an id >= n_experts or a token

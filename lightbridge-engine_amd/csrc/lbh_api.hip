@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <new>
 
@@ -70,7 +71,7 @@ MatView view_of(const lbh_matrix *m) {
     v.type = m->type;
     v.nb = (int32_t)m->nb;
     v.rows = (int32_t)m->rows;
-    v.pad = 0;
+    v.order = MAT_ROW_MAJOR;
     v.units = (long long)(m->rows * m->nb);
     v.bytes = (long long)m->bytes;
     return v;
@@ -865,6 +866,13 @@ struct lbh_moe {
     float *d_shared;
     float *dq;                // DequantF32 checked forward: one expert's gate and up values
     int two_stream;           // 1: the async forwards use side1, 0: one stream (default, measured faster)
+    // 16-row tile copies of routed IQ matrices for the batched matrix-core
+    // streams (lbh_moe_make_batch_tile_copies): one allocation, and the
+    // streams' expert table (tile views where copied, else the row-major ones).
+    uint8_t *tile_mem;
+    size_t tile_bytes;
+    ExpertDev *experts_mx_dev;
+    int engine_set;           // lbh_moe_set_batch_engine was called: the copies leave the engine alone
 };
 
 namespace {
@@ -879,6 +887,18 @@ void set_batch_defaults(lbh_moe *m, int mx_min) {
     m->tc = mx_min > 0 ? 16 : 8;
     m->rt_gu_r = 64, m->rt_gu_s = 64, m->rt_d_r = 160, m->rt_d_s = 64;
 }
+// With the tile copies (lbh_moe_make_batch_tile_copies) a step's 16 rows of a
+// block are two whole lines, so one wave per 16-row tile and chunks from three
+// tokens on the matrix cores measured fastest (configs[3]: 378-380 us against
+// 386 us with the split tiles and 4-token chunks, which stay the defaults
+// without copies: 430 us there against 467 us).
+constexpr int MX_MIN_TILED = 3;
+void set_engine_for_copies(lbh_moe *m, bool copies) {
+    if (m->engine_set) return;
+    m->mx_min = copies ? MX_MIN_TILED : MX_MIN_DEFAULT;
+    m->mx_split_gu = copies ? 1 : 4;
+    m->mx_split_d = copies ? 1 : 2;
+}
 
 void free_moe(lbh_moe *m) {
     if (!m) return;
@@ -887,6 +907,8 @@ void free_moe(lbh_moe *m) {
     delete[] m->experts_host;
     if (m->batch_mem) (void)hipFree(m->batch_mem);
     if (m->shared_gemm_mem) (void)hipFree(m->shared_gemm_mem);
+    if (m->tile_mem) (void)hipFree(m->tile_mem);
+    if (m->experts_mx_dev) (void)hipFree(m->experts_mx_dev);
     if (m->plan_host) (void)hipHostFree(m->plan_host);
     for (int i = 0; i < 4; ++i)
         if (m->ev[i]) (void)hipEventDestroy(m->ev[i]);
@@ -1527,6 +1549,7 @@ BatchArgs batch_args(const lbh_moe *m, const uint32_t *ids, const float *coefs, 
                      const float *x, float *y) {
     BatchArgs a = m->batch;
     a.experts = m->experts_dev;
+    a.experts_mx = m->experts_mx_dev ? m->experts_mx_dev : m->experts_dev;
     a.shared = m->shared;
     a.has_shared = m->has_shared;
     a.hidden = (int32_t)m->hidden;
@@ -1728,8 +1751,76 @@ lbh_status lbh_moe_set_batch_engine(lbh_moe *m, int32_t mx_min_tokens, int32_t m
             *m = saved;
             return LBH_UNSUPPORTED_SHAPE;
         }
+    m->engine_set = 1;
     return LBH_OK;
 }
+
+lbh_status lbh_moe_make_batch_tile_copies(lbh_ctx *ctx, lbh_moe *m, const uint32_t *experts, size_t n_experts,
+                                          lbh_error *err) {
+    if (!ctx || !m || (!experts && n_experts > 0)) return fail(err, LBH_NULL_ARGUMENT);
+    if (m->n_experts == 0 || !m->experts_host) return fail(err, LBH_INVALID_PARAMETER);   // cache-backed layer
+    if (ctx->device != m->device) return fail(err, LBH_INVALID_PARAMETER);
+    for (size_t i = 0; i < n_experts; ++i)
+        if (experts[i] >= m->n_experts) return fail(err, LBH_INVALID_PARAMETER, 0, i, m->n_experts, experts[i]);
+    // experts == NULL: every routed expert; an empty list drops the copies.
+    std::unique_ptr<char[]> pick(new (std::nothrow) char[m->n_experts]());
+    if (!pick) return fail(err, LBH_HIP_ERROR);
+    for (size_t e = 0; e < m->n_experts; ++e) pick[e] = experts ? 0 : 1;
+    for (size_t i = 0; i < n_experts; ++i) pick[experts[i]] = 1;
+    // The matrix-core streams' matrices: IQ2_S / IQ3_S, whole 16-row tiles.
+    auto copyable = [](const MatView &v) { return (v.type == LBH_IQ2_S || v.type == LBH_IQ3_S) && v.rows % 16 == 0; };
+    auto align = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    size_t total = 0;
+    for (size_t e = 0; e < m->n_experts; ++e) {
+        if (!pick[e]) continue;
+        const ExpertDev &x = m->experts_host[e];
+        for (const MatView *v : {&x.gate, &x.up, &x.down})
+            if (copyable(*v)) total += align((size_t)v->bytes);
+    }
+    DeviceGuard g(ctx->device);
+    uint8_t *mem = nullptr;
+    ExpertDev *table = nullptr;
+    std::unique_ptr<ExpertDev[]> host(new (std::nothrow) ExpertDev[m->n_experts]);
+    if (!host) return fail(err, LBH_HIP_ERROR);
+    if (total > 0) {
+        hipError_t e = hipMalloc(&mem, total);
+        if (e == hipSuccess) e = hipMalloc(&table, m->n_experts * sizeof(ExpertDev));
+        size_t off = 0;
+        for (size_t x = 0; x < m->n_experts && e == hipSuccess; ++x) {
+            host[x] = m->experts_host[x];
+            if (!pick[x]) continue;
+            for (MatView *v : {&host[x].gate, &host[x].up, &host[x].down}) {
+                if (!copyable(*v) || e != hipSuccess) continue;
+                e = launch_units_to_tiles(*v, mem + off, ctx->stream);
+                v->planes = mem + off;
+                v->order = MAT_TILE16;
+                off += align((size_t)v->bytes);
+            }
+        }
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(table, host.get(), m->n_experts * sizeof(ExpertDev), hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipStreamSynchronize(ctx->stream);
+            if (mem) (void)hipFree(mem);
+            if (table) (void)hipFree(table);
+            return hip_fail(err, e);
+        }
+    }
+    // Batched calls still in flight on any stream may read the old copies.
+    if (m->tile_mem || m->experts_mx_dev) {
+        HIP_TRY(hipDeviceSynchronize());
+        if (m->tile_mem) (void)hipFree(m->tile_mem);
+        if (m->experts_mx_dev) (void)hipFree(m->experts_mx_dev);
+    }
+    m->tile_mem = mem;
+    m->tile_bytes = total;
+    m->experts_mx_dev = table;
+    set_engine_for_copies(m, table != nullptr);
+    return ok(err);
+}
+
+size_t lbh_moe_batch_tile_copy_bytes(const lbh_moe *m) { return m ? m->tile_bytes : 0; }
 
 static lbh_status forward_batch(lbh_ctx *ctx, lbh_moe *m, const uint32_t *ids, const float *coefs, size_t n_tokens,
                                 size_t top_k, const float *x, float *y, int residual) {

@@ -888,10 +888,12 @@ __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1
     const int steps = rt0 < r1 && j < nb ? (nb - j + S - 1) / S : 0;
     Planes P[NM];
     uint32_t po[NM];
+    int32_t order[NM];   // wave-uniform: a tile copy (MAT_TILE16) or the row-major matrix
 #pragma unroll
     for (int t = 0; t < NM; ++t) {
         P[t] = make_planes(mv[t].planes, mv[t].units, mv[t].bytes);
         po[t] = part_offset<TY, 4>(P[t], q);
+        order[t] = __builtin_amdgcn_readfirstlane(mv[t].order);
     }
     // Rows past r1 load the last row (every register defined; never output).
     int r = rt0 + c;
@@ -903,7 +905,7 @@ __device__ __forceinline__ void mx_tiles(const MatView (&mv)[NM], int r0, int r1
         int b = j + S * (s < steps ? s : steps - 1);
         b = b < 0 ? 0 : b < nb ? b : nb - 1;
 #pragma unroll
-        for (int t = 0; t < NM; ++t) load_slice(P[t], (uint32_t)(r * nb + b), po[t], q, st.w[t]);
+        for (int t = 0; t < NM; ++t) load_slice(P[t], unit_index(order[t], r, b, nb), po[t], q, st.w[t]);
         const uint4 *src = reinterpret_cast<const uint4 *>(bq + b * 256 + 64 * q);
 #pragma unroll
         for (int k = 0; k < 4; ++k) st.bq[k] = src[k];
@@ -1012,7 +1014,7 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_gate_up(BatchArgs a) {
     } else {
         if (ci >= a.plan[0]) return;
         p0 = a.chunk_p0[ci], n = a.chunk_n[ci];
-        const ExpertDev &E = a.experts[a.chunk_expert[ci]];
+        const ExpertDev &E = a.experts_mx[a.chunk_expert[ci]];
         mv[0] = E.gate, mv[1] = E.up;
     }
     if (n < a.mx_min) return;
@@ -1055,7 +1057,7 @@ __global__ void __launch_bounds__(MX_THREADS) k_mx_down(BatchArgs a) {
     } else {
         if (ci >= a.plan[0]) return;
         p0 = a.chunk_p0[ci], n = a.chunk_n[ci];
-        mv[0] = a.experts[a.chunk_expert[ci]].down;
+        mv[0] = a.experts_mx[a.chunk_expert[ci]].down;
     }
     if (n < a.mx_min) return;
     const int c = (int)(threadIdx.x & 15) < n ? (int)(threadIdx.x & 15) : n - 1;

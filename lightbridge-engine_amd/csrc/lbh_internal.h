@@ -17,13 +17,24 @@ struct DevStatus {
     unsigned long long pad;
 };
 
+enum : int32_t { MAT_ROW_MAJOR = 0, MAT_TILE16 = 1 };
+
+// Unit of (row r, block b) of a matrix with nb blocks per row stored in unit
+// order `order` (MAT_TILE16 needs rows % 16 == 0).
+__host__ __device__ inline uint32_t unit_index(int32_t order, uint32_t r, uint32_t b, uint32_t nb) {
+    return order == MAT_TILE16 ? (((r >> 4) * nb + b) << 4) + (r & 15u) : r * nb + b;
+}
+
 // A matrix in the device layout (lbh_layout.h).
 struct MatView {
     const uint8_t *planes;
     int32_t type;
     int32_t nb;        // 256-element blocks per row
     int32_t rows;
-    int32_t pad;
+    // Unit order of the planes: MAT_ROW_MAJOR (u = r * nb + b) everywhere
+    // except the batched matrix-core streams' tile copies, MAT_TILE16
+    // (u = ((r / 16) * nb + b) * 16 + r % 16: the 16 rows of a block adjacent).
+    int32_t order;
     long long units;   // rows * nb
     long long bytes;   // size of the planes allocation
 };
@@ -213,6 +224,10 @@ struct BatchArgs {
     // and stage vc = min(tc, mx_min - 1) tokens (tc when mx = 0).
     int32_t mx, mx_min, mx_split_gu, mx_split_d, vc;
     int32_t residual;           // y[t][r] += delta (as MoeArgs::residual)
+    // The matrix-core streams' routed views [n_experts]: an expert's 16-row
+    // tile copies where lbh_moe_make_batch_tile_copies made them, else its
+    // views in `experts`.
+    const ExpertDev *experts_mx;
     uint8_t *xq_mx, *hq_mx_r, *hq_mx_s;
     float *xd_mx, *hd_mx_r, *hd_mx_s;
 };
@@ -281,6 +296,9 @@ hipError_t launch_repack(int ty, const uint8_t *ggml, uint8_t *planes, long long
                          hipStream_t s);
 hipError_t launch_repack_range(int ty, const uint8_t *src, uint8_t *dst, long long U, long long u0, long long n,
                                hipStream_t s);
+// Copy of an IQ2_S / IQ3_S matrix (rows % 16 == 0) with its units in
+// MAT_TILE16 order at dst (m.bytes bytes).
+hipError_t launch_units_to_tiles(const MatView &m, uint8_t *dst, hipStream_t s);
 hipError_t launch_validate_scales(int ty, const uint8_t *ggml, long long units,
                                   unsigned long long *first, hipStream_t s);
 hipError_t launch_f16_to_f32(const uint16_t *in, float *out, long long n, hipStream_t s);

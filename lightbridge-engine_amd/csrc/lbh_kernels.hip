@@ -191,6 +191,31 @@ __global__ void k_repack_range(const uint8_t *__restrict__ src, uint8_t *__restr
         unit_to_device<TY>(src + i * BB, dst, U, u0 + i);
 }
 
+// The same device-layout bytes with the units in 16-row tile order
+// (unit_index MAT_TILE16): one thread per destination unit, every plane's
+// piece of the unit copied whole.  rows % 16 == 0.
+template <int TY>
+__global__ void k_units_to_tiles(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, long long rows, int nb) {
+    constexpr TypeLayout L = layout_of(TY);
+    const long long U = rows * nb;
+    for (long long ut = (long long)blockIdx.x * blockDim.x + threadIdx.x; ut < U; ut += (long long)gridDim.x * blockDim.x) {
+        const long long tile = ut / (16LL * nb), rem = ut - tile * 16LL * nb;
+        const long long b = rem >> 4, r = tile * 16 + (rem & 15);
+        const long long u = r * nb + b;
+#pragma unroll
+        for (int c = 0; c < L.nchunk; ++c)
+            reinterpret_cast<uint4 *>(dst + c * U * 16)[ut] = reinterpret_cast<const uint4 *>(src + c * U * 16)[u];
+        const long long base = L.nchunk * U * 16;
+#pragma unroll
+        for (int t = 0; t < L.tail / 4; ++t)
+            reinterpret_cast<uint32_t *>(dst + base)[ut * (L.tail / 4) + t] =
+                reinterpret_cast<const uint32_t *>(src + base)[u * (L.tail / 4) + t];
+        if constexpr (L.dplane)
+            reinterpret_cast<uint16_t *>(dst + base + L.tail * U)[ut] =
+                reinterpret_cast<const uint16_t *>(src + base + L.tail * U)[u];
+    }
+}
+
 // First non-finite f16 d / dmin in unit order (validate_scales, k_quants.rs:178-208).
 template <int TY>
 __global__ void k_validate_scales(const uint8_t *__restrict__ ggml, long long U, unsigned long long *first) {
@@ -337,6 +362,22 @@ hipError_t launch_repack_range(int ty, const uint8_t *src, uint8_t *dst, long lo
     case T_IQ3_S: hipLaunchKernelGGL(k_repack_range<T_IQ3_S>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
     case T_Q4_K: hipLaunchKernelGGL(k_repack_range<T_Q4_K>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
     case T_Q5_K: hipLaunchKernelGGL(k_repack_range<T_Q5_K>, dim3(grid), dim3(256), 0, s, src, dst, U, u0, n); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_units_to_tiles(const MatView &m, uint8_t *dst, hipStream_t s) {
+    if (m.rows % 16 != 0) return hipErrorInvalidValue;
+    int grid = cdiv(m.units, 256);
+    grid = grid > 8192 ? 8192 : grid;
+    switch (m.type) {
+    case T_IQ2_S:
+        hipLaunchKernelGGL(k_units_to_tiles<T_IQ2_S>, dim3(grid), dim3(256), 0, s, m.planes, dst, (long long)m.rows, m.nb);
+        break;
+    case T_IQ3_S:
+        hipLaunchKernelGGL(k_units_to_tiles<T_IQ3_S>, dim3(grid), dim3(256), 0, s, m.planes, dst, (long long)m.rows, m.nb);
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -67,7 +67,7 @@ __device__ __forceinline__ MatView uniform_view(const MatView &v) {
     u.type = __builtin_amdgcn_readfirstlane(v.type);
     u.nb = __builtin_amdgcn_readfirstlane(v.nb);
     u.rows = __builtin_amdgcn_readfirstlane(v.rows);
-    u.pad = 0;
+    u.order = MAT_ROW_MAJOR;
     u.units = (long long)uniform_u64((uint64_t)v.units);
     u.bytes = (long long)uniform_u64((uint64_t)v.bytes);
     return u;

@@ -134,6 +134,8 @@ def lib() -> C.CDLL:
             "lbh_gemm_q8_k_noalloc": ([p, p, p, sz, p, E], i32),
             "lbh_moe_set_batch_tiles": ([p, i32, i32, i32, i32, i32], i32),
             "lbh_moe_set_batch_engine": ([p, i32, i32, i32], i32),
+            "lbh_moe_make_batch_tile_copies": ([p, p, p, sz, E], i32),
+            "lbh_moe_batch_tile_copy_bytes": ([p], sz),
             "lbh_moe_forward_batch": ([p, p, p, p, sz, sz, p, p], i32),
             "lbh_moe_routed_by_id_batch_into": ([p, p, p, p, sz, sz, p, sz, p, sz, E], i32),
             "lbh_route_experts_batch": ([p, p, sz, sz, sz, i32, C.c_float, p, p, p], i32),
@@ -533,6 +535,21 @@ class MoeLayer:
         st = lib().lbh_moe_set_batch_engine(self.handle, mx_min_tokens, mx_rows_gate_up, mx_rows_down)
         if st:
             raise KernelError(LbhError(status=st))
+
+    def make_batch_tile_copies(self, experts=None) -> None:
+        """16-row tile copies of the routed IQ matrices of `experts` (None: all; an
+        empty list drops them) for the batched matrix-core streams."""
+        if experts is None:
+            _call(lib().lbh_moe_make_batch_tile_copies, self.be.ctx, self.handle, None, 0)
+            return
+        ids = np.ascontiguousarray(experts, dtype=np.uint32)
+        buf = ids if ids.size else np.zeros(1, np.uint32)   # a list, possibly empty: never NULL
+        _call(lib().lbh_moe_make_batch_tile_copies, self.be.ctx, self.handle, C.c_void_p(buf.ctypes.data), ids.size)
+
+    @property
+    def batch_tile_copy_bytes(self) -> int:
+        """HBM bytes of the tile copies (0 when none)."""
+        return int(lib().lbh_moe_batch_tile_copy_bytes(self.handle))
 
     def set_streams(self, two_streams: bool) -> None:
         """Shared expert on a second stream beside the routed experts, or (default) all on one."""
