@@ -58,7 +58,7 @@ COLD_COPIES = 8
 # Bytes per launch (read from beyond L2 + written) measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain
 # copy of known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2368682 + 6144, "down": 3022281 + 19648, "prefill": 193271527 + 25638800}
+MEASURED_TRAFFIC = {"gate": 2363582 + 6144, "down": 2987416 + 19648, "prefill": 193314577 + 25350416}
 
 
 def parse():
@@ -849,6 +849,12 @@ def pmc_workloads():
     logits = torch.from_numpy(synth.zipf_routes(64, NE, 8, 1.1, seed=500)).cuda()
     ids = torch.zeros((64, 8), dtype=torch.int32, device='cuda'); coefs = torch.zeros((64, 8), device='cuda')
     xb = torch.randn(64, H, device='cuda'); yb = torch.zeros(64, H, device='cuda')
+    for _ in range(2):
+        be.route_experts_batch(logits, 8, ids, coefs)
+        be.moe_forward_batch(moe, ids, coefs, xb, yb)
+    torch.cuda.synchronize()
+    # the same batch over the 16-row tile copies (the bench's configs[3] setting)
+    moe.make_batch_tile_copies()
     for _ in range(2):
         be.route_experts_batch(logits, 8, ids, coefs)
         be.moe_forward_batch(moe, ids, coefs, xb, yb)
