@@ -415,7 +415,9 @@ lbh_status lbh_moe_set_batch_engine(lbh_moe *moe, int32_t mx_min_tokens, int32_t
  * copy of those bytes in HBM (lbh_moe_batch_tile_copy_bytes).
  *   experts = NULL: every routed expert.  n_experts = 0 with a list: drop the
  *   copies.  Each call replaces the previous copies.  It waits for the device's
- *   work in flight before releasing them.
+ *   work in flight before releasing them.  Graphs that captured batched calls
+ *   before it hold the released copies' addresses: capture them again. The
+ *   same holds after lbh_moe_reserve_batch.
  * The copies are taken at this call: call it again after an expert's bytes
  * change.  Until lbh_moe_set_batch_engine is called, the layer's engine follows
  * the copies.  With copies, chunks of 3+ tokens run on the matrix cores, one wave
