@@ -197,9 +197,10 @@ __global__ void __launch_bounds__(NT) k_gemv(GemvArgs p) {
 #endif
         const int r = it * L.rpw + L.slot;
         const bool on = L.lane_on && r < rows;
-        // One wave per SIMD: the codebook reads are gathered (the latency of a
-        // single wave's LDS round trips is the dot's critical path).
-        constexpr int GB = D == 1 ? 0 : TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
+        // One wave per SIMD (every instance but the 1024-thread ones): the
+        // codebook reads are gathered (the latency of a single wave's LDS round
+        // trips is the dot's critical path).
+        constexpr int GB = NT == GEMV_THREADS_XL ? 0 : TY == T_IQ2_S ? 4 : TY == T_IQ3_S ? 2 : 0;
         const float v =
             row_dot<TY, LPU, GB, Traits<TY>::KQ ? 16 : 8, A, GR>(w, act, on, L, s_grid, s_fold[wid],
                                                                  p.block_sums, (long long)r * NB + L.b);
