@@ -148,3 +148,32 @@ def test_tile_copies_refused_on_a_cached_layer(be):
     finally:
         layer.close()
         cache.close()
+
+
+def test_tile_copies_async_device_routed_and_residual(be, oracle, small):
+    """The asynchronous batched forward over the copies with device-selected
+    routes (lbh_route_experts_batch), and its residual form (hidden += the
+    block's output, residual_add_in_place, crates/bridge-kernels-reference/
+    src/norm.rs:83-98) against the oracle."""
+    logits, ids_w, coefs_w = zipf_routing(oracle, 30, 12, 4, seed=71)
+    xs = np.random.default_rng(72).standard_normal((30, 512)).astype(np.float32)
+    want = oracle_batch(oracle, small, ids_w, coefs_w, xs)
+    hidden0 = (np.random.default_rng(73).standard_normal((30, 512)) * 2).astype(np.float32)
+    small.moe.make_batch_tile_copies()
+    try:
+        ids = torch.zeros((30, 4), dtype=torch.int32, device="cuda")
+        coefs = torch.zeros((30, 4), dtype=torch.float32, device="cuda")
+        be.route_experts_batch(dev(logits), 4, ids, coefs)
+        y = dev(np.zeros((30, 512), np.float32))
+        be.moe_forward_batch(small.moe, ids, coefs, dev(xs), y)
+        got = host(y)
+        assert all(_same(got[t], want[t]) for t in range(30))
+        h = dev(hidden0)
+        be.moe_forward_batch_residual(small.moe, ids, coefs, dev(xs), h)
+        got_h = host(h)
+        for t in range(30):
+            w = hidden0[t].copy()
+            oracle.residual_add_in_place(w, want[t])
+            assert _same(got_h[t], w), f"token {t}"
+    finally:
+        small.moe.make_batch_tile_copies([])
