@@ -108,9 +108,11 @@ def test_tile_copies_reject_bad_expert_ids(small):
     assert e.value.variant == "InvalidParameter" and e.value.index == 1
 
 
-def test_tile_copies_with_an_iq_shared_expert(be, oracle):
-    """The shared expert's matrix-core streams keep reading its own matrices."""
-    layer = Layer(be, oracle, 6, 1024, 512, 256, (IQ2_S, IQ3_S, IQ2_S, IQ3_S), seed=161)
+@pytest.mark.parametrize("types", [(IQ2_S, IQ3_S, IQ2_S, IQ3_S), (IQ2_S, IQ2_S, IQ2_S, IQ2_S)])
+def test_tile_copies_with_an_iq_shared_expert(be, oracle, types):
+    """The shared expert's matrix-core streams keep reading its own matrices;
+    routed downs of either IQ type read their copies."""
+    layer = Layer(be, oracle, 6, 1024, 512, 256, types, seed=161)
     layer.moe.reserve_batch(32, 3)
     ids, coefs, xs, want = batch_case(oracle, layer, 24, 6, 3, seed=51)
     layer.moe.make_batch_tile_copies()
