@@ -311,7 +311,11 @@ __host__ __device__ constexpr int rows_per_step(int lpu, int nb) { return (64 / 
 // wave's first weight loads are issued before `prologue` (codebook fill and
 // activation staging, ended by a workgroup barrier), so their latency
 // overlaps it; then a software pipeline keeps the next step's loads in flight.
-template <int TY, int LPU, int NM, class Prologue, class Out>
+// FUSED (chunks of one token): each row is the matvec's row dot (lbh_rows.h
+// row_dot, the same terms and block-order fold as batch_step) on the staged
+// token, with no decoded copy of the slice held for reuse, which a single
+// token never needs; the wave's fold table holds its FoldLDS.
+template <int TY, int LPU, int NM, bool FUSED = false, class Prologue, class Out>
 __device__ __forceinline__ void batch_rows(const MatView (&mv)[NM], int r0, int r1, const uint8_t *s_act, int n,
                                            const void *grid, float *fold_lds, Prologue prologue, Out out) {
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -340,9 +344,18 @@ __device__ __forceinline__ void batch_rows(const MatView (&mv)[NM], int r0, int 
 #pragma unroll
         for (int m = 0; m < NM; ++m) load_slice(P[m], (uint32_t)(r * nb + L.b), po[m], L.part, w[m]);
     };
+    ActOf<TY, LPU> act1;   // FUSED: the staged token
     auto process = [&](int j, const W (&w)[NM]) {
         const int r = r0 + j * rpw + L.slot;
         const bool on = L.lane_on && r < r1;
+        if constexpr (FUSED) {
+            FoldLDS<TY> &fl = *reinterpret_cast<FoldLDS<TY> *>(terms);
+            float res[NM];
+#pragma unroll
+            for (int m = 0; m < NM; ++m) res[m] = row_dot<TY, LPU>(w[m], act1, on, L, grid, fl, nullptr, 0);
+            if (on && L.leader()) out(0, r, res);
+            return;
+        }
         DecOf<TY, LPU> dec[NM];
 #pragma unroll
         for (int m = 0; m < NM; ++m) decode(w[m], grid, L.part, dec[m]);
@@ -356,6 +369,7 @@ __device__ __forceinline__ void batch_rows(const MatView (&mv)[NM], int r0, int 
     W wa[NM], wb[NM];
     issue(j, wa);
     prologue();
+    if constexpr (FUSED) load_act_lds(s_act + L.b * Q8L, L.part, act1);
     while (j < steps) {
         issue(j + MB_WAVES, wb);
         process(j, wa);
@@ -544,7 +558,10 @@ __host__ __device__ inline int valu_cap(const BatchArgs &a, int ty) {
 // Gate/up, SwiGLU (activation.rs:170-178) -> h, one launch per stream:
 // SHARED: workgroup (token chunk, row tile) of the shared expert; else
 // workgroup (routed chunk, row tile), idle past the sort's chunk count.
-template <int TY, bool SHARED>
+// PART (routed IQ streams beside the matrix cores): 0 every VALU chunk, 1
+// the chunks of one token (the FUSED rows of batch_rows: 116 instead of 170
+// VGPRs, four waves per SIMD instead of two), 2 the other VALU chunks.
+template <int TY, bool SHARED, int PART = 0>
 __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     if (a.plan[1]) return;
@@ -580,9 +597,10 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_gate_up(BatchArgs a) {
         if (c >= a.plan[0]) return;
         const int e = a.chunk_expert[c], p0 = a.chunk_p0[c], n = a.chunk_n[c];
         if (mx_takes<TY>(a, n)) return;
+        if ((PART == 1 && n != 1) || (PART == 2 && n == 1)) return;
         const int r0 = tile * a.rt_gu_r, r1 = r0 + a.rt_gu_r < a.ffn_r ? r0 + a.rt_gu_r : a.ffn_r;
         const MatView mv[2] = {a.experts[e].gate, a.experts[e].up};
-        batch_rows<TY, LPU, 2>(
+        batch_rows<TY, LPU, 2, PART == 1>(
             mv, r0, r1, s_act, n, grid, fold,
             [&]() {
                 fill_grid<TY>(grid);
@@ -1164,9 +1182,25 @@ static hipError_t allow_lds(K kernel, int lds) {
 template <int TY, bool SHARED>
 static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
     lds -= al16(GridLDS<TY>::BYTES);
+    const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.ffn_s, a.rt_gu_s) : a.max_chunks * cdiv(a.ffn_r, a.rt_gu_r);
+    // Routed IQ chunks left to the VALU beside the matrix cores: one-token
+    // chunks in their own launch, then the rest (measured on MI355X at the
+    // configs[3] shapes: 378.7 -> 369.8 us per step; the same split of the
+    // downs, or the fused rows for two-token chunks too, measured slower:
+    // 382 and 405 us).
+    if constexpr (!SHARED && (TY == T_IQ2_S || TY == T_IQ3_S)) {
+        if (a.mx) {
+            hipError_t e = allow_lds(k_mb_gate_up<TY, SHARED, 1>, lds);
+            if (e == hipSuccess) e = allow_lds(k_mb_gate_up<TY, SHARED, 2>, lds);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((k_mb_gate_up<TY, SHARED, 1>), dim3(grid), dim3(MB_THREADS), lds, s, a);
+            if ((e = hipGetLastError()) != hipSuccess) return e;
+            hipLaunchKernelGGL((k_mb_gate_up<TY, SHARED, 2>), dim3(grid), dim3(MB_THREADS), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     hipError_t e = allow_lds(k_mb_gate_up<TY, SHARED>, lds);
     if (e != hipSuccess) return e;
-    const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.ffn_s, a.rt_gu_s) : a.max_chunks * cdiv(a.ffn_r, a.rt_gu_r);
     hipLaunchKernelGGL((k_mb_gate_up<TY, SHARED>), dim3(grid), dim3(MB_THREADS), lds, s, a);
     return hipGetLastError();
 }
