@@ -420,7 +420,7 @@ lbh_status lbh_moe_set_batch_engine(lbh_moe *moe, int32_t mx_min_tokens, int32_t
  *   same holds after lbh_moe_reserve_batch.
  * The copies are taken at this call: call it again after an expert's bytes
  * change.  Until lbh_moe_set_batch_engine is called, the layer's engine follows
- * the copies.  With copies, chunks of 3+ tokens run on the matrix cores, one wave
+ * the copies.  With copies, chunks of 2+ tokens run on the matrix cores, one wave
  * per 16-row tile.  Without, chunks of 4+ tokens run on the split tiles.  Each
  * measured fastest in its case.  Layers over an expert cache have no static
  * expert table and return LBH_INVALID_PARAMETER. */

@@ -888,11 +888,12 @@ void set_batch_defaults(lbh_moe *m, int mx_min) {
     m->rt_gu_r = 64, m->rt_gu_s = 64, m->rt_d_r = 160, m->rt_d_s = 64;
 }
 // With the tile copies (lbh_moe_make_batch_tile_copies) a step's 16 rows of a
-// block are two whole lines, so one wave per 16-row tile and chunks from three
-// tokens on the matrix cores measured fastest (configs[3]: 378-380 us against
-// 386 us with the split tiles and 4-token chunks, which stay the defaults
-// without copies: 430 us there against 467 us).
-constexpr int MX_MIN_TILED = 3;
+// block are two whole lines, so one wave per 16-row tile and chunks from two
+// tokens on the matrix cores measured fastest, the VALU keeping the one-token
+// chunks (configs[3]: 360-362 us; 369-371 from three tokens, 379 from four;
+// without copies the split tiles and 4-token chunks stay the defaults: 430 us
+// there against 477-555 us for these settings).
+constexpr int MX_MIN_TILED = 2;
 void set_engine_for_copies(lbh_moe *m, bool copies) {
     if (m->engine_set) return;
     m->mx_min = copies ? MX_MIN_TILED : MX_MIN_DEFAULT;

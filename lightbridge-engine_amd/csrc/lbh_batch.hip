@@ -1194,7 +1194,7 @@ static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
             if (e == hipSuccess) e = allow_lds(k_mb_gate_up<TY, SHARED, 2>, lds);
             if (e != hipSuccess) return e;
             hipLaunchKernelGGL((k_mb_gate_up<TY, SHARED, 1>), dim3(grid), dim3(MB_THREADS), lds, s, a);
-            if ((e = hipGetLastError()) != hipSuccess) return e;
+            if ((e = hipGetLastError()) != hipSuccess || a.mx_min <= 2) return e;   // no chunk of 2+ left
             hipLaunchKernelGGL((k_mb_gate_up<TY, SHARED, 2>), dim3(grid), dim3(MB_THREADS), lds, s, a);
             return hipGetLastError();
         }
