@@ -656,8 +656,9 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_quant_h(BatchArgs a, int shar
     }
 }
 
-// Down rows -> d, one launch per stream (as k_mb_gate_up).
-template <int TY, bool SHARED>
+// Down rows -> d, one launch per stream (as k_mb_gate_up; PART 1: every
+// chunk has one token, the FUSED rows of batch_rows).
+template <int TY, bool SHARED, int PART = 0>
 __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     if (a.plan[1]) return;
@@ -693,7 +694,7 @@ __global__ void __launch_bounds__(MB_THREADS) k_mb_down(BatchArgs a) {
         uint8_t *grid = static_grid<TY>();
         float *fold = reinterpret_cast<float *>(smem + al16(valu_cap(a, TY) * nb * Q8L));
         const MatView mv[1] = {a.experts[e].down};
-        batch_rows<TY, LPU, 1>(
+        batch_rows<TY, LPU, 1, PART == 1>(
             mv, r0, r1, s_act, n, grid, fold,
             [&]() {
                 fill_grid<TY>(grid);
@@ -1185,9 +1186,8 @@ static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
     const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.ffn_s, a.rt_gu_s) : a.max_chunks * cdiv(a.ffn_r, a.rt_gu_r);
     // Routed IQ chunks left to the VALU beside the matrix cores: one-token
     // chunks in their own launch, then the rest (measured on MI355X at the
-    // configs[3] shapes: 378.7 -> 369.8 us per step; the same split of the
-    // downs, or the fused rows for two-token chunks too, measured slower:
-    // 382 and 405 us).
+    // configs[3] shapes: 378.7 -> 369.8 us per step; the fused rows for
+    // two-token chunks too measured slower, 405 us).
     if constexpr (!SHARED && (TY == T_IQ2_S || TY == T_IQ3_S)) {
         if (a.mx) {
             hipError_t e = allow_lds(k_mb_gate_up<TY, SHARED, 1>, lds);
@@ -1208,9 +1208,22 @@ static hipError_t gate_up_typed(const BatchArgs &a, int lds, hipStream_t s) {
 template <int TY, bool SHARED>
 static hipError_t down_typed(const BatchArgs &a, int lds, hipStream_t s) {
     lds -= al16(GridLDS<TY>::BYTES);
+    const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.hidden, a.rt_d_s) : a.max_chunks * cdiv(a.hidden, a.rt_d_r);
+    // Routed IQ downs beside the matrix cores taking every chunk of 2+ tokens:
+    // the VALU chunks all hold one token and run the fused rows (measured on
+    // MI355X at the configs[3] shapes: 365.5 -> 359-362 us per step; with
+    // 2-token chunks also left to the VALU, a second launch for them made the
+    // split slower, 382 against 370 us).
+    if constexpr (!SHARED && (TY == T_IQ2_S || TY == T_IQ3_S)) {
+        if (a.mx && a.mx_min <= 2) {
+            const hipError_t e = allow_lds(k_mb_down<TY, SHARED, 1>, lds);
+            if (e != hipSuccess) return e;
+            hipLaunchKernelGGL((k_mb_down<TY, SHARED, 1>), dim3(grid), dim3(MB_THREADS), lds, s, a);
+            return hipGetLastError();
+        }
+    }
     hipError_t e = allow_lds(k_mb_down<TY, SHARED>, lds);
     if (e != hipSuccess) return e;
-    const int grid = SHARED ? cdiv(a.n_tokens, a.tc) * cdiv(a.hidden, a.rt_d_s) : a.max_chunks * cdiv(a.hidden, a.rt_d_r);
     hipLaunchKernelGGL((k_mb_down<TY, SHARED>), dim3(grid), dim3(MB_THREADS), lds, s, a);
     return hipGetLastError();
 }
