@@ -58,7 +58,7 @@ COLD_COPIES = 8
 # Bytes per launch (read from beyond L2 + written) measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE over `bench.py --pmc-workloads`, each scaled by the same counter's reading for a plain
 # copy of known size (profiles/pmc_hot_kernels_traffic_and_valu.md).
-MEASURED_TRAFFIC = {"gate": 2363582 + 6144, "down": 2987416 + 19648, "prefill": 193314577 + 25350416}
+MEASURED_TRAFFIC = {"gate": 2363569 + 6144, "down": 2987388 + 19648, "prefill": 193234918 + 25644960}
 
 
 def parse():
