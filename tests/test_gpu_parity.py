@@ -240,16 +240,16 @@ def test_upload_shape_errors(be):
                                        (IQ3_S, 1029, 1536), (IQ2_S, 33, 256), (Q5_K, 17, 16384)])
 def test_gemv_every_lanes_per_unit_and_persistent_loop(be, oracle, lpu, ty, rows, k):
     """Every launch shape gives the same bits: lanes per unit 1/2/4, one or two
-    row steps in flight per wave (one lane per unit at depth 1: 1024-thread
-    workgroups reading the activations from LDS), and a workgroup cap of 3 so
-    each wave walks many rows of the persistent loop."""
+    row steps in flight per wave: the shape's default and every forced depth 1-4
+    (one lane per unit at depth 1: 1024-thread workgroups reading the
+    activations from LDS), and a workgroup cap of 3 so each wave walks many
+    rows of the persistent loop."""
     try:
-        for depth in (0, 1):
-            for cap in (0, 3):
-                be.set_tuning(be.TUNE_GEMV_LPU, lpu)
-                be.set_tuning(be.TUNE_GEMV_DEPTH, depth)
-                be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
-                _check_gemv(be, oracle, ty, rows, k, seed=rows + lpu + cap)
+        for depth, cap in ((0, 0), (0, 3), (1, 0), (1, 3), (2, 3), (3, 3), (4, 0)):
+            be.set_tuning(be.TUNE_GEMV_LPU, lpu)
+            be.set_tuning(be.TUNE_GEMV_DEPTH, depth)
+            be.set_tuning(be.TUNE_GEMV_MAX_BLOCKS, cap)
+            _check_gemv(be, oracle, ty, rows, k, seed=rows + lpu + cap + depth)
     finally:
         be.set_tuning(be.TUNE_GEMV_LPU, 0)
         be.set_tuning(be.TUNE_GEMV_DEPTH, 0)
@@ -302,7 +302,7 @@ def test_fused_quantize_gemv_every_launch_shape(be, oracle, ty, rows, k):
     m = be.upload(ty, rows, k, w)
     xd = dev(x)
     try:
-        for lpu, depth in ((0, 0), (1, 0), (2, 0), (4, 0), (1, 1), (1, 2)):
+        for lpu, depth in ((0, 0), (1, 0), (2, 0), (4, 0), (1, 1), (1, 2), (2, 3), (4, 4)):
             for cap in (0, 3):
                 be.set_tuning(be.TUNE_GEMV_LPU, lpu)
                 be.set_tuning(be.TUNE_GEMV_DEPTH, depth)
